@@ -1,0 +1,214 @@
+"""FWLoss forward+backward throughput on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2] [--no-cpu-baseline]
+
+A step is one fused forward+backward (``fw_forward_backward``: H, losses, mean, kappa and the dense
+gradient) over one batch of synthetic logits resident in HBM.  The default workload is the headline
+configuration N=65536, C=1000 fp32 (logits N(0,1), labels uniform).  Input/output buffer sets are
+rotated between steps so the 256 MB Infinity Cache cannot hold a step's data from the previous use.
+
+Prints one JSON line.  ``roofline.achieved`` = algorithmic bytes per launch (read logits once,
+write the gradient once, read labels, write H/loss/kappa: 8*N*C + 20*N bytes) / the kernel's mean
+duration measured with HIP events on the stream the kernel runs on.  ``roofline.traffic`` is the
+HBM bytes per launch measured with rocprofv3 counters (profiles/traffic_*.json), or null.
+``cpu_baseline`` times the reference's own CPU path (compiled into oracle/_ref) on this host's cores,
+on the same host-generated inputs, as loss + full gradient per call (benchmarks/cpu_benchmarks/
+bench_cpu_e2e.py:13-15); without oracle/_ref the C restatement is timed instead.
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "fast-familywise-loss_amd")
+ORACLE = os.path.join(ROOT, "oracle")
+for _p in (PKG, ORACLE):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "rows/sec and achieved HBM GB/s (% of peak), fwd+bwd, N=65536 C=1000 fp32"
+HBM_PEAK_GBS = 8000.0
+
+
+def alg_bytes(N, C):
+    # logits read once + gradient written once + int64 labels + H, loss (f32) and kappa (i32)
+    return 8 * N * C + 8 * N + 12 * N
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--sets", type=int, default=3, help="rotated input/output buffer sets")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="time a plain 1 GiB device copy instead (calibrates rocprof byte counters)")
+    return ap.parse_args()
+
+
+def traffic_for(kernel_tag, cfg):
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel_tag}_{cfg}.json")
+    if not os.path.isfile(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    return d.get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(z_np, y_np, seconds):
+    """Time the reference CPU path (oracle/_ref) or the C restatement on the same inputs."""
+    import numpy as np
+    import torch
+    import oracle
+    N, C = z_np.shape
+    threads = torch.get_num_threads()
+    ref = oracle.load_ref()
+    if ref is not None:
+        Z = torch.from_numpy(z_np)
+        Y = torch.from_numpy(y_np)
+
+        def call():
+            Zg = Z.detach().requires_grad_(True)
+            loss = ref.familywise_loss(Zg, Y, 0)          # reduction "sum" (fwcpp.py:17)
+            loss.backward()
+            return Zg.grad
+        kind, label = "reference", f"oracle/_ref {oracle.ref_variant()} (src/cpu/fw_cpu.cpp)"
+    else:
+        def call():
+            return oracle.single_pass(z_np, y_np, scale=1.0, nthreads=threads)
+        kind, label = "port", "oracle/fwl_oracle.c fwo_single_pass"
+    call()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": N / med, "unit": "rows/s", "cores": threads, "kind": kind,
+            "sample": f"{label}: full {N}x{C} batch, loss + dense gradient per call, median of {len(times)} "
+                      f"calls ({sum(times):.1f} s of CPU work), {threads} threads",
+            "ms_per_call": med * 1e3, "gbps": alg_bytes(N, C) / med / 1e9}
+
+
+def copy_probe(args):
+    import torch
+    n = 1 << 28  # 1 GiB of fp32
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    print(json.dumps({"probe": "copy", "bytes_per_launch_read": 4 * n, "bytes_per_launch_write": 4 * n,
+                      "ms": dt * 1e3, "gbps": 8 * n / dt / 1e9}), flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the row-sharded multi-GPU design is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import fwloss
+    import fwloss_data
+
+    if args.copy_probe:
+        copy_probe(args)
+        return
+
+    dev = torch.device("cuda:0")
+    z_np, y_np = fwloss_data.make(args.config, seed=0)
+    N, C = z_np.shape
+    sets = []
+    for s in range(args.sets):
+        zt = torch.from_numpy(z_np).to(dev) if s == 0 else sets[0][0].roll(s, dims=0).contiguous()
+        yt = torch.from_numpy(y_np).to(dev) if s == 0 else sets[0][1].roll(s, dims=0).contiguous()
+        sets.append((zt, yt))
+    torch.cuda.synchronize()
+
+    def step(i):
+        zt, yt = sets[i % len(sets)]
+        return fwloss.fw_forward_backward(zt, yt)
+
+    for i in range(args.warmup):
+        out = step(i)
+    del out
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    keep = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        o = step(i)
+        ev[i][1].record(stream)
+        keep.append(o[1])  # hold the losses so the allocator cannot reuse them within the region
+        del o
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    ms_per_step = wall * 1e3 / args.steps
+    nbytes = alg_bytes(N, C)
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+
+    # the reference's two-op sequence (fw_forward_small + fw_backward_small), for comparison
+    def two_op(i):
+        zt, yt = sets[i % len(sets)]
+        H, losses, mean, kappa, sel = fwloss.fw_forward_small(zt, yt)
+        return fwloss.fw_backward_small(yt, sel, kappa)
+    for i in range(5):
+        two_op(i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for i in range(args.steps):
+        two_op(i)
+    torch.cuda.synchronize()
+    two_op_ms = (time.perf_counter() - t1) * 1e3 / args.steps
+
+    tag = "fwl_wave_rows" if C <= 1024 else "fwl_block_rows"
+    traffic = traffic_for(tag, args.config)
+    result = {
+        "metric": METRIC,
+        "value": N * args.steps / wall,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config} fused FW loss forward+backward, N={N} C={C} fp32 logits N(0,1) "
+                               "(fwloss_data.make), labels uniform int64, buffers rotated over "
+                               f"{args.sets} sets", "N": N, "C": C, "op": "fw_forward_backward",
+                   "parallelism": "single GPU"},
+        "gbps": nbytes / (ms_per_step * 1e-3) / 1e9,
+        "hbm_frac": nbytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "kernel_ms": kern_ms,
+        "two_op_ms_per_step": two_op_ms,
+        "roofline": {"bound": "hbm", "kernel": tag, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "alg_bytes": nbytes},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(z_np, y_np, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,230 @@
+// fw_radix_cuda -- PyTorch extension with the op names, signatures and outputs of the reference
+// extension (src/cuda/binding.cpp:3-13, setup.py:5-8), implemented over the C ABI of libfwloss
+// (include/fwloss.h).  This file holds no device code: it checks arguments, allocates outputs with
+// the torch allocator, passes the current HIP stream and turns a non-zero status into a
+// RuntimeError.
+//
+// Differences from the reference host code (src/cuda/fw_radix_argmax.cu:1381-1609), all additive:
+//   * targets, kappas, masks and candidate tensors are validated (the reference checks only the
+//     logits of the forwards, :1383-1386, :1419-1421);
+//   * non-contiguous inputs are made contiguous instead of being read with the wrong strides;
+//   * launches go on the current stream instead of the legacy default stream;
+//   * any K is accepted by every op (the reference's small kernel has no bound check above
+//     K = 10000, :1405-1408).
+#include <torch/extension.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "fwloss.h"
+
+namespace {
+
+hipStream_t current_stream(const at::Tensor& t) {
+  return reinterpret_cast<hipStream_t>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
+}
+
+void check_status(int rc, const char* op) {
+  TORCH_CHECK(rc == FWL_OK, op, ": ", fwl_status_string(rc));
+}
+
+// One zero-initialised workspace per (device, stream).  The kernels leave it zeroed again, and
+// work on one stream is ordered, so calls never share a workspace concurrently.
+at::Tensor workspace(const at::Tensor& like, size_t bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, at::Tensor> cache;
+  const auto key = std::make_pair((int)like.get_device(), current_stream(like));
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it == cache.end() || (size_t)it->second.numel() < bytes) {
+    const size_t grow = bytes < 65536 ? 65536 : bytes;
+    at::Tensor ws = at::zeros({(int64_t)grow}, like.options().dtype(at::kByte));
+    if (it == cache.end()) cache.emplace(key, ws);
+    else it->second = ws;
+    return ws;
+  }
+  return it->second;
+}
+
+void check_logits(const at::Tensor& logits) {
+  // messages as in src/cuda/fw_radix_argmax.cu:1383-1386
+  TORCH_CHECK(logits.is_cuda(), "logits must be a CUDA tensor");
+  TORCH_CHECK(logits.dim() == 2, "logits must have shape [N, K]");
+  TORCH_CHECK(logits.scalar_type() == torch::kFloat32, "logits must be float32");
+  TORCH_CHECK(logits.size(1) >= 1, "logits must have K >= 1 classes");
+}
+
+void check_rows(const at::Tensor& t, const at::Tensor& logits, at::ScalarType dt, const char* name) {
+  TORCH_CHECK(t.device() == logits.device(), name, " must be on the same device as logits");
+  TORCH_CHECK(t.dim() == 1 && t.size(0) == logits.size(0), name, " must have shape [N]");
+  TORCH_CHECK(t.scalar_type() == dt, name, " must be ", c10::toString(dt));
+}
+
+void check_matrix(const at::Tensor& t, const at::Tensor& logits, at::ScalarType dt, const char* name) {
+  TORCH_CHECK(t.device() == logits.device(), name, " must be on the same device as logits");
+  TORCH_CHECK(t.dim() == 2 && t.size(0) == logits.size(0) && t.size(1) == logits.size(1), name,
+              " must have the shape of logits [N, K]");
+  TORCH_CHECK(t.scalar_type() == dt, name, " must be ", c10::toString(dt));
+}
+
+struct Common {
+  at::Tensor logits, targets, H, losses, mean, kappa, ws;
+};
+
+Common prepare(const at::Tensor& logits_in, const at::Tensor& targets_in) {
+  check_logits(logits_in);
+  check_rows(targets_in, logits_in, torch::kInt64, "targets");
+  Common c;
+  c.logits = logits_in.contiguous();
+  c.targets = targets_in.contiguous();
+  const int64_t N = c.logits.size(0), K = c.logits.size(1);
+  c.H = torch::empty({N}, c.logits.options());
+  c.losses = torch::empty({N}, c.logits.options());
+  c.mean = torch::empty({}, c.logits.options());
+  c.kappa = torch::empty({N}, c.logits.options().dtype(torch::kInt32));
+  c.ws = workspace(c.logits, fwl_workspace_bytes(N, K));
+  return c;
+}
+
+// fw_forward_small(logits, targets) -> [H, losses, mean_loss, kappa, selected_logits]
+// (src/cuda/fw_radix_argmax.cu:1381-1414)
+std::vector<at::Tensor> fw_forward_small(at::Tensor logits, at::Tensor targets) {
+  c10::DeviceGuard guard(logits.device());
+  Common c = prepare(logits, targets);
+  const int64_t N = c.logits.size(0), K = c.logits.size(1);
+  at::Tensor selected = torch::empty({N, K}, c.logits.options().dtype(torch::kBool));
+  const int rc = fwl_forward_small(
+      c.logits.data_ptr<float>(), c.targets.data_ptr<int64_t>(), N, K, c.H.data_ptr<float>(),
+      c.losses.data_ptr<float>(), c.mean.data_ptr<float>(), c.kappa.data_ptr<int32_t>(),
+      reinterpret_cast<uint8_t*>(selected.data_ptr<bool>()), c.ws.data_ptr(), (size_t)c.ws.numel(),
+      current_stream(c.logits));
+  check_status(rc, "fw_forward_small");
+  return {c.H, c.losses, c.mean, c.kappa, selected};
+}
+
+// fw_backward_small(targets, selected_logits, kappas) -> grad   (:1591-1609)
+at::Tensor fw_backward_small(at::Tensor targets, at::Tensor selected_logits, at::Tensor kappas) {
+  TORCH_CHECK(selected_logits.is_cuda(), "selected_logits must be a CUDA tensor");
+  TORCH_CHECK(selected_logits.dim() == 2, "selected_logits must have shape [N, K]");
+  TORCH_CHECK(selected_logits.scalar_type() == torch::kBool, "selected_logits must be bool");
+  c10::DeviceGuard guard(selected_logits.device());
+  check_rows(targets, selected_logits, torch::kInt64, "targets");
+  check_rows(kappas, selected_logits, torch::kInt32, "kappas");
+  at::Tensor sel = selected_logits.contiguous(), tg = targets.contiguous(), kp = kappas.contiguous();
+  const int64_t N = sel.size(0), K = sel.size(1);
+  at::Tensor grad = torch::empty({N, K}, sel.options().dtype(torch::kFloat32));
+  const int rc = fwl_backward_small(tg.data_ptr<int64_t>(), reinterpret_cast<const uint8_t*>(sel.data_ptr<bool>()),
+                                    kp.data_ptr<int32_t>(), N, K, grad.data_ptr<float>(), current_stream(sel));
+  check_status(rc, "fw_backward_small");
+  return grad;
+}
+
+// fw_forward(logits, targets) -> [H, losses, mean_loss, kappa, candidate_buffer,
+//                                 candidate_indices, candidate_counts]   (:1417-1496)
+std::vector<at::Tensor> fw_forward(at::Tensor logits, at::Tensor targets) {
+  c10::DeviceGuard guard(logits.device());
+  Common c = prepare(logits, targets);
+  const int64_t N = c.logits.size(0), K = c.logits.size(1);
+  at::Tensor cbuf = torch::empty({N, K}, c.logits.options());
+  at::Tensor cidx = torch::empty({N, K}, c.logits.options().dtype(torch::kInt32));
+  at::Tensor ccnt = torch::empty({N}, c.logits.options().dtype(torch::kInt32));
+  const int rc = fwl_forward_large(
+      c.logits.data_ptr<float>(), c.targets.data_ptr<int64_t>(), N, K, c.H.data_ptr<float>(),
+      c.losses.data_ptr<float>(), c.mean.data_ptr<float>(), c.kappa.data_ptr<int32_t>(),
+      cbuf.data_ptr<float>(), cidx.data_ptr<int32_t>(), ccnt.data_ptr<int32_t>(), c.ws.data_ptr(),
+      (size_t)c.ws.numel(), current_stream(c.logits));
+  check_status(rc, "fw_forward");
+  return {c.H, c.losses, c.mean, c.kappa, cbuf, cidx, ccnt};
+}
+
+// fw_backward(logits, targets, H, kappas, candidate_buffer, candidate_indices, candidate_counts)
+// -> grad   (:1536-1559)
+at::Tensor fw_backward(at::Tensor logits, at::Tensor targets, at::Tensor H, at::Tensor kappas,
+                       at::Tensor candidate_buffer, at::Tensor candidate_indices,
+                       at::Tensor candidate_counts) {
+  check_logits(logits);
+  c10::DeviceGuard guard(logits.device());
+  check_rows(targets, logits, torch::kInt64, "targets");
+  check_rows(H, logits, torch::kFloat32, "H");
+  check_rows(kappas, logits, torch::kInt32, "kappas");
+  check_matrix(candidate_buffer, logits, torch::kFloat32, "candidate_buffer");
+  check_matrix(candidate_indices, logits, torch::kInt32, "candidate_indices");
+  check_rows(candidate_counts, logits, torch::kInt32, "candidate_counts");
+  at::Tensor z = logits.contiguous(), tg = targets.contiguous(), h = H.contiguous(), kp = kappas.contiguous(),
+             cb = candidate_buffer.contiguous(), ci = candidate_indices.contiguous(),
+             cc = candidate_counts.contiguous();
+  const int64_t N = z.size(0), K = z.size(1);
+  at::Tensor grad = torch::empty({N, K}, z.options());
+  const int rc = fwl_backward_large(z.data_ptr<float>(), tg.data_ptr<int64_t>(), h.data_ptr<float>(),
+                                    kp.data_ptr<int32_t>(), cb.data_ptr<float>(), ci.data_ptr<int32_t>(),
+                                    cc.data_ptr<int32_t>(), N, K, grad.data_ptr<float>(), current_stream(z));
+  check_status(rc, "fw_backward");
+  return grad;
+}
+
+// fw_forward_backward(logits, targets, scale=1/N, reduce_div=N) -> [H, losses, reduced, kappa, grad]
+// The fused hot path: one launch, logits read once, dense gradient written once.
+std::vector<at::Tensor> fw_forward_backward(at::Tensor logits, at::Tensor targets, double scale,
+                                            double reduce_div) {
+  c10::DeviceGuard guard(logits.device());
+  Common c = prepare(logits, targets);
+  const int64_t N = c.logits.size(0), K = c.logits.size(1);
+  if (scale < 0) scale = N > 0 ? 1.0 / (double)N : 1.0;
+  if (reduce_div < 0) reduce_div = (double)N;
+  at::Tensor grad = torch::empty({N, K}, c.logits.options());
+  const int rc = fwl_forward_backward(
+      c.logits.data_ptr<float>(), c.targets.data_ptr<int64_t>(), N, K, scale, reduce_div,
+      c.H.data_ptr<float>(), c.losses.data_ptr<float>(), c.mean.data_ptr<float>(),
+      c.kappa.data_ptr<int32_t>(), grad.data_ptr<float>(), c.ws.data_ptr(), (size_t)c.ws.numel(),
+      current_stream(c.logits));
+  check_status(rc, "fw_forward_backward");
+  return {c.H, c.losses, c.mean, c.kappa, grad};
+}
+
+// grad *= grad_output (a 0-dim factor, or one factor per row), in place; rows whose factor is 1
+// are skipped on the device (src/cpu/fw_cpu.cpp:734-740)
+at::Tensor fw_scale_grad(at::Tensor grad, at::Tensor grad_output) {
+  TORCH_CHECK(grad.is_cuda() && grad.dim() == 2 && grad.scalar_type() == torch::kFloat32 && grad.is_contiguous(),
+              "grad must be a contiguous float32 CUDA tensor [N, K]");
+  c10::DeviceGuard guard(grad.device());
+  TORCH_CHECK(grad_output.device() == grad.device(), "grad_output must be on the device of grad");
+  at::Tensor go = grad_output.to(torch::kFloat32).contiguous();
+  int64_t stride = 0;
+  if (go.numel() == 1) stride = 0;
+  else {
+    TORCH_CHECK(go.dim() == 1 && go.size(0) == grad.size(0), "grad_output must be a scalar or have shape [N]");
+    stride = 1;
+  }
+  const int rc = fwl_scale_grad(grad.data_ptr<float>(), go.data_ptr<float>(), stride, grad.size(0), grad.size(1),
+                                current_stream(grad));
+  check_status(rc, "fw_scale_grad");
+  return grad;
+}
+
+void set_params(int64_t path, int64_t cand_cap) {
+  check_status(fwl_set_params((int)path, (int)cand_cap), "set_params");
+}
+
+std::pair<int64_t, int64_t> get_params() {
+  int p = 0, c = 0;
+  fwl_get_params(&p, &c);
+  return {p, c};
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("fw_forward", &fw_forward, "FW loss forward with candidate lists (MI355X)");
+  m.def("fw_backward", &fw_backward, "FW loss backward from candidate lists (MI355X)");
+  m.def("fw_forward_small", &fw_forward_small, "FW loss forward with the support mask (MI355X)");
+  m.def("fw_backward_small", &fw_backward_small, "FW loss backward from the support mask (MI355X)");
+  m.def("fw_forward_backward", &fw_forward_backward, "Fused FW loss forward + backward (MI355X)",
+        py::arg("logits"), py::arg("targets"), py::arg("scale") = -1.0, py::arg("reduce_div") = -1.0);
+  m.def("fw_scale_grad", &fw_scale_grad, "In-place grad *= grad_output (device-side skip when 1)");
+  m.def("set_params", &set_params, "Dispatch switches: path (0 auto, 1 wave, 2 block, 3 generic), cand_cap",
+        py::arg("path"), py::arg("cand_cap") = 512);
+  m.def("get_params", &get_params);
+}

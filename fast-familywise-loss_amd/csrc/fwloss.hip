@@ -1,0 +1,1342 @@
+// libfwloss.so -- Familywise (FW) loss forward/backward for MI355X (gfx950), behind the C ABI of
+// include/fwloss.h.
+//
+// Per row z (C fp32 logits) the threshold tau = max_k (S_k - 1)/k (reference_impl.py:11-35) is
+// the root of sum_j max(z_j - tau, 0) = 1 (src/cpu/fw_cpu.cpp:1-4).  Two facts drive the design:
+//   * tau >= max(z) - 1, so the support {z > tau} lies in (max - 1, max]: only a few entries per
+//     row ("candidates") matter, the rest of the row is read once and written once;
+//   * H(A) = (sum_A z - 1)/|A| <= tau for every non-empty subset A of the row, so any such value is
+//     a lower bound that may be used to discard entries early (fw_cpu.cpp:201-211).
+//
+// Kernels
+//   fwl_wave_rows   C <= 1024: one wavefront per row, the row held in VGPRs (128-bit loads),
+//                   candidates z > max-1 compacted into LDS with ballot/mbcnt, then sorted across
+//                   the wavefront (bitonic network over DPP / ds_swizzle), prefix-summed in fp64
+//                   (DPP row_shr + row_bcast scan) and tau = max_k (S_k - 1)/k.  Rows with more
+//                   than 64 candidates use fixed-point (Michelot) iterations on the register row.
+//                   The epilogue writes H, loss, kappa and the gradient / mask / candidate list.
+//   fwl_block_rows  C > 1024: one block (4 wavefronts) per row.  Each wavefront streams its share
+//                   of the row once with a running lower bound t = (its max so far) - 1, keeps
+//                   the entries z > t in an LDS list (value, index) and writes the output of every
+//                   other entry immediately (they are <= t <= tau).  A full list is tightened by
+//                   fixed-point iterations on the list; a list that cannot be tightened sends the
+//                   row to the generic multi-pass path.
+//   fwl_mask_to_grad, fwl_cand_to_grad   the two-op backward of the drop-in interface.
+// The mean loss is reduced in fp64 in a fixed order: per-block partial sums, then the last block
+// to finish (ticket counter in the caller's workspace) sums the partials and resets the counter.
+//
+// Compile with -Xclang -target-feature -Xclang -packed-fp32-ops (see fwloss_build.py).
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "fwloss.h"
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlock = kWave * kWavesPerBlock;
+constexpr int kMaxWaveC = 1024;        // longest row held in registers by one wavefront
+constexpr int kCapMax = 512;           // LDS candidate slots per wavefront in fwl_block_rows
+constexpr int kMaxBlocksWave = 2048;   // grid cap of fwl_wave_rows (4 rows in flight per block)
+constexpr int kMaxBlocksRow = 4096;    // grid cap of fwl_block_rows
+constexpr int kStreamUnroll = 4;       // 128-bit loads in flight per lane per streaming round
+constexpr size_t kWsHeader = 256;      // ticket counter, then fp64 partial sums
+
+enum Mode : int { kGrad = 0, kMask = 1, kCand = 2 };
+
+struct Outs {
+  float* H;
+  float* loss;
+  int32_t* kappa;
+  float* mean;
+  float* grad;
+  uint8_t* mask;
+  float* cval;
+  int32_t* cidx;
+  int32_t* ccnt;
+  double scale;        // gradient scale (1/N for the mean reduction)
+  double reduce_div;   // mean = sum(losses) / reduce_div
+  float scale_f;
+  unsigned* ticket;
+  double* partials;
+  int force_generic;
+  int cap;             // LDS candidate capacity per wavefront (<= kCapMax)
+};
+
+// ------------------------------------------------------------------------------------------------
+// wavefront primitives (all lanes of the wavefront must be active when these are called)
+
+__device__ __forceinline__ int lane_id() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+// number of set bits of b in lanes below this one
+__device__ __forceinline__ int rank_in(uint64_t b) {
+  return __builtin_amdgcn_mbcnt_hi((unsigned)(b >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)b, 0u));
+}
+
+// DPP controls (GFX9 encoding)
+constexpr int kQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kRowRor8 = 0x128;       // row_ror:8  (lane ^ 8 inside a row of 16)
+constexpr int kRowMirror = 0x140;     // lane 15 - i inside a row of 16
+constexpr int kRowHalfMirror = 0x141; // lane 7 - i inside a half row of 8
+constexpr int kRowBcast15 = 0x142;    // lane 15 of each row to the next row
+constexpr int kRowBcast31 = 0x143;    // lane 31 to rows 2 and 3
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int x) {
+  return __builtin_amdgcn_mov_dpp(x, CTRL, 0xF, 0xF, false);
+}
+
+// lanes whose DPP source is out of range (or whose row is masked off) read 0
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_or0(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, ROW_MASK, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_f64(double v) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = dpp_mov<CTRL>((int)b);
+  const int hi = dpp_mov<CTRL>((int)(b >> 32));
+  return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_or0_f64(double v) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = dpp_or0<CTRL, ROW_MASK>((int)b);
+  const int hi = dpp_or0<CTRL, ROW_MASK>((int)(b >> 32));
+  return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)b, l);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+  return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+// partner value of lane ^ M
+template <int M>
+__device__ __forceinline__ float xor_lane(float v) {
+  const int x = __float_as_int(v);
+  if constexpr (M == 1) return __int_as_float(dpp_mov<kQuadXor1>(x));
+  else if constexpr (M == 2) return __int_as_float(dpp_mov<kQuadXor2>(x));
+  else if constexpr (M == 8) return __int_as_float(dpp_mov<kRowRor8>(x));
+  else if constexpr (M == 4 || M == 16) return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x1F | (M << 10)));
+  else {
+    static_assert(M == 32, "xor distance");
+    return __int_as_float(__builtin_amdgcn_ds_bpermute((lane_id() ^ 32) << 2, x));
+  }
+}
+
+// maximum over the wavefront, returned in every lane (wavefront-uniform)
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, __int_as_float(dpp_mov<kQuadXor1>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<kQuadXor2>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<kRowHalfMirror>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<kRowMirror>(__float_as_int(v))));
+  const int x = __float_as_int(v);
+  const float a = __int_as_float(__builtin_amdgcn_readlane(x, 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(x, 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(x, 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(x, 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// fp64 sum over the wavefront in a fixed order, returned in every lane
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v += dpp_mov_f64<kQuadXor1>(v);
+  v += dpp_mov_f64<kQuadXor2>(v);
+  v += dpp_mov_f64<kRowHalfMirror>(v);
+  v += dpp_mov_f64<kRowMirror>(v);
+  return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+}
+
+__device__ __forceinline__ double wave_max_f64(double v) {
+  v = fmax(v, dpp_mov_f64<kQuadXor1>(v));
+  v = fmax(v, dpp_mov_f64<kQuadXor2>(v));
+  v = fmax(v, dpp_mov_f64<kRowHalfMirror>(v));
+  v = fmax(v, dpp_mov_f64<kRowMirror>(v));
+  return fmax(fmax(readlane_f64(v, 0), readlane_f64(v, 16)), fmax(readlane_f64(v, 32), readlane_f64(v, 48)));
+}
+
+// inclusive prefix sum over the 64 lanes (row_shr within rows of 16, then row_bcast across rows)
+__device__ __forceinline__ double wave_scan_f64(double v) {
+  v += dpp_or0_f64<0x111, 0xF>(v);          // row_shr:1
+  v += dpp_or0_f64<0x112, 0xF>(v);          // row_shr:2
+  v += dpp_or0_f64<0x114, 0xF>(v);          // row_shr:4
+  v += dpp_or0_f64<0x118, 0xF>(v);          // row_shr:8
+  v += dpp_or0_f64<kRowBcast15, 0xA>(v);    // rows 1, 3 += last lane of rows 0, 2
+  v += dpp_or0_f64<kRowBcast31, 0xC>(v);    // rows 2, 3 += lane 31
+  return v;
+}
+
+// one compare-exchange step of a bitonic network sorting the wavefront in descending order
+template <int K, int J>
+__device__ __forceinline__ float bitonic_step(float v, int lane) {
+  const float p = xor_lane<J>(v);
+  const bool keep_max = ((lane & J) == 0) == ((lane & K) == 0);
+  return keep_max ? fmaxf(v, p) : fminf(v, p);
+}
+
+__device__ __forceinline__ float sort_desc64(float v, int lane) {
+  v = bitonic_step<2, 1>(v, lane);
+  v = bitonic_step<4, 2>(v, lane);
+  v = bitonic_step<4, 1>(v, lane);
+  v = bitonic_step<8, 4>(v, lane);
+  v = bitonic_step<8, 2>(v, lane);
+  v = bitonic_step<8, 1>(v, lane);
+  v = bitonic_step<16, 8>(v, lane);
+  v = bitonic_step<16, 4>(v, lane);
+  v = bitonic_step<16, 2>(v, lane);
+  v = bitonic_step<16, 1>(v, lane);
+  v = bitonic_step<32, 16>(v, lane);
+  v = bitonic_step<32, 8>(v, lane);
+  v = bitonic_step<32, 4>(v, lane);
+  v = bitonic_step<32, 2>(v, lane);
+  v = bitonic_step<32, 1>(v, lane);
+  v = bitonic_step<64, 32>(v, lane);
+  v = bitonic_step<64, 16>(v, lane);
+  v = bitonic_step<64, 8>(v, lane);
+  v = bitonic_step<64, 4>(v, lane);
+  v = bitonic_step<64, 2>(v, lane);
+  v = bitonic_step<64, 1>(v, lane);
+  return v;
+}
+
+// largest float <= t (so that x > t <=> x > rd32(t) for every float x; fw_cpu.cpp:96-101)
+__device__ __forceinline__ float rd32(double t) {
+  float r = (float)t;
+  if ((double)r > t) {
+    unsigned b = __float_as_uint(r);
+    if (r > 0.0f) b -= 1u;
+    else if (r < 0.0f) b += 1u;
+    else b = 0x80000001u;
+    r = __uint_as_float(b);
+  }
+  return r;
+}
+
+// next float / double below a finite value
+__device__ __forceinline__ float prev_f32(float r) {
+  unsigned b = __float_as_uint(r);
+  if (r > 0.0f) b -= 1u;
+  else if (r < 0.0f) b += 1u;
+  else b = 0x80000001u;
+  return __uint_as_float(b);
+}
+__device__ __forceinline__ double prev_f64(double r) {
+  uint64_t b = (uint64_t)__double_as_longlong(r);
+  if (r > 0.0) b -= 1u;
+  else if (r < 0.0) b += 1u;
+  else b = 0x8000000000000001ull;
+  return __longlong_as_double((int64_t)b);
+}
+
+// largest float <= m - 1 (tau >= m - 1, so every support entry is > this bound).  For |m| >= 2^53
+// the fp64 subtraction loses the 1; the float below m is then the answer.
+__device__ __forceinline__ float bound_below_max(float m) {
+  const float t = rd32((double)m - 1.0);
+  return (t >= m && isfinite(m)) ? prev_f32(m) : t;
+}
+
+// tau < max always; fp64 rounding can only violate this when the 1 of S - 1 is lost (|z| >= 2^53)
+__device__ __forceinline__ double clamp_below_max(double tau, float m) {
+  return (tau >= (double)m && isfinite(m)) ? prev_f64((double)m) : tau;
+}
+
+// tau of a candidate set held one value per lane in lanes [0, n), 1 <= n <= 64:
+// sort descending, S_k = fp64 prefix sums, tau = max_k (S_k - 1)/k (reference_impl.py:17-21)
+__device__ __forceinline__ double select_small(float c, int n, int lane) {
+  float v = lane < n ? c + 0.0f : -INFINITY;   // + 0.0f: -0.0 -> +0.0 before min/max
+  v = sort_desc64(v, lane);
+  const double S = wave_scan_f64(lane < n ? (double)v : 0.0);
+  const double f = (S - 1.0) / (double)(lane + 1);
+  return wave_max_f64(lane < n ? f : -INFINITY);
+}
+
+// ------------------------------------------------------------------------------------------------
+// mean of the per-row losses: block partial sums, the last block reduces them (fixed order)
+
+__device__ void mean_epilogue(double bsum, const Outs& o) {
+  __shared__ int s_last;
+  __shared__ double s_red[kBlock];
+  if (o.mean == nullptr) return;
+  if (threadIdx.x == 0) {
+    o.partials[blockIdx.x] = bsum;
+    __threadfence();
+    const unsigned t = atomicAdd(o.ticket, 1u);
+    s_last = (t == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  double acc = 0.0;
+  for (unsigned i = threadIdx.x; i < gridDim.x; i += kBlock)
+    acc += __hip_atomic_load(o.partials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  s_red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int s = kBlock / 2; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) s_red[threadIdx.x] += s_red[threadIdx.x + s];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    *o.mean = (float)(s_red[0] / o.reduce_div);
+    __hip_atomic_store(o.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// fwl_wave_rows: one wavefront per row, C <= 64 * E (E elements per lane)
+
+template <int NV, bool V4>
+__device__ __forceinline__ void load_row(const float* __restrict__ z, int64_t r, int C, int lane,
+                                         float* x) {
+  const float* row = z + r * (int64_t)C;
+  if constexpr (V4) {
+    const int nvec = C >> 2;
+    const v4f* row4 = reinterpret_cast<const v4f*>(row);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int q = lane + kWave * k;
+      v4f v = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      if (q < nvec) v = __builtin_nontemporal_load(row4 + q);
+      x[4 * k + 0] = v.x;
+      x[4 * k + 1] = v.y;
+      x[4 * k + 2] = v.z;
+      x[4 * k + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int j = lane + kWave * k;
+      x[k] = j < C ? __builtin_nontemporal_load(row + j) : -INFINITY;
+    }
+  }
+}
+
+// element index of register slot i of this lane
+template <bool V4>
+__device__ __forceinline__ int slot_index(int i, int lane) {
+  if constexpr (V4) return 4 * (lane + kWave * (i >> 2)) + (i & 3);
+  else return lane + kWave * i;
+}
+
+// sum (fp64) and count of the register-row entries > thr, wavefront totals
+template <int E>
+__device__ __forceinline__ void reg_sum_count(const float* x, float thr, double& s, int& c) {
+  double acc = 0.0;
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const bool p = x[i] > thr;
+    acc += p ? (double)x[i] : 0.0;
+    cnt += __popcll(ballot(p));
+  }
+  s = wave_sum_f64(acc);
+  c = cnt;
+}
+
+template <int MODE, int NV, bool V4>
+__device__ __forceinline__ float process_row(const float* __restrict__ z,
+                                             const int64_t* __restrict__ tgt, int64_t r, int C,
+                                             int lane, const float* x, float* cb, const Outs& o) {
+  constexpr int E = V4 ? 4 * NV : NV;
+  const int64_t y64 = tgt[r];
+  const bool yok = y64 >= 0 && y64 < C;
+  const int yr = yok ? (int)y64 : -1;
+
+  // row maximum and the first lower bound max - 1 (rounded down: every support entry passes)
+  float lm = x[0];
+#pragma unroll
+  for (int i = 1; i < E; ++i) lm = fmaxf(lm, x[i]);
+  const float m = wave_max_f32(lm);
+  const float t0 = bound_below_max(m);
+
+  // compact the candidates z > t0 into LDS (first 64 only; n counts all of them)
+  int n = 0;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const bool p = x[i] > t0;
+    const uint64_t b = ballot(p);
+    if (b) {
+      if (p) {
+        const int pos = n + rank_in(b);
+        if (pos < kWave) cb[pos] = x[i];
+      }
+      n += __popcll(b);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  double tau = NAN;
+  int kappa = 0;
+  if (n > 0 && n <= kWave) {
+    const float c = lane < n ? cb[lane] : -INFINITY;
+    tau = clamp_below_max(select_small(c, n, lane), m);
+    kappa = __popcll(ballot(lane < n && c > rd32(tau)));
+  } else if (n > kWave) {
+    // fixed-point iteration t <- H({z > t}) from t = max - 1 (each iterate is <= tau; the set
+    // shrinks every step until it is {z > tau})
+    double t = (double)t0, s;
+    int c;
+    reg_sum_count<E>(x, t0, s, c);
+    for (int it = 0; it <= C + 1; ++it) {
+      const double tn = (s - 1.0) / (double)c;
+      double s2;
+      int c2;
+      reg_sum_count<E>(x, rd32(tn), s2, c2);
+      if (c2 == c || !(tn > t)) {
+        tau = tn;
+        kappa = c2;
+        break;
+      }
+      t = tn;
+      s = s2;
+      c = c2;
+    }
+    const double tc = clamp_below_max(tau, m);
+    if (tc != tau) {
+      double s3;
+      tau = tc;
+      reg_sum_count<E>(x, rd32(tau), s3, kappa);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  const float Hf = rd32(tau);
+  const float inv = (float)(o.scale / (double)kappa);
+  float* const row_out_g = o.grad + r * (int64_t)C;
+  uint8_t* const row_out_m = o.mask + r * (int64_t)C;
+
+  if constexpr (MODE == kGrad || MODE == kMask) {
+    if constexpr (V4) {
+      const int nvec = C >> 2;
+      const int qy = yr >> 2, ky = yr >= 0 ? qy >> 6 : -1, ly = qy & 63, ey = yr & 3;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int q = lane + kWave * k;
+        if (q < nvec) {
+          if constexpr (MODE == kGrad) {
+            v4f g;
+            g.x = x[4 * k + 0] > Hf ? inv : 0.0f;
+            g.y = x[4 * k + 1] > Hf ? inv : 0.0f;
+            g.z = x[4 * k + 2] > Hf ? inv : 0.0f;
+            g.w = x[4 * k + 3] > Hf ? inv : 0.0f;
+            if (k == ky && lane == ly) {
+              if (ey == 0) g.x -= o.scale_f;
+              else if (ey == 1) g.y -= o.scale_f;
+              else if (ey == 2) g.z -= o.scale_f;
+              else g.w -= o.scale_f;
+            }
+            __builtin_nontemporal_store(g, reinterpret_cast<v4f*>(row_out_g) + q);
+          } else {
+            const unsigned mk = (unsigned)(x[4 * k + 0] > Hf) | ((unsigned)(x[4 * k + 1] > Hf) << 8) |
+                                ((unsigned)(x[4 * k + 2] > Hf) << 16) | ((unsigned)(x[4 * k + 3] > Hf) << 24);
+            __builtin_nontemporal_store(mk, reinterpret_cast<unsigned*>(row_out_m) + q);
+          }
+        }
+      }
+    } else {
+      const int ky = yr >= 0 ? yr >> 6 : -1, ly = yr & 63;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int j = lane + kWave * k;
+        if (j < C) {
+          if constexpr (MODE == kGrad) {
+            float g = x[k] > Hf ? inv : 0.0f;
+            if (k == ky && lane == ly) g -= o.scale_f;
+            __builtin_nontemporal_store(g, row_out_g + j);
+          } else {
+            row_out_m[j] = (uint8_t)(x[k] > Hf);
+          }
+        }
+      }
+    }
+  } else {
+    // support list in index order (ballot ranks keep lanes in order within a slot)
+    float* const cv = o.cval + r * (int64_t)C;
+    int32_t* const ci = o.cidx + r * (int64_t)C;
+    int base = 0;
+    if constexpr (V4) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const bool p0 = x[4 * k + 0] > Hf, p1 = x[4 * k + 1] > Hf, p2 = x[4 * k + 2] > Hf,
+                   p3 = x[4 * k + 3] > Hf;
+        const uint64_t b0 = ballot(p0), b1 = ballot(p1), b2 = ballot(p2), b3 = ballot(p3);
+        int pos = base + rank_in(b0) + rank_in(b1) + rank_in(b2) + rank_in(b3);
+        const int j0 = 4 * (lane + kWave * k);
+        if (p0) { cv[pos] = x[4 * k + 0]; ci[pos] = j0 + 0; ++pos; }
+        if (p1) { cv[pos] = x[4 * k + 1]; ci[pos] = j0 + 1; ++pos; }
+        if (p2) { cv[pos] = x[4 * k + 2]; ci[pos] = j0 + 2; ++pos; }
+        if (p3) { cv[pos] = x[4 * k + 3]; ci[pos] = j0 + 3; }
+        base += __popcll(b0) + __popcll(b1) + __popcll(b2) + __popcll(b3);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const bool p = x[k] > Hf;
+        const uint64_t b = ballot(p);
+        if (p) {
+          const int pos = base + rank_in(b);
+          cv[pos] = x[k];
+          ci[pos] = lane + kWave * k;
+        }
+        base += __popcll(b);
+      }
+    }
+  }
+
+  const float zy = yok ? z[r * (int64_t)C + yr] : NAN;
+  const float loss = (float)((1.0 - (double)zy) + tau);
+  if (lane == 0) {
+    if (o.H) o.H[r] = Hf;
+    if (o.loss) o.loss[r] = loss;
+    if (o.kappa) o.kappa[r] = kappa;
+    if constexpr (MODE == kCand) o.ccnt[r] = kappa;
+  }
+  return loss;
+}
+
+template <int MODE, int NV, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_wave_rows(const float* __restrict__ z,
+                                                        const int64_t* __restrict__ tgt, int64_t N,
+                                                        int C, Outs o) {
+  constexpr int E = V4 ? 4 * NV : NV;
+  __shared__ float s_cand[kWavesPerBlock][kWave];
+  __shared__ double s_wsum[kWavesPerBlock];
+  const int lane = lane_id();
+  const int wid = uniform((int)(threadIdx.x >> 6));
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+  double lsum = 0.0;
+  float x[E], nx[E];
+  int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid;
+  if (r < N) load_row<NV, V4>(z, r, C, lane, x);
+  for (; r < N; r += stride) {
+    const int64_t rn = r + stride;
+    if (rn < N) load_row<NV, V4>(z, rn, C, lane, nx);   // next row in flight while this one runs
+    lsum += (double)process_row<MODE, NV, V4>(z, tgt, r, C, lane, x, s_cand[wid], o);
+#pragma unroll
+    for (int i = 0; i < E; ++i) x[i] = nx[i];
+  }
+  if (lane == 0) s_wsum[wid] = lsum;
+  __syncthreads();
+  const double bsum = (s_wsum[0] + s_wsum[1]) + (s_wsum[2] + s_wsum[3]);
+  mean_epilogue(bsum, o);
+}
+
+// ------------------------------------------------------------------------------------------------
+// fwl_block_rows: one block per row, streaming with LDS candidate lists
+
+struct BlockShared {
+  float bval[kWavesPerBlock][kCapMax];
+  int bidx[kWavesPerBlock][kCapMax];
+  float sel[kWave];
+  float wmax[kWavesPerBlock];
+  int wn[kWavesPerBlock];
+  int wsel[kWavesPerBlock];
+  int ovf[kWavesPerBlock];
+  double red_s[kWavesPerBlock];
+  double red_c[kWavesPerBlock];
+  float red_m[kWavesPerBlock];
+  double tau;
+  int kappa;
+};
+
+template <int MODE>
+__device__ __forceinline__ void write_zero(const Outs& o, int64_t r, int C, int j) {
+  if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + j] = 0.0f;
+  else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + j] = 0;
+}
+
+// sum/count over the first n entries of one wavefront's list, entries > thr
+__device__ __forceinline__ void list_sum_count(const float* bv, int n, float thr, int lane, double& s,
+                                               int& c) {
+  double acc = 0.0;
+  int cnt = 0;
+  for (int p0 = 0; p0 < n; p0 += kWave) {
+    const int p = p0 + lane;
+    const float v = p < n ? bv[p] : -INFINITY;
+    const bool k = v > thr;
+    acc += k ? (double)v : 0.0;
+    cnt += __popcll(ballot(k));
+  }
+  s = wave_sum_f64(acc);
+  c = cnt;
+}
+
+// Raise the wavefront's lower bound t with a few fixed-point steps on its list, then drop the
+// entries <= t (their output is written now: they are not in the support).
+template <int MODE>
+__device__ void tighten(float* bv, int* bi, int& n, float& t, const Outs& o, int64_t r, int C,
+                        int yr, int lane) {
+  float tf = t;
+  for (int it = 0; it < 8; ++it) {
+    double s;
+    int c;
+    list_sum_count(bv, n, tf, lane, s, c);
+    if (c == 0) break;
+    // H(A) <= tau for the non-empty set A; one float lower absorbs the fp64 rounding of H(A)
+    float nt = rd32((s - 1.0) / (double)c);
+    if (isfinite(nt)) nt = prev_f32(nt);
+    if (!(nt > tf)) break;
+    tf = nt;
+  }
+  t = fmaxf(t, tf);
+  int w = 0;
+  for (int p0 = 0; p0 < n; p0 += kWave) {
+    const int p = p0 + lane;
+    const float v = p < n ? bv[p] : -INFINITY;
+    const int id = p < n ? bi[p] : -1;
+    const bool keep = v > t;
+    const uint64_t b = ballot(keep);
+    __builtin_amdgcn_wave_barrier();
+    if (keep) {
+      const int pos = w + rank_in(b);
+      bv[pos] = v;
+      bi[pos] = id;
+    } else if (p < n && id != yr) {
+      write_zero<MODE>(o, r, C, id);
+    }
+    w += __popcll(b);
+    __builtin_amdgcn_wave_barrier();
+  }
+  n = w;
+}
+
+// Stream this wavefront's share of row r once.  Returns false if its list overflowed.
+template <int MODE, bool V4>
+__device__ bool stream_row(const float* __restrict__ row, int64_t r, int C, int yr, int lane,
+                           int wid, float* bv, int* bi, const Outs& o, int& n, float& m, float& t) {
+  constexpr int U = kStreamUnroll;
+  const int cap = o.cap;
+  if constexpr (V4) {
+    const int nvec = C >> 2;
+    const v4f* row4 = reinterpret_cast<const v4f*>(row);
+    for (int k0 = 0; k0 * kBlock < nvec; k0 += U) {
+      v4f v[U];
+      int q[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        q[u] = wid * kWave + lane + kBlock * (k0 + u);
+        v[u] = v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        if (q[u] < nvec) v[u] = __builtin_nontemporal_load(row4 + q[u]);
+      }
+      float lm = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u) lm = fmaxf(fmaxf(lm, fmaxf(v[u].x, v[u].y)), fmaxf(v[u].z, v[u].w));
+      m = fmaxf(m, wave_max_f32(lm));
+      t = fmaxf(t, bound_below_max(m));
+      unsigned defer = 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float xv = v[u][e];
+          bool p = xv > t;
+          uint64_t b = ballot(p);
+          if (b) {
+            int cnt = __popcll(b);
+            if (n + cnt > cap) {
+              tighten<MODE>(bv, bi, n, t, o, r, C, yr, lane);
+              p = xv > t;
+              b = ballot(p);
+              cnt = __popcll(b);
+              if (n + cnt > cap) return false;
+            }
+            if (p) {
+              const int pos = n + rank_in(b);
+              bv[pos] = xv;
+              bi[pos] = 4 * q[u] + e;
+            }
+            n += cnt;
+          }
+          defer |= (unsigned)p << (4 * u + e);
+        }
+      }
+      if constexpr (MODE != kCand) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (q[u] < nvec) {
+            const int j0 = 4 * q[u];
+            unsigned dm = (defer >> (4 * u)) & 0xFu;
+            if (yr >= j0 && yr < j0 + 4) dm |= 1u << (yr - j0);
+            if (dm == 0) {
+              if constexpr (MODE == kGrad)
+                __builtin_nontemporal_store(v4f{0.0f, 0.0f, 0.0f, 0.0f},
+                                            reinterpret_cast<v4f*>(o.grad + r * (int64_t)C) + q[u]);
+              else
+                __builtin_nontemporal_store(0u, reinterpret_cast<unsigned*>(o.mask + r * (int64_t)C) + q[u]);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (!((dm >> e) & 1u)) write_zero<MODE>(o, r, C, j0 + e);
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  } else {
+    for (int k0 = 0; k0 * kBlock < C; k0 += U) {
+      float v[U];
+      int jj[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        jj[u] = wid * kWave + lane + kBlock * (k0 + u);
+        v[u] = jj[u] < C ? __builtin_nontemporal_load(row + jj[u]) : -INFINITY;
+      }
+      float lm = v[0];
+#pragma unroll
+      for (int u = 1; u < U; ++u) lm = fmaxf(lm, v[u]);
+      m = fmaxf(m, wave_max_f32(lm));
+      t = fmaxf(t, bound_below_max(m));
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        bool p = v[u] > t;
+        uint64_t b = ballot(p);
+        if (b) {
+          int cnt = __popcll(b);
+          if (n + cnt > cap) {
+            tighten<MODE>(bv, bi, n, t, o, r, C, yr, lane);
+            p = v[u] > t;
+            b = ballot(p);
+            cnt = __popcll(b);
+            if (n + cnt > cap) return false;
+          }
+          if (p) {
+            const int pos = n + rank_in(b);
+            bv[pos] = v[u];
+            bi[pos] = jj[u];
+          }
+          n += cnt;
+        }
+        if constexpr (MODE != kCand)
+          if (jj[u] < C && !p && jj[u] != yr) write_zero<MODE>(o, r, C, jj[u]);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  return true;
+}
+
+// block-wide fp64 sum and count of the row entries > thr (fixed order)
+__device__ void block_sum_count(const float* __restrict__ row, int C, float thr, BlockShared& sh,
+                                int lane, int wid, double& s, int& c) {
+  double acc = 0.0;
+  int cnt = 0;
+  for (int j = threadIdx.x; j < C; j += kBlock) {
+    const float v = row[j];
+    if (v > thr) {
+      acc += (double)v;
+      ++cnt;
+    }
+  }
+  const double ws = wave_sum_f64(acc);
+  const double wc = wave_sum_f64((double)cnt);
+  __syncthreads();
+  if (lane == 0) {
+    sh.red_s[wid] = ws;
+    sh.red_c[wid] = wc;
+  }
+  __syncthreads();
+  s = (sh.red_s[0] + sh.red_s[1]) + (sh.red_s[2] + sh.red_s[3]);
+  c = (int)((sh.red_c[0] + sh.red_c[1]) + (sh.red_c[2] + sh.red_c[3]));
+}
+
+// Generic path: fixed-point iterations over the row in global memory, then every output is
+// (re)written.  Used when a candidate list overflows and when forced by fwl_set_params(3, .).
+template <int MODE>
+__device__ void generic_row(const float* __restrict__ row, int64_t r, int C, int yr, int lane,
+                            int wid, BlockShared& sh, const Outs& o, double& tau, int& kappa) {
+  float lm = -INFINITY;
+  for (int j = threadIdx.x; j < C; j += kBlock) lm = fmaxf(lm, row[j]);
+  const float wm = wave_max_f32(lm);
+  __syncthreads();
+  if (lane == 0) sh.red_m[wid] = wm;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(sh.red_m[0], sh.red_m[1]), fmaxf(sh.red_m[2], sh.red_m[3]));
+  const float t0 = bound_below_max(M);
+  double t = (double)t0, s;
+  int c;
+  block_sum_count(row, C, t0, sh, lane, wid, s, c);
+  tau = NAN;
+  kappa = 0;
+  if (c > 0) {
+    for (int it = 0; it <= C + 1; ++it) {
+      const double tn = (s - 1.0) / (double)c;
+      double s2;
+      int c2;
+      block_sum_count(row, C, rd32(tn), sh, lane, wid, s2, c2);
+      if (c2 == c || !(tn > t)) {
+        tau = tn;
+        kappa = c2;
+        break;
+      }
+      t = tn;
+      s = s2;
+      c = c2;
+    }
+    const double tc = clamp_below_max(tau, M);
+    if (tc != tau) {
+      double s3;
+      tau = tc;
+      block_sum_count(row, C, rd32(tau), sh, lane, wid, s3, kappa);
+    }
+  }
+  // outputs written while streaming must land before these rewrites
+  __threadfence();
+  __syncthreads();
+  const float Hf = rd32(tau);
+  const float inv = (float)(o.scale / (double)kappa);
+  if constexpr (MODE == kGrad) {
+    float* g = o.grad + r * (int64_t)C;
+    for (int j = threadIdx.x; j < C; j += kBlock)
+      if (j != yr) g[j] = row[j] > Hf ? inv : 0.0f;
+  } else if constexpr (MODE == kMask) {
+    uint8_t* mk = o.mask + r * (int64_t)C;
+    for (int j = threadIdx.x; j < C; j += kBlock)
+      if (j != yr) mk[j] = (uint8_t)(row[j] > Hf);
+  } else {
+    float* cv = o.cval + r * (int64_t)C;
+    int32_t* ci = o.cidx + r * (int64_t)C;
+    int base = 0;
+    for (int j0 = 0; j0 < C; j0 += kBlock) {
+      const int j = j0 + (int)threadIdx.x;
+      const float v = j < C ? row[j] : -INFINITY;
+      const bool p = v > Hf;
+      const uint64_t b = ballot(p);
+      __syncthreads();
+      if (lane == 0) sh.wsel[wid] = __popcll(b);
+      __syncthreads();
+      int off = base;
+      for (int w = 0; w < wid; ++w) off += sh.wsel[w];
+      if (p) {
+        const int pos = off + rank_in(b);
+        cv[pos] = v;
+        ci[pos] = j;
+      }
+      base += (sh.wsel[0] + sh.wsel[1]) + (sh.wsel[2] + sh.wsel[3]);
+    }
+  }
+}
+
+template <int MODE, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict__ z,
+                                                         const int64_t* __restrict__ tgt, int64_t N,
+                                                         int C, Outs o) {
+  __shared__ BlockShared sh;
+  const int lane = lane_id();
+  const int wid = uniform((int)(threadIdx.x >> 6));
+  double bsum = 0.0;
+  for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
+    const float* row = z + r * (int64_t)C;
+    const int64_t y64 = tgt[r];
+    const bool yok = y64 >= 0 && y64 < C;
+    const int yr = yok ? (int)y64 : -1;
+    float* bv = sh.bval[wid];
+    int* bi = sh.bidx[wid];
+
+    int n = 0;
+    float m = -INFINITY, t = -INFINITY;
+    bool ok = !o.force_generic;
+    if (ok) ok = stream_row<MODE, V4>(row, r, C, yr, lane, wid, bv, bi, o, n, m, t);
+    if (lane == 0) {
+      sh.wmax[wid] = m;
+      sh.wn[wid] = n;
+      sh.ovf[wid] = !ok;
+    }
+    __syncthreads();
+    const bool overflow = sh.ovf[0] | sh.ovf[1] | sh.ovf[2] | sh.ovf[3];
+
+    double tau = NAN;
+    int kappa = 0;
+    if (!overflow) {
+      const float M = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
+      const float tb = bound_below_max(M);
+      int nb = 0;
+      for (int p0 = 0; p0 < n; p0 += kWave) {
+        const int p = p0 + lane;
+        nb += __popcll(ballot(p < n && bv[p] > tb));
+      }
+      if (lane == 0) sh.wsel[wid] = nb;
+      __syncthreads();
+      const int ntot = (sh.wsel[0] + sh.wsel[1]) + (sh.wsel[2] + sh.wsel[3]);
+      if (ntot > 0 && ntot <= kWave) {
+        int off = 0;
+        for (int w = 0; w < wid; ++w) off += sh.wsel[w];
+        for (int p0 = 0; p0 < n; p0 += kWave) {
+          const int p = p0 + lane;
+          const float v = p < n ? bv[p] : -INFINITY;
+          const bool k = v > tb;
+          const uint64_t b = ballot(k);
+          if (k) sh.sel[off + rank_in(b)] = v;
+          off += __popcll(b);
+        }
+        __syncthreads();
+        if (wid == 0) {
+          const float c = lane < ntot ? sh.sel[lane] : -INFINITY;
+          const double tt = clamp_below_max(select_small(c, ntot, lane), M);
+          const int kk = __popcll(ballot(lane < ntot && c > rd32(tt)));
+          if (lane == 0) {
+            sh.tau = tt;
+            sh.kappa = kk;
+          }
+        }
+      } else if (ntot > kWave) {
+        if (wid == 0) {
+          // fixed-point iterations over the four lists (wavefront 0)
+          auto all_sum_count = [&](float thr, double& s, int& c) {
+            double st = 0.0;
+            int ct = 0;
+            for (int w = 0; w < kWavesPerBlock; ++w) {
+              double sw;
+              int cw;
+              list_sum_count(sh.bval[w], sh.wn[w], thr, lane, sw, cw);
+              st += sw;
+              ct += cw;
+            }
+            s = st;
+            c = ct;
+          };
+          double tt = (double)tb, s;
+          int c;
+          all_sum_count(tb, s, c);
+          double res_t = NAN;
+          int res_k = 0;
+          for (int it = 0; it <= C + 1; ++it) {
+            const double tn = (s - 1.0) / (double)c;
+            double s2;
+            int c2;
+            all_sum_count(rd32(tn), s2, c2);
+            if (c2 == c || !(tn > tt)) {
+              res_t = tn;
+              res_k = c2;
+              break;
+            }
+            tt = tn;
+            s = s2;
+            c = c2;
+          }
+          const double tc = clamp_below_max(res_t, M);
+          if (tc != res_t) {
+            double s3;
+            res_t = tc;
+            all_sum_count(rd32(res_t), s3, res_k);
+          }
+          if (lane == 0) {
+            sh.tau = res_t;
+            sh.kappa = res_k;
+          }
+        }
+      } else if (threadIdx.x == 0) {
+        sh.tau = NAN;
+        sh.kappa = 0;
+      }
+      __syncthreads();
+      tau = sh.tau;
+      kappa = sh.kappa;
+      const float Hf = rd32(tau);
+      const float inv = (float)(o.scale / (double)kappa);
+      if constexpr (MODE == kGrad || MODE == kMask) {
+        for (int p = lane; p < n; p += kWave) {
+          const int id = bi[p];
+          if (id == yr) continue;
+          const bool s = bv[p] > Hf;
+          if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + id] = s ? inv : 0.0f;
+          else o.mask[r * (int64_t)C + id] = (uint8_t)s;
+        }
+      } else {
+        int ns = 0;
+        for (int p0 = 0; p0 < n; p0 += kWave) {
+          const int p = p0 + lane;
+          ns += __popcll(ballot(p < n && bv[p] > Hf));
+        }
+        __syncthreads();
+        if (lane == 0) sh.wsel[wid] = ns;
+        __syncthreads();
+        int off = 0;
+        for (int w = 0; w < wid; ++w) off += sh.wsel[w];
+        float* cv = o.cval + r * (int64_t)C;
+        int32_t* ci = o.cidx + r * (int64_t)C;
+        for (int p0 = 0; p0 < n; p0 += kWave) {
+          const int p = p0 + lane;
+          const float v = p < n ? bv[p] : -INFINITY;
+          const bool k = v > Hf;
+          const uint64_t b = ballot(k);
+          if (k) {
+            const int pos = off + rank_in(b);
+            cv[pos] = v;
+            ci[pos] = bi[p];
+          }
+          off += __popcll(b);
+        }
+      }
+    } else {
+      generic_row<MODE>(row, r, C, yr, lane, wid, sh, o, tau, kappa);
+    }
+
+    if (threadIdx.x == 0) {
+      const float Hf = rd32(tau);
+      const float inv = (float)(o.scale / (double)kappa);
+      const float zy = yok ? row[yr] : NAN;
+      if (yok) {
+        if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + yr] = (zy > Hf ? inv : 0.0f) - o.scale_f;
+        else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
+      }
+      const float loss = (float)((1.0 - (double)zy) + tau);
+      if (o.H) o.H[r] = Hf;
+      if (o.loss) o.loss[r] = loss;
+      if (o.kappa) o.kappa[r] = kappa;
+      if constexpr (MODE == kCand) o.ccnt[r] = kappa;
+      bsum += (double)loss;
+    }
+    __syncthreads();
+  }
+  mean_epilogue(bsum, o);
+}
+
+// ------------------------------------------------------------------------------------------------
+// two-op backward kernels of the drop-in interface
+
+template <bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_mask_to_grad(const int64_t* __restrict__ tgt,
+                                                           const uint8_t* __restrict__ mask,
+                                                           const int32_t* __restrict__ kap,
+                                                           int64_t N, int C, double scale,
+                                                           float scale_f, float* __restrict__ grad) {
+  const int lane = lane_id();
+  const int wid = uniform((int)(threadIdx.x >> 6));
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid; r < N; r += stride) {
+    const int64_t y64 = tgt[r];
+    const int yr = (y64 >= 0 && y64 < C) ? (int)y64 : -1;
+    const float inv = (float)(scale / (double)kap[r]);
+    const uint8_t* mr = mask + r * (int64_t)C;
+    float* gr = grad + r * (int64_t)C;
+    if constexpr (V4) {
+      const int nvec = C >> 2;
+      for (int q = lane; q < nvec; q += kWave) {
+        const unsigned mk = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(mr) + q);
+        v4f g;
+        g.x = (mk & 0xFFu) ? inv : 0.0f;
+        g.y = (mk & 0xFF00u) ? inv : 0.0f;
+        g.z = (mk & 0xFF0000u) ? inv : 0.0f;
+        g.w = (mk & 0xFF000000u) ? inv : 0.0f;
+        const int d = yr - 4 * q;
+        if (d == 0) g.x -= scale_f;
+        else if (d == 1) g.y -= scale_f;
+        else if (d == 2) g.z -= scale_f;
+        else if (d == 3) g.w -= scale_f;
+        __builtin_nontemporal_store(g, reinterpret_cast<v4f*>(gr) + q);
+      }
+    } else {
+      for (int j = lane; j < C; j += kWave) {
+        float g = mr[j] ? inv : 0.0f;
+        if (j == yr) g -= scale_f;
+        __builtin_nontemporal_store(g, gr + j);
+      }
+    }
+  }
+}
+
+template <bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_cand_to_grad(
+    const float* __restrict__ z, const int64_t* __restrict__ tgt, const float* __restrict__ Hin,
+    const int32_t* __restrict__ kap, const float* __restrict__ cval, const int32_t* __restrict__ cidx,
+    const int32_t* __restrict__ ccnt, int64_t N, int C, double scale, float scale_f,
+    float* __restrict__ grad) {
+  for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
+    float* gr = grad + r * (int64_t)C;
+    if constexpr (V4) {
+      const int nvec = C >> 2;
+      for (int q = threadIdx.x; q < nvec; q += kBlock)
+        __builtin_nontemporal_store(v4f{0.0f, 0.0f, 0.0f, 0.0f}, reinterpret_cast<v4f*>(gr) + q);
+    } else {
+      for (int j = threadIdx.x; j < C; j += kBlock) __builtin_nontemporal_store(0.0f, gr + j);
+    }
+    // the zeros must land before the scattered values below (same addresses, other threads)
+    __threadfence();
+    __syncthreads();
+    const int64_t y64 = tgt[r];
+    const int yr = (y64 >= 0 && y64 < C) ? (int)y64 : -1;
+    const float h = Hin[r];
+    const float inv = (float)(scale / (double)kap[r]);
+    int cnt = ccnt[r];
+    cnt = cnt < 0 ? 0 : (cnt > C ? C : cnt);
+    for (int p = threadIdx.x; p < cnt; p += kBlock) {
+      const float v = cval[r * (int64_t)C + p];
+      const int id = cidx[r * (int64_t)C + p];
+      if (id >= 0 && id < C && id != yr && v > h) gr[id] = inv;
+    }
+    if (threadIdx.x == 0 && yr >= 0) gr[yr] = (z[r * (int64_t)C + yr] > h ? inv : 0.0f) - scale_f;
+    __syncthreads();
+  }
+}
+
+template <bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_scale_rows(float* __restrict__ grad,
+                                                         const float* __restrict__ go,
+                                                         int64_t go_stride, int64_t N, int C) {
+  const int lane = lane_id();
+  const int wid = uniform((int)(threadIdx.x >> 6));
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid; r < N; r += stride) {
+    const float s = go[r * go_stride];
+    if (s == 1.0f) continue;
+    float* gr = grad + r * (int64_t)C;
+    if constexpr (V4) {
+      for (int q = lane; q < (C >> 2); q += kWave) {
+        v4f g = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(gr) + q);
+        g *= s;
+        __builtin_nontemporal_store(g, reinterpret_cast<v4f*>(gr) + q);
+      }
+    } else {
+      for (int j = lane; j < C; j += kWave) gr[j] *= s;
+    }
+  }
+}
+
+__global__ void fwl_empty_mean(float* mean, double reduce_div) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) *mean = (float)(0.0 / reduce_div);
+}
+
+// ------------------------------------------------------------------------------------------------
+// host side
+
+int g_path = 0;
+int g_cap = kCapMax;
+
+int blocks_wave(int64_t N) {
+  const int64_t b = (N + kWavesPerBlock - 1) / kWavesPerBlock;
+  return (int)(b < kMaxBlocksWave ? (b > 0 ? b : 1) : kMaxBlocksWave);
+}
+int blocks_row(int64_t N) { return (int)(N < kMaxBlocksRow ? (N > 0 ? N : 1) : kMaxBlocksRow); }
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+int launch_status() { return hipGetLastError() == hipSuccess ? FWL_OK : FWL_ERR_LAUNCH; }
+
+template <int MODE, int NV, bool V4>
+void launch_wave(const float* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+  hipLaunchKernelGGL((fwl_wave_rows<MODE, NV, V4>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, y, N, C, o);
+}
+
+template <int MODE>
+void dispatch_wave(const float* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
+                   hipStream_t s) {
+  if (v4) {
+    if (C <= 256) launch_wave<MODE, 1, true>(z, y, N, C, o, s);
+    else if (C <= 512) launch_wave<MODE, 2, true>(z, y, N, C, o, s);
+    else launch_wave<MODE, 4, true>(z, y, N, C, o, s);
+  } else {
+    if (C <= 64) launch_wave<MODE, 1, false>(z, y, N, C, o, s);
+    else if (C <= 128) launch_wave<MODE, 2, false>(z, y, N, C, o, s);
+    else if (C <= 256) launch_wave<MODE, 4, false>(z, y, N, C, o, s);
+    else if (C <= 512) launch_wave<MODE, 8, false>(z, y, N, C, o, s);
+    else launch_wave<MODE, 16, false>(z, y, N, C, o, s);
+  }
+}
+
+template <int MODE>
+void dispatch_block(const float* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
+                    hipStream_t s) {
+  if (v4)
+    hipLaunchKernelGGL((fwl_block_rows<MODE, true>), dim3(blocks_row(N)), dim3(kBlock), 0, s, z, y, N, C, o);
+  else
+    hipLaunchKernelGGL((fwl_block_rows<MODE, false>), dim3(blocks_row(N)), dim3(kBlock), 0, s, z, y, N, C, o);
+}
+
+bool bad_shape(int64_t N, int64_t C) { return N < 0 || C < 1 || C >= (int64_t)INT32_MAX - 64; }
+
+// shared forward driver; `out_v4_ok` says whether the mode's dense output allows 128-bit access
+template <int MODE>
+int forward(const float* z, const int64_t* y, int64_t N, int64_t C64, double scale, double reduce_div,
+            Outs o, bool out_v4_ok, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (bad_shape(N, C64) || (N > 0 && (z == nullptr || y == nullptr))) return FWL_ERR_INVALID_ARG;
+  if (!aligned(z, 4) || !aligned(y, 8)) return FWL_ERR_ALIGNMENT;
+  const int C = (int)C64;
+  o.scale = scale;
+  o.reduce_div = reduce_div;
+  o.scale_f = (float)scale;
+  o.cap = g_cap;
+  o.force_generic = g_path == 3;
+  if (o.mean != nullptr) {
+    if (ws == nullptr || ws_bytes < fwl_workspace_bytes(N, C64) || !aligned(ws, 8)) return FWL_ERR_WORKSPACE;
+    o.ticket = static_cast<unsigned*>(ws);
+    o.partials = reinterpret_cast<double*>(static_cast<char*>(ws) + kWsHeader);
+  }
+  if (N == 0) {
+    if (o.mean != nullptr) hipLaunchKernelGGL(fwl_empty_mean, dim3(1), dim3(1), 0, s, o.mean, reduce_div);
+    return launch_status();
+  }
+  const bool v4 = (C % 4) == 0 && aligned(z, 16) && out_v4_ok;
+  int path = g_path;
+  if (path == 0) path = C <= kMaxWaveC ? 1 : 2;
+  if (path == 1 && C > kMaxWaveC) path = 2;
+  if (path == 1) dispatch_wave<MODE>(z, y, N, C, v4, o, s);
+  else dispatch_block<MODE>(z, y, N, C, v4, o, s);
+  return launch_status();
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------
+// C ABI
+
+extern "C" {
+
+const char* fwl_status_string(int status) {
+  switch (status) {
+    case FWL_OK: return "ok";
+    case FWL_ERR_INVALID_ARG: return "invalid argument (null pointer, N < 0, C < 1 or C too large)";
+    case FWL_ERR_WORKSPACE: return "workspace missing, misaligned or smaller than fwl_workspace_bytes(N, C)";
+    case FWL_ERR_ALIGNMENT: return "misaligned pointer (logits/grad need 4 bytes, targets 8 bytes)";
+    case FWL_ERR_LAUNCH: return "kernel launch failed (is the current device a gfx950?)";
+    case FWL_ERR_DEVICE: return "no usable device";
+    default: return "unknown fwloss status";
+  }
+}
+
+size_t fwl_workspace_bytes(int64_t N, int64_t C) {
+  (void)C;
+  const int64_t b = blocks_wave(N) > blocks_row(N) ? blocks_wave(N) : blocks_row(N);
+  return kWsHeader + sizeof(double) * (size_t)b;
+}
+
+int fwl_forward_backward(const float* logits, const int64_t* targets, int64_t N, int64_t C,
+                         double scale, double reduce_div, float* H, float* losses,
+                         float* mean_loss, int32_t* kappa, float* grad, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
+  if (N > 0 && grad == nullptr) return FWL_ERR_INVALID_ARG;
+  if (!aligned(grad, 4)) return FWL_ERR_ALIGNMENT;
+  Outs o = {};
+  o.H = H;
+  o.loss = losses;
+  o.mean = mean_loss;
+  o.kappa = kappa;
+  o.grad = grad;
+  return forward<kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
+                        workspace_bytes, stream);
+}
+
+int fwl_forward_small(const float* logits, const int64_t* targets, int64_t N, int64_t C,
+                      float* H, float* losses, float* mean_loss, int32_t* kappa,
+                      uint8_t* selected, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream) {
+  if (N > 0 && selected == nullptr) return FWL_ERR_INVALID_ARG;
+  Outs o = {};
+  o.H = H;
+  o.loss = losses;
+  o.mean = mean_loss;
+  o.kappa = kappa;
+  o.mask = selected;
+  return forward<kMask>(logits, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o,
+                        aligned(selected, 4), workspace, workspace_bytes, stream);
+}
+
+int fwl_forward_large(const float* logits, const int64_t* targets, int64_t N, int64_t C,
+                      float* H, float* losses, float* mean_loss, int32_t* kappa,
+                      float* cand_values, int32_t* cand_indices, int32_t* cand_counts,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (N > 0 && (cand_values == nullptr || cand_indices == nullptr || cand_counts == nullptr))
+    return FWL_ERR_INVALID_ARG;
+  if (!aligned(cand_values, 4) || !aligned(cand_indices, 4) || !aligned(cand_counts, 4))
+    return FWL_ERR_ALIGNMENT;
+  Outs o = {};
+  o.H = H;
+  o.loss = losses;
+  o.mean = mean_loss;
+  o.kappa = kappa;
+  o.cval = cand_values;
+  o.cidx = cand_indices;
+  o.ccnt = cand_counts;
+  return forward<kCand>(logits, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o, true,
+                        workspace, workspace_bytes, stream);
+}
+
+int fwl_backward_small(const int64_t* targets, const uint8_t* selected, const int32_t* kappa,
+                       int64_t N, int64_t C, float* grad, hipStream_t stream) {
+  if (bad_shape(N, C) || (N > 0 && (targets == nullptr || selected == nullptr || kappa == nullptr ||
+                                    grad == nullptr)))
+    return FWL_ERR_INVALID_ARG;
+  if (!aligned(targets, 8) || !aligned(kappa, 4) || !aligned(grad, 4)) return FWL_ERR_ALIGNMENT;
+  if (N == 0) return FWL_OK;
+  const double scale = 1.0 / (double)N;
+  const bool v4 = (C % 4) == 0 && aligned(selected, 4) && aligned(grad, 16);
+  const int Ci = (int)C;
+  if (v4)
+    hipLaunchKernelGGL((fwl_mask_to_grad<true>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, targets,
+                       selected, kappa, N, Ci, scale, (float)scale, grad);
+  else
+    hipLaunchKernelGGL((fwl_mask_to_grad<false>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, targets,
+                       selected, kappa, N, Ci, scale, (float)scale, grad);
+  return launch_status();
+}
+
+int fwl_backward_large(const float* logits, const int64_t* targets, const float* H,
+                       const int32_t* kappa, const float* cand_values,
+                       const int32_t* cand_indices, const int32_t* cand_counts, int64_t N,
+                       int64_t C, float* grad, hipStream_t stream) {
+  if (bad_shape(N, C) || (N > 0 && (logits == nullptr || targets == nullptr || H == nullptr ||
+                                    kappa == nullptr || cand_values == nullptr ||
+                                    cand_indices == nullptr || cand_counts == nullptr || grad == nullptr)))
+    return FWL_ERR_INVALID_ARG;
+  if (!aligned(logits, 4) || !aligned(targets, 8) || !aligned(grad, 4)) return FWL_ERR_ALIGNMENT;
+  if (N == 0) return FWL_OK;
+  const double scale = 1.0 / (double)N;
+  const bool v4 = (C % 4) == 0 && aligned(grad, 16);
+  const int Ci = (int)C;
+  if (v4)
+    hipLaunchKernelGGL((fwl_cand_to_grad<true>), dim3(blocks_row(N)), dim3(kBlock), 0, stream, logits,
+                       targets, H, kappa, cand_values, cand_indices, cand_counts, N, Ci, scale,
+                       (float)scale, grad);
+  else
+    hipLaunchKernelGGL((fwl_cand_to_grad<false>), dim3(blocks_row(N)), dim3(kBlock), 0, stream, logits,
+                       targets, H, kappa, cand_values, cand_indices, cand_counts, N, Ci, scale,
+                       (float)scale, grad);
+  return launch_status();
+}
+
+int fwl_scale_grad(float* grad, const float* grad_output, int64_t go_stride, int64_t N, int64_t C,
+                   hipStream_t stream) {
+  if (bad_shape(N, C) || go_stride < 0 || (N > 0 && (grad == nullptr || grad_output == nullptr)))
+    return FWL_ERR_INVALID_ARG;
+  if (!aligned(grad, 4) || !aligned(grad_output, 4)) return FWL_ERR_ALIGNMENT;
+  if (N == 0) return FWL_OK;
+  const int Ci = (int)C;
+  if ((C % 4) == 0 && aligned(grad, 16))
+    hipLaunchKernelGGL((fwl_scale_rows<true>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, grad, grad_output,
+                       go_stride, N, Ci);
+  else
+    hipLaunchKernelGGL((fwl_scale_rows<false>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, grad, grad_output,
+                       go_stride, N, Ci);
+  return launch_status();
+}
+
+int fwl_set_params(int path, int cand_cap) {
+  if (path < 0 || path > 3 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
+  g_path = path;
+  g_cap = cand_cap;
+  return FWL_OK;
+}
+
+int fwl_get_params(int* path, int* cand_cap) {
+  if (path) *path = g_path;
+  if (cand_cap) *cand_cap = g_cap;
+  return FWL_OK;
+}
+
+}  // extern "C"

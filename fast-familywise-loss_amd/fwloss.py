@@ -1,0 +1,91 @@
+"""Familywise (FW) loss on MI355X: the Python API over the ``fw_radix_cuda`` extension.
+
+Mirrors the reference's CPU module ``src/cpu/fwcpp.py:18-26``::
+
+    from fwloss import familywise_loss
+    loss = familywise_loss(logits, target, reduction="mean")   # logits: float32 [N, C] on the GPU
+    loss.backward()
+
+The forward runs the fused HIP kernel, which computes the loss and the gradient in one pass over
+the logits (as the reference's C++ autograd Function does eagerly, src/cpu/fw_cpu.cpp:721-733);
+the backward multiplies the stored gradient by ``grad_output`` on the device, skipping rows whose
+factor is 1 (fw_cpu.cpp:734-740).  There is no CPU fallback: without the HIP extension the import
+fails, and CPU tensors are rejected.
+
+The reference GPU ops are re-exported unchanged: ``fw_forward``, ``fw_backward``,
+``fw_forward_small``, ``fw_backward_small`` (src/cuda/binding.cpp:8-13).
+"""
+import os
+import sys
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+if _HERE not in sys.path:
+    sys.path.insert(0, _HERE)
+
+try:
+    import fw_radix_cuda as _ext  # noqa: E402  (torch must be imported first: one HIP runtime)
+except ImportError as e:  # pragma: no cover - exercised only on a broken install
+    raise ImportError("fw_radix_cuda is not built; run `python fast-familywise-loss_amd/fwloss_build.py` "
+                      "(there is no CPU fallback)") from e
+
+fw_forward = _ext.fw_forward
+fw_backward = _ext.fw_backward
+fw_forward_small = _ext.fw_forward_small
+fw_backward_small = _ext.fw_backward_small
+fw_forward_backward = _ext.fw_forward_backward
+set_params = _ext.set_params
+get_params = _ext.get_params
+
+_REDUCTIONS = ("mean", "sum", "none")
+
+
+class FWFunction(torch.autograd.Function):
+    """Eager-gradient autograd Function (the GPU counterpart of fw_cpu.cpp:721-741)."""
+
+    @staticmethod
+    def forward(ctx, logits, target, reduction):
+        N = logits.shape[0]
+        if reduction == "mean":
+            scale, rdiv = (1.0 / N if N else 1.0), float(N)
+        else:
+            scale, rdiv = 1.0, 1.0
+        _, losses, reduced, _, grad = _ext.fw_forward_backward(logits.detach(), target, scale, rdiv)
+        ctx.save_for_backward(grad)
+        return losses if reduction == "none" else reduced
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (grad,) = ctx.saved_tensors
+        if not ctx.needs_input_grad[0]:
+            return None, None, None
+        _ext.fw_scale_grad(grad, grad_output.detach())
+        return grad, None, None
+
+
+def familywise_loss(logits, target, reduction="mean"):
+    """FW loss of float32 logits [N, C] (GPU) and int64 targets [N]; reduction 'mean' | 'sum' | 'none'.
+
+    Same call shape as the reference's ``fwcpp.familywise_loss`` (src/cpu/fwcpp.py:18-19), which
+    accepts 'sum' and 'mean'; 'none' returns the per-row losses (reference_impl.py:30-33).
+    """
+    if reduction not in _REDUCTIONS:
+        raise ValueError(f"Invalid reduction mode: {reduction}")
+    if not logits.is_cuda:
+        raise RuntimeError("familywise_loss: logits must be a CUDA (ROCm) tensor; this package has no CPU path")
+    return FWFunction.apply(logits, target, reduction)
+
+
+def fw_loss_grad(Z, y, scale=1.0):
+    """(per-row loss [N] float32, scale * gradient [N, C], kappa [N] int32), as fwcpp.fw_loss_grad
+    (src/cpu/fwcpp.py:21-23) returns (loss, scale * gradient, kappa) for the CPU path."""
+    if not Z.is_cuda:
+        raise RuntimeError("fw_loss_grad: Z must be a CUDA (ROCm) tensor")
+    _, losses, _, kappa, grad = _ext.fw_forward_backward(Z, y, float(scale), 1.0)
+    return losses, grad, kappa
+
+
+def native_libraries():
+    """Paths of the native libraries this module runs on (for load checks)."""
+    return [os.path.join(_HERE, "libfwloss.so"), _ext.__file__]

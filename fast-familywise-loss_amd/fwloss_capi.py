@@ -1,0 +1,107 @@
+"""ctypes binding of libfwloss.so's C ABI (include/fwloss.h).
+
+This is the binding a Python caller without the torch extension would use (see INTEGRATION.md for
+the same stubs in other languages).  Pointers are passed as integers, so any device allocator
+works; the helpers below take torch tensors for convenience.  ``torch`` is imported before the
+library is opened so that the process holds a single HIP runtime (torch's).
+"""
+import ctypes
+import os
+import re
+
+import torch  # noqa: F401  (must precede loading libfwloss.so)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libfwloss.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "fwloss.h")
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_D = ctypes.c_double
+
+SIGNATURES = {
+    "fwl_status_string": ([ctypes.c_int], ctypes.c_char_p),
+    "fwl_workspace_bytes": ([_I64, _I64], ctypes.c_size_t),
+    "fwl_forward_backward": ([_P, _P, _I64, _I64, _D, _D, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], ctypes.c_int),
+    "fwl_forward_small": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], ctypes.c_int),
+    "fwl_backward_small": ([_P, _P, _P, _I64, _I64, _P, _P], ctypes.c_int),
+    "fwl_forward_large": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], ctypes.c_int),
+    "fwl_backward_large": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P], ctypes.c_int),
+    "fwl_scale_grad": ([_P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
+    "fwl_set_params": ([ctypes.c_int, ctypes.c_int], ctypes.c_int),
+    "fwl_get_params": ([ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.isfile(LIB_PATH):
+            raise RuntimeError("libfwloss.so is not built; run python fast-familywise-loss_amd/fwloss_build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def declared_functions():
+    """Names of the functions declared in include/fwloss.h."""
+    with open(HEADER_PATH) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(fwl_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+def status_string(rc):
+    return lib().fwl_status_string(rc).decode()
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _check(rc, name):
+    if rc != 0:
+        raise RuntimeError(f"{name}: {status_string(rc)} ({rc})")
+
+
+class Workspace:
+    """Zero-filled device workspace; the library leaves it zero-filled after every call."""
+
+    def __init__(self, device, nbytes=1 << 16):
+        self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+    def get(self, N, C):
+        need = lib().fwl_workspace_bytes(N, C)
+        if self.buf.numel() < need:
+            self.buf = torch.zeros(need, dtype=torch.uint8, device=self.buf.device)
+        return self.buf
+
+
+def forward_backward(z, y, scale=None, reduce_div=None, ws=None):
+    """Fused op through the C ABI.  Returns dict(H, loss, mean, kappa, grad)."""
+    N, C = z.shape
+    scale = (1.0 / N if N else 1.0) if scale is None else scale
+    reduce_div = float(N) if reduce_div is None else reduce_div
+    ws = ws or Workspace(z.device)
+    buf = ws.get(N, C)
+    out = dict(H=torch.empty(N, device=z.device), loss=torch.empty(N, device=z.device),
+               mean=torch.empty((), device=z.device), kappa=torch.empty(N, dtype=torch.int32, device=z.device),
+               grad=torch.empty_like(z))
+    rc = lib().fwl_forward_backward(_ptr(z), _ptr(y), N, C, scale, reduce_div, _ptr(out["H"]), _ptr(out["loss"]),
+                                    _ptr(out["mean"]), _ptr(out["kappa"]), _ptr(out["grad"]), _ptr(buf),
+                                    buf.numel(), _stream())
+    _check(rc, "fwl_forward_backward")
+    return out
+
+
+def set_params(path, cand_cap=512):
+    _check(lib().fwl_set_params(path, cand_cap), "fwl_set_params")

@@ -1,0 +1,76 @@
+"""Seeded synthetic inputs for the benchmark configurations.
+
+One generator per configuration, as the configurations are specified for this operator (logits and
+int64 labels uniform in [0, C)); the reference seeds its GPU harness with torch.manual_seed(0)
+(benchmarks/cuda_benchmarks/CE_FW_perf.py:91-92) and its CPU harness with default_rng(0)
+(benchmarks/cpu_benchmarks/bench_cpu_e2e.py:30).  Inputs are produced on the host with numpy's
+PCG64 so that the CPU checkers and the GPU see identical bytes.
+
+    cfg1  N=1024,  C=10      N(0,1)
+    cfg2  N=65536, C=1000    N(0,1)                                  (headline)
+    cfg3  N=16384, C=100     0.5 * integers in [-8, 8]               (heavy exact ties)
+    cfg4  N=8192,  C=32000   N(0,1), +4 on the label in 70% of rows
+    cfg5  N=2048,  C=131072  Gumbel(0,1); 1% -inf, 0.1% +-0.0, labels kept finite
+"""
+import numpy as np
+
+CONFIGS = {
+    "cfg1": dict(N=1024, C=10),
+    "cfg2": dict(N=65536, C=1000),
+    "cfg3": dict(N=16384, C=100),
+    "cfg4": dict(N=8192, C=32000),
+    "cfg5": dict(N=2048, C=131072),
+}
+
+
+def make(cfg, N=None, seed=0):
+    """(z float32 [N, C], y int64 [N]) for configuration ``cfg`` (N defaults to the config's)."""
+    spec = CONFIGS[cfg]
+    N = spec["N"] if N is None else N
+    C = spec["C"]
+    rng = np.random.default_rng(seed)
+    y = rng.integers(0, C, size=N, dtype=np.int64)
+    if cfg in ("cfg1", "cfg2"):
+        z = rng.standard_normal((N, C), dtype=np.float32)
+    elif cfg == "cfg3":
+        z = (0.5 * rng.integers(-8, 9, size=(N, C))).astype(np.float32)
+    elif cfg == "cfg4":
+        z = rng.standard_normal((N, C), dtype=np.float32)
+        boost = rng.random(N) < 0.7
+        z[np.arange(N)[boost], y[boost]] += np.float32(4.0)
+    elif cfg == "cfg5":
+        u = rng.random((N, C), dtype=np.float32)
+        u = np.clip(u, np.float32(1e-7), np.float32(1.0 - 6e-8))
+        z = -np.log(-np.log(u))
+        w = rng.random((N, C), dtype=np.float32)
+        zy = z[np.arange(N), y].copy()
+        z[w < 0.01] = -np.inf
+        z[(w >= 0.01) & (w < 0.0105)] = 0.0
+        z[(w >= 0.0105) & (w < 0.011)] = -0.0
+        z[np.arange(N), y] = zy
+        z = z.astype(np.float32, copy=False)
+    else:
+        raise KeyError(cfg)
+    return np.ascontiguousarray(z, dtype=np.float32), y
+
+
+def edge_rows():
+    """Hand-made rows exercising the special cases of the definition: (z [R, C], y [R]) per C."""
+    C = 16
+    rows = [
+        np.zeros(C),                                            # constant row: kappa = C
+        np.full(C, 3.25),                                       # constant, shifted
+        np.r_[5.0, np.zeros(C - 1)],                            # top gap >= 1: kappa = 1
+        np.r_[1.0, 1.0, np.zeros(C - 2)],                       # gap exactly 1 below a tie pair
+        np.r_[np.full(4, 2.0), np.full(C - 4, 1.0)],            # two levels
+        np.r_[4.0, 4.0, 3.5, 3.5, np.full(C - 4, -1.0)],        # exact tie at the boundary
+        np.r_[-0.0, 0.0, -0.0, 0.0, np.full(C - 4, -3.0)],      # signed zeros are equal
+        np.r_[np.full(C - 1, -np.inf), 0.5],                    # -inf entries never selected
+        np.linspace(-1.0, 1.0, C),                              # evenly spaced
+        np.r_[1e-30, -1e-30, 1e-38, np.zeros(C - 3)],            # tiny magnitudes
+        np.r_[1e30, 1e30 - 2**80, np.full(C - 2, -1e30)],       # huge magnitudes
+        np.r_[np.float32(1) + np.float32(2**-23), 2.0, np.full(C - 2, -5.0)],
+    ]
+    z = np.stack([np.asarray(r, dtype=np.float64) for r in rows]).astype(np.float32)
+    y = np.array([3, 0, 0, 1, 7, 2, 1, 15, 8, 4, 1, 0], dtype=np.int64)
+    return z, y

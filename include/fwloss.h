@@ -1,0 +1,124 @@
+/*
+ * fwloss.h -- C ABI of the MI355X (gfx950) Familywise (FW) loss library, libfwloss.so.
+ *
+ * For each row z (C fp32 logits) with label y the library computes the FW threshold
+ *     tau = max_k (S_k - 1)/k,   S_k = sum of the k largest entries of z,
+ * the support {j : z_j > tau} (strict), kappa = its size, the loss 1 - z_y + tau and the gradient
+ *     grad_j = scale * ( [z_j > tau] / kappa - [j == y] ).
+ * (Reference definition: reference_impl.py:11-35; closed form: src/cpu/fw_cpu.cpp:1-4.)
+ *
+ * Output conventions (every entry point):
+ *   H[r]       largest float <= tau, so that for every float x:  x > H[r]  <=>  x > tau.  Any test
+ *              "z > H" therefore selects exactly the support.
+ *   losses[r]  (float)((1 - z_y) + tau), evaluated in fp64.
+ *   kappa[r]   |{j : z_j > tau}|.
+ *   mean_loss  (float)(sum_r losses[r] / N), summed in fp64 in a fixed order (deterministic).
+ *   grad       inv = (float)(scale / kappa); grad[r,j] = z_j > tau ? inv : 0; grad[r,y] -= (float)scale.
+ *              The ops that mirror the reference bake in scale = 1/N (mean reduction).
+ * Threshold decisions are exact for rows whose fp64 partial sums are exact (every row whose
+ * candidates (max-1, max] span fewer than 29 binades, which includes every finite row away from 0).
+ *
+ * Calling convention:
+ *   - all pointers are device pointers; logits and grad are row-major [N, C], contiguous;
+ *   - every call is asynchronous on `stream` and allocates nothing;
+ *   - `workspace` is caller-provided device memory of at least fwl_workspace_bytes(N, C) bytes,
+ *     zero-filled before its first use; every call leaves it zero-filled again.  Calls that run
+ *     concurrently (different streams) must not share one workspace;
+ *   - targets outside [0, C) do not fault: that row gets loss = NaN and no label term in grad;
+ *   - NaN logits are never selected; rows without a finite maximum give kappa = 0, H = NaN;
+ *   - the return value is FWL_OK or an fwl_status (argument errors are detected before launch).
+ */
+#ifndef FWLOSS_H
+#define FWLOSS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+enum fwl_status {
+  FWL_OK = 0,
+  FWL_ERR_INVALID_ARG = 1,  /* null pointer, N < 0, C < 1, C >= 2^31 - 64 */
+  FWL_ERR_WORKSPACE = 2,    /* workspace missing or smaller than fwl_workspace_bytes(N, C) */
+  FWL_ERR_ALIGNMENT = 3,    /* logits/grad not 4-byte aligned, or targets not 8-byte aligned */
+  FWL_ERR_LAUNCH = 4,       /* the HIP runtime rejected a launch */
+  FWL_ERR_DEVICE = 5        /* no usable gfx950 device current */
+};
+
+/* Human-readable text of a status code (static storage). */
+const char* fwl_status_string(int status);
+
+/* Bytes of device workspace the forward entry points need for an [N, C] problem. */
+size_t fwl_workspace_bytes(int64_t N, int64_t C);
+
+/* Fused forward + backward: the whole hot path in one launch, reading logits once and writing the
+ * dense gradient once.  mean_loss receives (float)(sum_r losses[r] / reduce_div) (reduce_div = N
+ * for a mean, 1 for a sum).  Any of H, losses, kappa, mean_loss may be NULL.
+ * Replaces the two-op sequence fw_radix_forward_small + fw_radix_backward_small
+ * (src/cuda/fw_radix_argmax.cu:1381-1414, :1591-1609; driven by
+ * benchmarks/cuda_benchmarks/CE_FW_perf.py:76-88) and the eager-gradient forward of the CPU
+ * autograd Function (src/cpu/fw_cpu.cpp:721-741, scale as in :746-748). */
+int fwl_forward_backward(const float* logits, const int64_t* targets, int64_t N, int64_t C,
+                         double scale, double reduce_div, float* H, float* losses,
+                         float* mean_loss, int32_t* kappa, float* grad, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
+
+/* Forward with the support mask: selected[r,j] = (z_j > tau) as bytes 0/1 (torch.bool layout).
+ * Replaces fw_radix_forward_small (src/cuda/fw_radix_argmax.cu:1381-1414; binding.cpp:11):
+ * outputs [H, losses, mean_loss, kappa, selected_logits]. */
+int fwl_forward_small(const float* logits, const int64_t* targets, int64_t N, int64_t C,
+                      float* H, float* losses, float* mean_loss, int32_t* kappa,
+                      uint8_t* selected, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
+/* grad[r,j] = (selected[r,j] ? (float)((1/N)/kappa[r]) : 0) - [j == y_r] * (float)(1/N).
+ * Replaces fw_radix_backward_small (src/cuda/fw_radix_argmax.cu:1561-1609; binding.cpp:12). */
+int fwl_backward_small(const int64_t* targets, const uint8_t* selected, const int32_t* kappa,
+                       int64_t N, int64_t C, float* grad, hipStream_t stream);
+
+/* Forward with candidate lists.  Row r's list (cand_values[r*C + p], cand_indices[r*C + p],
+ * p < cand_counts[r]) holds exactly the support, so cand_counts[r] == kappa[r]; entries past the
+ * count are left untouched.  The order of a list is deterministic, not sorted.
+ * Replaces fw_radix_forward (src/cuda/fw_radix_argmax.cu:1417-1496; binding.cpp:9): outputs
+ * [H, losses, mean_loss, kappa, candidate_buffer, candidate_indices, candidate_counts]. */
+int fwl_forward_large(const float* logits, const int64_t* targets, int64_t N, int64_t C,
+                      float* H, float* losses, float* mean_loss, int32_t* kappa,
+                      float* cand_values, int32_t* cand_indices, int32_t* cand_counts,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Dense gradient from candidate lists: zeros, then (float)((1/N)/kappa[r]) at every listed index
+ * whose listed value is > H[r], then -(float)(1/N) at y_r (added to the selected value when y_r is
+ * selected, tested as logits[r, y_r] > H[r]).
+ * Replaces fw_radix_backward (src/cuda/fw_radix_argmax.cu:1498-1559; binding.cpp:10). */
+int fwl_backward_large(const float* logits, const int64_t* targets, const float* H,
+                       const int32_t* kappa, const float* cand_values,
+                       const int32_t* cand_indices, const int32_t* cand_counts, int64_t N,
+                       int64_t C, float* grad, hipStream_t stream);
+
+/* grad[r, :] *= grad_output[r * go_stride] for every row whose factor is not 1 (go_stride = 0: one
+ * scalar for all rows, as for a 'mean'/'sum' loss; 1: one factor per row, as for 'none').  The
+ * factor is read on the device, so the autograd backward needs no host synchronisation; rows with
+ * factor 1 are not touched.  Counterpart of FWFunction::backward (src/cpu/fw_cpu.cpp:734-740),
+ * which skips the multiply when grad_output == 1. */
+int fwl_scale_grad(float* grad, const float* grad_output, int64_t go_stride, int64_t N, int64_t C,
+                   hipStream_t stream);
+
+/* Process-wide dispatch switches, the GPU counterpart of the reference CPU path's set_params
+ * (src/cpu/fw_cpu.cpp:758-763, used by its tests to force each branch).  Not thread-safe; meant
+ * for tests and tuning.
+ *   path:      0 = automatic, 1 = one wavefront per row (C <= 1024 only), 2 = one block per row
+ *              with LDS candidate compaction, 3 = the generic multi-pass block path.
+ *   cand_cap:  LDS candidate capacity per wavefront of path 2, in [64, 512] (512 = default);
+ *              smaller values make rows overflow into the generic path sooner.
+ * Returns FWL_ERR_INVALID_ARG for values out of range. */
+int fwl_set_params(int path, int cand_cap);
+int fwl_get_params(int* path, int* cand_cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FWLOSS_H */

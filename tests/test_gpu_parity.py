@@ -1,0 +1,290 @@
+"""Parity of the HIP path with the CPU oracle (the definition, reference_impl.py:11-35, with the
+strict-support semantics of src/cpu/fw_cpu.cpp:96-101).
+
+Bar: kappa, the support (mask / candidate lists), H, per-row losses and the gradient are
+bit-identical to the oracle on every seeded configuration; the mean loss is within 1e-6 relative
+(it is summed in a different fixed order).  Full-size configurations are checked through
+size-independent properties plus a random sample of rows against the oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import fwloss_capi
+import fwloss_data as data
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(dev, z, y):
+    return torch.from_numpy(z).to(dev), torch.from_numpy(y).to(dev)
+
+
+def fused(ext, zt, yt, scale=-1.0, rdiv=-1.0):
+    H, loss, mean, kappa, grad = ext.fw_forward_backward(zt, yt, scale, rdiv)
+    torch.cuda.synchronize()
+    return dict(H=H.cpu().numpy(), loss=loss.cpu().numpy(), mean=float(mean.cpu()),
+                kappa=kappa.cpu().numpy(), grad=grad.cpu().numpy())
+
+
+def bits_equal(a, b):
+    a = np.asarray(a)
+    b = np.asarray(b)
+    if a.shape != b.shape:
+        return False
+    na, nb = np.isnan(a), np.isnan(b)
+    if not np.array_equal(na, nb):
+        return False
+    return np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+def assert_parity(out, ref, z, mean_rtol=1e-6):
+    bad = np.nonzero(out["kappa"] != ref["kappa"])[0]
+    assert bad.size == 0, f"kappa differs on rows {bad[:10]}: {out['kappa'][bad[:10]]} vs {ref['kappa'][bad[:10]]}"
+    assert bits_equal(out["H"], ref["H"]), "H not bit-identical"
+    assert bits_equal(out["loss"], ref["loss"]), "losses not bit-identical"
+    if "grad" in out:
+        assert bits_equal(out["grad"], ref["grad"]), "grad not bit-identical"
+    if out.get("mean") is not None and z.shape[0] > 0 and np.isfinite(ref["mean"]):
+        assert abs(out["mean"] - ref["mean"]) <= mean_rtol * max(1.0, abs(ref["mean"]))
+
+
+@pytest.fixture
+def reset_params(ext):
+    yield
+    ext.set_params(0, 512)
+
+
+# ---------------------------------------------------------------- seeded configurations (reduced N)
+
+REDUCED = {"cfg1": 1024, "cfg2": 2048, "cfg3": 16384, "cfg4": 96, "cfg5": 24}
+
+
+@pytest.mark.parametrize("cfg", sorted(REDUCED))
+def test_fused_matches_oracle(ext, dev, cfg):
+    z, y = data.make(cfg, N=REDUCED[cfg], seed=1)
+    print(f"fused {cfg} N={z.shape[0]} C={z.shape[1]}", flush=True)
+    ref = oracle.definition(z, y)
+    out = fused(ext, *to_dev(dev, z, y))
+    assert_parity(out, ref, z)
+
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3", "cfg4"])
+def test_drop_in_small_ops(ext, dev, cfg):
+    z, y = data.make(cfg, N=min(REDUCED[cfg], 512), seed=2)
+    print(f"small ops {cfg} N={z.shape[0]}", flush=True)
+    zt, yt = to_dev(dev, z, y)
+    H, losses, mean, kappa, sel = ext.fw_forward_small(zt, yt)
+    grad = ext.fw_backward_small(yt, sel, kappa)
+    torch.cuda.synchronize()
+    ref = oracle.definition(z, y)
+    assert sel.dtype == torch.bool and sel.shape == zt.shape
+    assert kappa.dtype == torch.int32 and mean.dim() == 0
+    np.testing.assert_array_equal(sel.cpu().numpy(), z > ref["tau"][:, None])
+    out = dict(H=H.cpu().numpy(), loss=losses.cpu().numpy(), mean=float(mean.cpu()), kappa=kappa.cpu().numpy(),
+               grad=grad.cpu().numpy())
+    assert_parity(out, ref, z)
+
+
+@pytest.mark.parametrize("cfg", ["cfg2", "cfg3", "cfg4", "cfg5"])
+def test_drop_in_large_ops(ext, dev, cfg):
+    z, y = data.make(cfg, N=min(REDUCED[cfg], 256), seed=3)
+    print(f"large ops {cfg} N={z.shape[0]}", flush=True)
+    zt, yt = to_dev(dev, z, y)
+    H, losses, mean, kappa, cbuf, cidx, ccnt = ext.fw_forward(zt, yt)
+    grad = ext.fw_backward(zt, yt, H, kappa, cbuf, cidx, ccnt)
+    torch.cuda.synchronize()
+    ref = oracle.definition(z, y)
+    cnt = ccnt.cpu().numpy()
+    np.testing.assert_array_equal(cnt, ref["kappa"])
+    cb, ci = cbuf.cpu().numpy(), cidx.cpu().numpy()
+    for r in range(z.shape[0]):
+        idx = ci[r, :cnt[r]]
+        assert np.array_equal(np.sort(idx), np.nonzero(z[r] > ref["tau"][r])[0]), f"row {r} support"
+        assert bits_equal(cb[r, :cnt[r]], z[r, idx])
+    out = dict(H=H.cpu().numpy(), loss=losses.cpu().numpy(), mean=float(mean.cpu()), kappa=kappa.cpu().numpy(),
+               grad=grad.cpu().numpy())
+    assert_parity(out, ref, z)
+
+
+# ---------------------------------------------------------------- every kernel path, same answers
+
+@pytest.mark.parametrize("path,cap", [(1, 512), (2, 512), (2, 64), (3, 512)])
+@pytest.mark.parametrize("C", [10, 100, 1000, 1024])
+def test_forced_paths(ext, dev, reset_params, path, cap, C):
+    rng = np.random.default_rng(C)
+    z = rng.standard_normal((300, C)).astype(np.float32)
+    z[::7] *= np.float32(0.01)          # flat rows: many candidates, long supports
+    z[3::11] = np.round(z[3::11] * 2) / 2   # dyadic ties
+    y = rng.integers(0, C, 300)
+    print(f"path={path} cap={cap} C={C}", flush=True)
+    ext.set_params(path, cap)
+    ref = oracle.definition(z, y)
+    out = fused(ext, *to_dev(dev, z, y))
+    assert_parity(out, ref, z)
+
+
+@pytest.mark.parametrize("cap", [64, 512])
+def test_block_path_overflow_and_tighten(ext, dev, reset_params, cap):
+    # C = 4096 rows: a flat row overflows any list (generic path), a row with many candidates but a
+    # short support exercises list tightening
+    rng = np.random.default_rng(7)
+    C = 4096
+    z = rng.standard_normal((64, C)).astype(np.float32)
+    z[0] = 0.0
+    z[1] = rng.random(C).astype(np.float32) * np.float32(0.9)       # all candidates, short support
+    z[2, :] = np.float32(1e-3) * rng.standard_normal(C).astype(np.float32)
+    z[3, ::2] = 5.0
+    y = rng.integers(0, C, 64)
+    print(f"block overflow cap={cap}", flush=True)
+    ext.set_params(2, cap)
+    ref = oracle.definition(z, y)
+    assert_parity(fused(ext, *to_dev(dev, z, y)), ref, z)
+
+
+# ---------------------------------------------------------------- shapes, layouts, special values
+
+@pytest.mark.parametrize("C", [1, 2, 3, 5, 10, 37, 63, 64, 65, 255, 257, 999, 1001, 1023, 1025, 2049, 5000, 10001])
+def test_shapes(ext, dev, C):
+    rng = np.random.default_rng(C + 11)
+    N = 67
+    z = (rng.standard_normal((N, C)) * rng.choice([0.01, 1.0, 10.0], size=(N, 1))).astype(np.float32)
+    y = rng.integers(0, C, N)
+    print(f"shape N={N} C={C}", flush=True)
+    assert_parity(fused(ext, *to_dev(dev, z, y)), oracle.definition(z, y), z)
+
+
+def test_edge_rows(ext, dev):
+    z, y = data.edge_rows()
+    print("edge rows", flush=True)
+    ref = oracle.definition(z, y)
+    out = fused(ext, *to_dev(dev, z, y))
+    assert_parity(out, ref, z)
+    # closed forms
+    C = z.shape[1]
+    assert out["kappa"][0] == C and out["kappa"][2] == 1
+    assert out["loss"][2] == np.float32(0.0)                        # 1 - 5 + (5 - 1)
+
+
+def test_label_at_minus_inf_and_bad_label(ext, dev):
+    z = np.zeros((3, 8), np.float32)
+    z[:, 5] = -np.inf
+    y = np.array([5, 8, -1], np.int64)          # -inf label, then labels out of range
+    out = fused(ext, *to_dev(dev, z, y))
+    assert np.isposinf(out["loss"][0])
+    assert np.isnan(out["loss"][1]) and np.isnan(out["loss"][2])
+    assert np.all(out["kappa"] == 7)
+    # out-of-range labels leave the gradient without the label term
+    np.testing.assert_array_equal(out["grad"][1], np.where(z[1] > out["H"][1], np.float32((1 / 3) / 7), 0))
+
+
+def test_misaligned_and_strided_inputs(ext, dev):
+    rng = np.random.default_rng(5)
+    big = torch.from_numpy(rng.standard_normal((40, 1001)).astype(np.float32)).to(dev)
+    zt = big[:, 1:]                              # non-contiguous view, C = 1000
+    yt = torch.from_numpy(rng.integers(0, 1000, 40)).to(dev)
+    z = zt.cpu().numpy()
+    ref = oracle.definition(z, yt.cpu().numpy())
+    assert_parity(fused(ext, zt, yt), ref, z)
+    flat = torch.from_numpy(rng.standard_normal(40 * 1000 + 1).astype(np.float32)).to(dev)
+    zt2 = flat[1:].view(40, 1000)                # contiguous but only 4-byte aligned
+    z2 = zt2.cpu().numpy()
+    assert_parity(fused(ext, zt2, yt), oracle.definition(z2, yt.cpu().numpy()), z2)
+
+
+def test_empty_batch(ext, dev):
+    zt = torch.empty((0, 10), device=dev)
+    yt = torch.empty((0,), dtype=torch.int64, device=dev)
+    H, loss, mean, kappa, grad = ext.fw_forward_backward(zt, yt)
+    assert H.shape == (0,) and grad.shape == (0, 10) and torch.isnan(mean).item()
+    H, loss, mean, kappa, sel = ext.fw_forward_small(zt, yt)
+    assert sel.shape == (0, 10)
+
+
+def test_deterministic(ext, dev):
+    z, y = data.make("cfg4", N=64, seed=9)
+    zt, yt = to_dev(dev, z, y)
+    a = fused(ext, zt, yt)
+    b = fused(ext, zt, yt)
+    for k in ("H", "loss", "kappa", "grad"):
+        assert bits_equal(a[k], b[k]) if a[k].dtype == np.float32 else np.array_equal(a[k], b[k])
+    assert a["mean"] == b["mean"]
+
+
+# ---------------------------------------------------------------- full-size configurations
+
+def _row_properties(zt, yt, H, loss, kappa, grad, scale):
+    """Size-independent checks on the device in fp64: the support is {z > H}, the threshold solves
+    sum(z - tau)_+ = 1, and the gradient is the closed form."""
+    z64 = zt.double()
+    sel = zt > H[:, None]
+    k = sel.sum(1)
+    assert torch.equal(k.int(), kappa), "kappa != |{z > H}|"
+    S = torch.where(sel, z64, torch.zeros_like(z64)).sum(1)
+    tau = (S - 1.0) / k.double()
+    # H is the largest float <= tau
+    assert torch.all(H.double() <= tau) and torch.all(torch.nextafter(H, torch.full_like(H, np.inf)).double() > tau)
+    # sum over the support of (z - tau) = 1, and nothing outside the support is above tau
+    resid = torch.where(sel, z64 - tau[:, None], torch.zeros_like(z64)).sum(1) - 1.0
+    assert resid.abs().max().item() < 1e-9
+    assert torch.all(torch.where(sel, torch.full_like(z64, -np.inf), z64).max(1).values <= tau)
+    zy = z64.gather(1, yt[:, None])[:, 0]
+    assert torch.allclose(loss.double(), (1.0 - zy) + tau, rtol=1e-6, atol=1e-6)
+    inv = (scale / k.double()).float()
+    expect = torch.where(sel, inv[:, None], torch.zeros_like(zt))
+    expect.scatter_(1, yt[:, None], expect.gather(1, yt[:, None]) - np.float32(scale))
+    assert torch.equal(grad, expect), "grad differs from the closed form"
+    assert grad.double().sum(1).abs().max().item() < 1e-6
+
+
+@pytest.mark.parametrize("cfg", ["cfg2", "cfg3", "cfg4", "cfg5"])
+def test_full_size(ext, dev, cfg):
+    z, y = data.make(cfg, seed=0)
+    N = z.shape[0]
+    print(f"full size {cfg} N={N} C={z.shape[1]}", flush=True)
+    zt, yt = to_dev(dev, z, y)
+    H, loss, mean, kappa, grad = ext.fw_forward_backward(zt, yt)
+    torch.cuda.synchronize()
+    _row_properties(zt, yt, H, loss, kappa, grad, 1.0 / N)
+    assert abs(mean.item() - loss.double().mean().item()) <= 1e-6 * max(1.0, abs(mean.item()))
+    rows = np.random.default_rng(0).choice(N, size=min(N, 64), replace=False)
+    ref = oracle.definition(z[rows], y[rows], scale=1.0 / N)
+    sub = dict(H=H[rows].cpu().numpy(), loss=loss[rows].cpu().numpy(), kappa=kappa[rows].cpu().numpy(),
+               grad=grad[rows].cpu().numpy(), mean=None)
+    assert_parity(sub, ref, z[rows])
+    del zt, grad
+    torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------- autograd API and the C ABI
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+def test_autograd(ext, dev, reduction):
+    z, y = data.make("cfg2", N=300, seed=4)
+    zt, yt = to_dev(dev, z, y)
+    zt.requires_grad_(True)
+    loss = ext.familywise_loss(zt, yt, reduction)
+    N = z.shape[0]
+    ref = oracle.definition(z, y, scale=1.0 / N if reduction == "mean" else 1.0)
+    if reduction == "none":
+        go = torch.linspace(0.5, 2.0, N, device=dev)
+        go[::3] = 1.0
+        loss.backward(go)
+        expect = ref["grad"] * go.cpu().numpy()[:, None]
+        np.testing.assert_array_equal(loss.detach().cpu().numpy(), ref["loss"])
+    else:
+        (loss * 3.0).backward()
+        expect = ref["grad"] * np.float32(3.0)
+        tot = ref["loss"].astype(np.float64).sum() / (N if reduction == "mean" else 1)
+        assert abs(loss.item() - tot) <= 1e-6 * max(1.0, abs(tot))
+    assert bits_equal(zt.grad.cpu().numpy(), expect.astype(np.float32))
+
+
+def test_c_abi_direct(ext, dev):
+    z, y = data.make("cfg2", N=256, seed=6)
+    zt, yt = to_dev(dev, z, y)
+    out = fwloss_capi.forward_backward(zt, yt)
+    torch.cuda.synchronize()
+    got = {k: (v.cpu().numpy() if v.dim() else float(v.cpu())) for k, v in out.items()}
+    assert_parity(got, oracle.definition(z, y), z)
