@@ -31,11 +31,27 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "fwloss.h"
 
 namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer resources (GFX9 layout): the hardware range check drops stores and zero-fills loads
+// past `bytes`, so every lane can issue the same unconditional instruction.  Memory instructions
+// under lane-dependent branches would make the compiler's wait counting fall back to draining all
+// outstanding stores at the top of each row.
+constexpr int kRsrcFlags = 0x00020000;
+constexpr int kNonTemporal = 2;   // cache-policy bits of the buffer instructions: nt
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kRsrcFlags);
+}
 
 constexpr int kWave = 64;
 constexpr int kWavesPerBlock = 4;
@@ -127,18 +143,34 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
   return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
 }
 
-// partner value of lane ^ M
+// partner value of lane ^ M, without LDS: DPP inside rows of 16 lanes, the gfx950 permlane swaps
+// across rows (v_permlane16_swap / v_permlane32_swap with both operands x return, per lane, the
+// value of the other row / half in r[1] for the lower and r[0] for the upper one)
 template <int M>
-__device__ __forceinline__ float xor_lane(float v) {
+__device__ __forceinline__ float xor_lane(float v, int lane) {
   const int x = __float_as_int(v);
   if constexpr (M == 1) return __int_as_float(dpp_mov<kQuadXor1>(x));
   else if constexpr (M == 2) return __int_as_float(dpp_mov<kQuadXor2>(x));
-  else if constexpr (M == 8) return __int_as_float(dpp_mov<kRowRor8>(x));
-  else if constexpr (M == 4 || M == 16) return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x1F | (M << 10)));
-  else {
+  else if constexpr (M == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, false);   // row_shl:4
+    const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);   // row_shr:4
+    return __int_as_float((lane & 4) ? dn : up);
+  } else if constexpr (M == 8) return __int_as_float(dpp_mov<kRowRor8>(x));
+  else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return __int_as_float((lane & 16) ? r[0] : r[1]);
+  } else {
     static_assert(M == 32, "xor distance");
-    return __int_as_float(__builtin_amdgcn_ds_bpermute((lane_id() ^ 32) << 2, x));
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return __int_as_float((lane & 32) ? r[0] : r[1]);
   }
+}
+
+// per-lane select with a wavefront-constant lane mask held in SGPRs (one v_cndmask)
+__device__ __forceinline__ float select_lanes(uint64_t mask, float if_set, float if_clear) {
+  float r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(if_clear), "v"(if_set), "s"(mask));
+  return r;
 }
 
 // maximum over the wavefront, returned in every lane (wavefront-uniform)
@@ -172,47 +204,52 @@ __device__ __forceinline__ double wave_max_f64(double v) {
   return fmax(fmax(readlane_f64(v, 0), readlane_f64(v, 16)), fmax(readlane_f64(v, 32), readlane_f64(v, 48)));
 }
 
-// inclusive prefix sum over the 64 lanes (row_shr within rows of 16, then row_bcast across rows)
-__device__ __forceinline__ double wave_scan_f64(double v) {
+// one compare-exchange step of a bitonic network sorting groups of K lanes (descending where
+// lane & K == 0); the lanes keeping the maximum form a constant mask
+constexpr uint64_t keep_max_mask(int K, int J) {
+  uint64_t m = 0;
+  for (int i = 0; i < 64; ++i)
+    if (((i & J) == 0) == ((i & K) == 0)) m |= 1ull << i;
+  return m;
+}
+
+template <int K, int J>
+__device__ __forceinline__ float bitonic_step(float v, int lane) {
+  const float p = xor_lane<J>(v, lane);
+  return select_lanes(keep_max_mask(K, J), fmaxf(v, p), fminf(v, p));
+}
+
+template <int K>
+__device__ __forceinline__ float bitonic_merge(float v, int lane) {
+  if constexpr (K >= 64) v = bitonic_step<K, 32>(v, lane);
+  if constexpr (K >= 32) v = bitonic_step<K, 16>(v, lane);
+  if constexpr (K >= 16) v = bitonic_step<K, 8>(v, lane);
+  if constexpr (K >= 8) v = bitonic_step<K, 4>(v, lane);
+  if constexpr (K >= 4) v = bitonic_step<K, 2>(v, lane);
+  return bitonic_step<K, 1>(v, lane);
+}
+
+// sort lanes [0, T) descending (T = 16, 32 or 64)
+template <int T>
+__device__ __forceinline__ float sort_desc(float v, int lane) {
+  v = bitonic_merge<2>(v, lane);
+  v = bitonic_merge<4>(v, lane);
+  v = bitonic_merge<8>(v, lane);
+  v = bitonic_merge<16>(v, lane);
+  if constexpr (T >= 32) v = bitonic_merge<32>(v, lane);
+  if constexpr (T >= 64) v = bitonic_merge<64>(v, lane);
+  return v;
+}
+
+// inclusive prefix sum over lanes [0, T)
+template <int T>
+__device__ __forceinline__ double scan_f64(double v) {
   v += dpp_or0_f64<0x111, 0xF>(v);          // row_shr:1
   v += dpp_or0_f64<0x112, 0xF>(v);          // row_shr:2
   v += dpp_or0_f64<0x114, 0xF>(v);          // row_shr:4
   v += dpp_or0_f64<0x118, 0xF>(v);          // row_shr:8
-  v += dpp_or0_f64<kRowBcast15, 0xA>(v);    // rows 1, 3 += last lane of rows 0, 2
-  v += dpp_or0_f64<kRowBcast31, 0xC>(v);    // rows 2, 3 += lane 31
-  return v;
-}
-
-// one compare-exchange step of a bitonic network sorting the wavefront in descending order
-template <int K, int J>
-__device__ __forceinline__ float bitonic_step(float v, int lane) {
-  const float p = xor_lane<J>(v);
-  const bool keep_max = ((lane & J) == 0) == ((lane & K) == 0);
-  return keep_max ? fmaxf(v, p) : fminf(v, p);
-}
-
-__device__ __forceinline__ float sort_desc64(float v, int lane) {
-  v = bitonic_step<2, 1>(v, lane);
-  v = bitonic_step<4, 2>(v, lane);
-  v = bitonic_step<4, 1>(v, lane);
-  v = bitonic_step<8, 4>(v, lane);
-  v = bitonic_step<8, 2>(v, lane);
-  v = bitonic_step<8, 1>(v, lane);
-  v = bitonic_step<16, 8>(v, lane);
-  v = bitonic_step<16, 4>(v, lane);
-  v = bitonic_step<16, 2>(v, lane);
-  v = bitonic_step<16, 1>(v, lane);
-  v = bitonic_step<32, 16>(v, lane);
-  v = bitonic_step<32, 8>(v, lane);
-  v = bitonic_step<32, 4>(v, lane);
-  v = bitonic_step<32, 2>(v, lane);
-  v = bitonic_step<32, 1>(v, lane);
-  v = bitonic_step<64, 32>(v, lane);
-  v = bitonic_step<64, 16>(v, lane);
-  v = bitonic_step<64, 8>(v, lane);
-  v = bitonic_step<64, 4>(v, lane);
-  v = bitonic_step<64, 2>(v, lane);
-  v = bitonic_step<64, 1>(v, lane);
+  if constexpr (T >= 32) v += dpp_or0_f64<kRowBcast15, 0xA>(v);   // rows 1, 3 += last lane of 0, 2
+  if constexpr (T >= 64) v += dpp_or0_f64<kRowBcast31, 0xC>(v);   // rows 2, 3 += lane 31
   return v;
 }
 
@@ -257,32 +294,45 @@ __device__ __forceinline__ double clamp_below_max(double tau, float m) {
   return (tau >= (double)m && isfinite(m)) ? prev_f64((double)m) : tau;
 }
 
-// tau of a candidate set held one value per lane in lanes [0, n), 1 <= n <= 64:
+// tau of a candidate set held one value per lane in lanes [0, n), 1 <= n <= T <= 64:
 // sort descending, S_k = fp64 prefix sums, tau = max_k (S_k - 1)/k (reference_impl.py:17-21)
-__device__ __forceinline__ double select_small(float c, int n, int lane) {
+template <int T>
+__device__ __forceinline__ double select_tier(float c, int n, int lane) {
   float v = lane < n ? c + 0.0f : -INFINITY;   // + 0.0f: -0.0 -> +0.0 before min/max
-  v = sort_desc64(v, lane);
-  const double S = wave_scan_f64(lane < n ? (double)v : 0.0);
+  v = sort_desc<T>(v, lane);
+  const double S = scan_f64<T>(lane < n ? (double)v : 0.0);
   const double f = (S - 1.0) / (double)(lane + 1);
   return wave_max_f64(lane < n ? f : -INFINITY);
 }
 
+__device__ __forceinline__ double select_small(float c, int n, int lane) {
+  if (n <= 16) return select_tier<16>(c, n, lane);
+  if (n <= 32) return select_tier<32>(c, n, lane);
+  return select_tier<64>(c, n, lane);
+}
+
 // ------------------------------------------------------------------------------------------------
 // mean of the per-row losses: block partial sums, the last block reduces them (fixed order)
+
+// Wait until this thread's earlier vector memory operations have completed (stores acknowledged).
+// Unlike a device-scope fence this does not write back the L2 cache.
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ void mean_epilogue(double bsum, const Outs& o) {
   __shared__ int s_last;
   __shared__ double s_red[kBlock];
   if (o.mean == nullptr) return;
   if (threadIdx.x == 0) {
-    o.partials[blockIdx.x] = bsum;
-    __threadfence();
-    const unsigned t = atomicAdd(o.ticket, 1u);
+    // The partial is an agent-scope atomic store (coherent across the XCDs' L2 caches); once it
+    // has completed, the ticket increment publishes it.  A device-scope fence here would write
+    // back the whole L2 of the XCD at the end of every block.
+    __hip_atomic_store(o.partials + blockIdx.x, bsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vmem();
+    const unsigned t = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (t == gridDim.x - 1);
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
   double acc = 0.0;
   for (unsigned i = threadIdx.x; i < gridDim.x; i += kBlock)
     acc += __hip_atomic_load(o.partials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -302,17 +352,12 @@ __device__ void mean_epilogue(double bsum, const Outs& o) {
 // fwl_wave_rows: one wavefront per row, C <= 64 * E (E elements per lane)
 
 template <int NV, bool V4>
-__device__ __forceinline__ void load_row(const float* __restrict__ z, int64_t r, int C, int lane,
-                                         float* x) {
-  const float* row = z + r * (int64_t)C;
+__device__ __forceinline__ void load_row(rsrc_t row, int lane, float* x) {
+  // all lanes load unconditionally; offsets past the row (or a zero-size resource: no row) read 0
   if constexpr (V4) {
-    const int nvec = C >> 2;
-    const v4f* row4 = reinterpret_cast<const v4f*>(row);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int q = lane + kWave * k;
-      v4f v = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-      if (q < nvec) v = __builtin_nontemporal_load(row4 + q);
+      const v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(row, 16 * (lane + kWave * k), 0, kNonTemporal));
       x[4 * k + 0] = v.x;
       x[4 * k + 1] = v.y;
       x[4 * k + 2] = v.z;
@@ -320,10 +365,28 @@ __device__ __forceinline__ void load_row(const float* __restrict__ z, int64_t r,
     }
   } else {
 #pragma unroll
+    for (int k = 0; k < NV; ++k)
+      x[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(row, 4 * (lane + kWave * k), 0, kNonTemporal));
+  }
+}
+
+// set the register slots past the row end to -inf (only the last partial slots need it)
+template <int NV, bool V4>
+__device__ __forceinline__ void mask_tail(float* x, int C, int lane) {
+  if constexpr (V4) {
+    const int nvec = C >> 2;
+#pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int j = lane + kWave * k;
-      x[k] = j < C ? __builtin_nontemporal_load(row + j) : -INFINITY;
+      if (kWave * (k + 1) > nvec) {
+        const bool ok = lane + kWave * k < nvec;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[4 * k + e] = ok ? x[4 * k + e] : -INFINITY;
+      }
     }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (kWave * (k + 1) > C) x[k] = lane + kWave * k < C ? x[k] : -INFINITY;
   }
 }
 
@@ -334,29 +397,81 @@ __device__ __forceinline__ int slot_index(int i, int lane) {
   else return lane + kWave * i;
 }
 
-// sum (fp64) and count of the register-row entries > thr, wavefront totals
-template <int E>
-__device__ __forceinline__ void reg_sum_count(const float* x, float thr, double& s, int& c) {
+// sum/count over the first n entries of one wavefront's list, entries > thr
+__device__ __forceinline__ void list_sum_count(const float* bv, int n, float thr, int lane, double& s,
+                                               int& c) {
   double acc = 0.0;
   int cnt = 0;
-#pragma unroll
-  for (int i = 0; i < E; ++i) {
-    const bool p = x[i] > thr;
-    acc += p ? (double)x[i] : 0.0;
-    cnt += __popcll(ballot(p));
+  for (int p0 = 0; p0 < n; p0 += kWave) {
+    const int p = p0 + lane;
+    const float v = p < n ? bv[p] : -INFINITY;
+    const bool k = v > thr;
+    acc += k ? (double)v : 0.0;
+    cnt += __popcll(ballot(k));
   }
   s = wave_sum_f64(acc);
   c = cnt;
 }
 
-template <int MODE, int NV, bool V4>
-__device__ __forceinline__ float process_row(const float* __restrict__ z,
-                                             const int64_t* __restrict__ tgt, int64_t r, int C,
-                                             int lane, const float* x, float* cb, const Outs& o) {
+// element j of the register row (j wavefront-uniform, 0 <= j < C)
+template <int NV, bool V4>
+__device__ __forceinline__ float element_at(const float* x, int j) {
   constexpr int E = V4 ? 4 * NV : NV;
-  const int64_t y64 = tgt[r];
+  int slot, owner;
+  if constexpr (V4) {
+    slot = 4 * ((j >> 2) >> 6) + (j & 3);
+    owner = (j >> 2) & 63;
+  } else {
+    slot = j >> 6;
+    owner = j & 63;
+  }
+  // read the owner lane of every slot and pick with scalar selects (a vector select chain would be
+  // turned back into a dynamically indexed array, which lives in scratch memory)
+  int v = __builtin_amdgcn_readlane(__float_as_int(x[0]), owner);
+#pragma unroll
+  for (int i = 1; i < E; ++i) {
+    const int w = __builtin_amdgcn_readlane(__float_as_int(x[i]), owner);
+    v = i == slot ? w : v;
+  }
+  return __int_as_float(v);
+}
+
+// exclusive prefix sum of v over the wavefront; `total` receives the sum of all lanes
+__device__ __forceinline__ int wave_excl_scan_i32(int v, int& total) {
+  int s = v;
+  s += dpp_or0<0x111, 0xF>(s);          // row_shr:1
+  s += dpp_or0<0x112, 0xF>(s);          // row_shr:2
+  s += dpp_or0<0x114, 0xF>(s);          // row_shr:4
+  s += dpp_or0<0x118, 0xF>(s);          // row_shr:8
+  s += dpp_or0<kRowBcast15, 0xA>(s);
+  s += dpp_or0<kRowBcast31, 0xC>(s);
+  total = __builtin_amdgcn_readlane(s, 63);
+  return s - v;
+}
+
+struct RowResult {
+  float H;
+  float loss;
+  int kappa;
+};
+
+// LDS candidate list of one wavefront: kMaxWaveC entries, then one spare slot per lane (the target
+// of the branch-free writes of non-candidates); the candidate-list mode keeps the indices alongside
+constexpr int kListCap = kMaxWaveC;
+constexpr int kListFloats = kListCap + kWave;
+constexpr int kRowsPerWave = kWave;   // rows of one wavefront per launch (labels/results: one lane each)
+
+// One row: x holds it (E values per lane).  Once its candidates are in the LDS list, the loads of
+// the next row (resource `next`, zero-size if there is none) are issued into x, so they are in
+// flight during the selection and the stores of this row; no second row buffer is needed.
+template <int MODE, int NV, bool V4>
+__device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t y64, int C, int lane,
+                                                 float* x, float* cl, int* ci_lds, const Outs& o) {
+  constexpr int E = V4 ? 4 * NV : NV;
+  static_assert(E <= 32, "one mask bit per register slot");
   const bool yok = y64 >= 0 && y64 < C;
   const int yr = yok ? (int)y64 : -1;
+  mask_tail<NV, V4>(x, C, lane);
 
   // row maximum and the first lower bound max - 1 (rounded down: every support entry passes)
   float lm = x[0];
@@ -365,39 +480,46 @@ __device__ __forceinline__ float process_row(const float* __restrict__ z,
   const float m = wave_max_f32(lm);
   const float t0 = bound_below_max(m);
 
-  // compact the candidates z > t0 into LDS (first 64 only; n counts all of them)
-  int n = 0;
+  // candidates z > t0: one bit per register slot, then lane-major positions in the LDS list
+  unsigned cm = 0;
 #pragma unroll
-  for (int i = 0; i < E; ++i) {
-    const bool p = x[i] > t0;
-    const uint64_t b = ballot(p);
-    if (b) {
-      if (p) {
-        const int pos = n + rank_in(b);
-        if (pos < kWave) cb[pos] = x[i];
-      }
-      n += __popcll(b);
+  for (int i = 0; i < E; ++i) cm |= (unsigned)(x[i] > t0) << i;
+  int n;
+  const int base = wave_excl_scan_i32(__popc(cm), n);
+  {
+    int pos = base;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int bit = (cm >> i) & 1;
+      const int at = bit ? pos : kListCap + lane;
+      cl[at] = x[i];
+      if constexpr (MODE == kCand) ci_lds[at] = slot_index<V4>(i, lane);
+      pos += bit;
     }
   }
+  const float zy = yok ? element_at<NV, V4>(x, yr) : NAN;
   __builtin_amdgcn_wave_barrier();
+  load_row<NV, V4>(next, lane, x);
 
   double tau = NAN;
   int kappa = 0;
+  uint64_t support = 0;   // n <= 64: bit p set <=> list entry p is in the support
   if (n > 0 && n <= kWave) {
-    const float c = lane < n ? cb[lane] : -INFINITY;
+    const float c = lane < n ? cl[lane] : -INFINITY;
     tau = clamp_below_max(select_small(c, n, lane), m);
-    kappa = __popcll(ballot(lane < n && c > rd32(tau)));
+    support = ballot(lane < n && c > rd32(tau));
+    kappa = __popcll(support);
   } else if (n > kWave) {
-    // fixed-point iteration t <- H({z > t}) from t = max - 1 (each iterate is <= tau; the set
-    // shrinks every step until it is {z > tau})
+    // fixed-point iteration t <- H({z > t}) over the list, from t = max - 1 (each iterate is
+    // <= tau; the set shrinks every step until it is {z > tau})
     double t = (double)t0, s;
     int c;
-    reg_sum_count<E>(x, t0, s, c);
-    for (int it = 0; it <= C + 1; ++it) {
+    list_sum_count(cl, n, t0, lane, s, c);
+    for (int it = 0; it <= n + 1; ++it) {
       const double tn = (s - 1.0) / (double)c;
       double s2;
       int c2;
-      reg_sum_count<E>(x, rd32(tn), s2, c2);
+      list_sum_count(cl, n, rd32(tn), lane, s2, c2);
       if (c2 == c || !(tn > t)) {
         tau = tn;
         kappa = c2;
@@ -411,125 +533,179 @@ __device__ __forceinline__ float process_row(const float* __restrict__ z,
     if (tc != tau) {
       double s3;
       tau = tc;
-      reg_sum_count<E>(x, rd32(tau), s3, kappa);
+      list_sum_count(cl, n, rd32(tau), lane, s3, kappa);
+    }
+  }
+  const float Hf = rd32(tau);
+
+  // support bit of every register slot of this lane (supports are subsets of the candidates)
+  unsigned sm = 0;
+  if (n <= kWave) {
+    unsigned sb = base < kWave ? (unsigned)(support >> base) : 0u;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const unsigned bit = (cm >> i) & 1u;
+      sm |= (bit & sb) << i;
+      sb >>= bit;
+    }
+  } else {
+    int pos = base;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      if ((cm >> i) & 1u) {
+        sm |= (unsigned)(cl[pos] > Hf) << i;
+        ++pos;
+      }
     }
   }
   __builtin_amdgcn_wave_barrier();
 
-  const float Hf = rd32(tau);
   const float inv = (float)(o.scale / (double)kappa);
-  float* const row_out_g = o.grad + r * (int64_t)C;
-  uint8_t* const row_out_m = o.mask + r * (int64_t)C;
-
-  if constexpr (MODE == kGrad || MODE == kMask) {
+  if constexpr (MODE == kGrad) {
+    const rsrc_t out = make_rsrc(o.grad + r * (int64_t)C, 4u * (uint32_t)C);
     if constexpr (V4) {
-      const int nvec = C >> 2;
       const int qy = yr >> 2, ky = yr >= 0 ? qy >> 6 : -1, ly = qy & 63, ey = yr & 3;
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
-        const int q = lane + kWave * k;
-        if (q < nvec) {
-          if constexpr (MODE == kGrad) {
-            v4f g;
-            g.x = x[4 * k + 0] > Hf ? inv : 0.0f;
-            g.y = x[4 * k + 1] > Hf ? inv : 0.0f;
-            g.z = x[4 * k + 2] > Hf ? inv : 0.0f;
-            g.w = x[4 * k + 3] > Hf ? inv : 0.0f;
-            if (k == ky && lane == ly) {
-              if (ey == 0) g.x -= o.scale_f;
-              else if (ey == 1) g.y -= o.scale_f;
-              else if (ey == 2) g.z -= o.scale_f;
-              else g.w -= o.scale_f;
-            }
-            __builtin_nontemporal_store(g, reinterpret_cast<v4f*>(row_out_g) + q);
-          } else {
-            const unsigned mk = (unsigned)(x[4 * k + 0] > Hf) | ((unsigned)(x[4 * k + 1] > Hf) << 8) |
-                                ((unsigned)(x[4 * k + 2] > Hf) << 16) | ((unsigned)(x[4 * k + 3] > Hf) << 24);
-            __builtin_nontemporal_store(mk, reinterpret_cast<unsigned*>(row_out_m) + q);
-          }
+        const unsigned b4 = (sm >> (4 * k)) & 0xFu;
+        v4f g;
+        g.x = (b4 & 1u) ? inv : 0.0f;
+        g.y = (b4 & 2u) ? inv : 0.0f;
+        g.z = (b4 & 4u) ? inv : 0.0f;
+        g.w = (b4 & 8u) ? inv : 0.0f;
+        if (k == ky && lane == ly) {
+          if (ey == 0) g.x -= o.scale_f;
+          else if (ey == 1) g.y -= o.scale_f;
+          else if (ey == 2) g.z -= o.scale_f;
+          else g.w -= o.scale_f;
         }
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, g), out, 16 * (lane + kWave * k), 0, kNonTemporal);
       }
     } else {
       const int ky = yr >= 0 ? yr >> 6 : -1, ly = yr & 63;
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
-        const int j = lane + kWave * k;
-        if (j < C) {
-          if constexpr (MODE == kGrad) {
-            float g = x[k] > Hf ? inv : 0.0f;
-            if (k == ky && lane == ly) g -= o.scale_f;
-            __builtin_nontemporal_store(g, row_out_g + j);
-          } else {
-            row_out_m[j] = (uint8_t)(x[k] > Hf);
-          }
-        }
+        float g = ((sm >> k) & 1u) ? inv : 0.0f;
+        if (k == ky && lane == ly) g -= o.scale_f;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(g), out, 4 * (lane + kWave * k), 0, kNonTemporal);
       }
     }
-  } else {
-    // support list in index order (ballot ranks keep lanes in order within a slot)
-    float* const cv = o.cval + r * (int64_t)C;
-    int32_t* const ci = o.cidx + r * (int64_t)C;
-    int base = 0;
+  } else if constexpr (MODE == kMask) {
+    const rsrc_t out = make_rsrc(o.mask + r * (int64_t)C, (uint32_t)C);
     if constexpr (V4) {
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
-        const bool p0 = x[4 * k + 0] > Hf, p1 = x[4 * k + 1] > Hf, p2 = x[4 * k + 2] > Hf,
-                   p3 = x[4 * k + 3] > Hf;
-        const uint64_t b0 = ballot(p0), b1 = ballot(p1), b2 = ballot(p2), b3 = ballot(p3);
-        int pos = base + rank_in(b0) + rank_in(b1) + rank_in(b2) + rank_in(b3);
-        const int j0 = 4 * (lane + kWave * k);
-        if (p0) { cv[pos] = x[4 * k + 0]; ci[pos] = j0 + 0; ++pos; }
-        if (p1) { cv[pos] = x[4 * k + 1]; ci[pos] = j0 + 1; ++pos; }
-        if (p2) { cv[pos] = x[4 * k + 2]; ci[pos] = j0 + 2; ++pos; }
-        if (p3) { cv[pos] = x[4 * k + 3]; ci[pos] = j0 + 3; }
-        base += __popcll(b0) + __popcll(b1) + __popcll(b2) + __popcll(b3);
+        const unsigned b4 = (sm >> (4 * k)) & 0xFu;
+        const unsigned mk = (b4 & 1u) | ((b4 & 2u) << 7) | ((b4 & 4u) << 14) | ((b4 & 8u) << 21);
+        __builtin_amdgcn_raw_buffer_store_b32(mk, out, 4 * (lane + kWave * k), 0, kNonTemporal);
       }
     } else {
 #pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        const bool p = x[k] > Hf;
-        const uint64_t b = ballot(p);
-        if (p) {
-          const int pos = base + rank_in(b);
-          cv[pos] = x[k];
-          ci[pos] = lane + kWave * k;
-        }
-        base += __popcll(b);
-      }
+      for (int k = 0; k < NV; ++k)
+        __builtin_amdgcn_raw_buffer_store_b8((unsigned char)((sm >> k) & 1u), out, lane + kWave * k, 0,
+                                             kNonTemporal);
+    }
+  } else {
+    // the support list, in the (deterministic) order of the candidate list; lanes without an
+    // entry store past the end of the resource (dropped)
+    const rsrc_t outv = make_rsrc(o.cval + r * (int64_t)C, 4u * (uint32_t)C);
+    const rsrc_t outi = make_rsrc(o.cidx + r * (int64_t)C, 4u * (uint32_t)C);
+    int out = 0;
+    for (int p0 = 0; p0 < n; p0 += kWave) {
+      const int p = p0 + lane;
+      const float v = p < n ? cl[p] : -INFINITY;
+      const bool k = v > Hf;
+      const uint64_t b = ballot(k);
+      const uint32_t at = k ? 4u * (uint32_t)(out + rank_in(b)) : 4u * (uint32_t)C;
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), outv, at, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32((unsigned)(p < n ? ci_lds[p] : 0), outi, at, 0, 0);
+      out += __popcll(b);
     }
   }
+  __builtin_amdgcn_wave_barrier();
 
-  const float zy = yok ? z[r * (int64_t)C + yr] : NAN;
-  const float loss = (float)((1.0 - (double)zy) + tau);
-  if (lane == 0) {
-    if (o.H) o.H[r] = Hf;
-    if (o.loss) o.loss[r] = loss;
-    if (o.kappa) o.kappa[r] = kappa;
-    if constexpr (MODE == kCand) o.ccnt[r] = kappa;
-  }
-  return loss;
+  RowResult res;
+  res.H = Hf;
+  res.loss = (float)((1.0 - (double)zy) + tau);
+  res.kappa = kappa;
+  return res;
 }
 
+// Stores to a zero-size resource (dropped by the range check, no memory traffic), issued after the
+// first row's loads so that the wait counts at the top of the row loop are the same on entry as on
+// every later iteration (4 row loads followed by the row's stores); with a different mix on entry
+// the compiler waits for every outstanding store at the top of each row.
+template <int MODE, int NV, bool V4>
+__device__ __forceinline__ void mirror_row_stores(int lane) {
+  const rsrc_t none = make_rsrc(nullptr, 0u);
+  if constexpr (MODE == kGrad) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      if constexpr (V4)
+        __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, none, 16 * (lane + kWave * k), 0, kNonTemporal);
+      else
+        __builtin_amdgcn_raw_buffer_store_b32(0u, none, 4 * (lane + kWave * k), 0, kNonTemporal);
+    }
+  } else if constexpr (MODE == kMask) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      if constexpr (V4) __builtin_amdgcn_raw_buffer_store_b32(0u, none, 4 * (lane + kWave * k), 0, kNonTemporal);
+      else __builtin_amdgcn_raw_buffer_store_b8((unsigned char)0, none, lane + kWave * k, 0, kNonTemporal);
+    }
+  }
+}
+
+// A wavefront handles rows w + k*stride, k < nrows <= 64.  Their labels arrive in one gather load
+// before the first row, and their H, loss and kappa stay in registers (row k in lane k) until the
+// last row, so the only memory instructions inside the row loop are the row loads and stores.
 template <int MODE, int NV, bool V4>
 __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const float* __restrict__ z,
                                                         const int64_t* __restrict__ tgt, int64_t N,
                                                         int C, Outs o) {
   constexpr int E = V4 ? 4 * NV : NV;
-  __shared__ float s_cand[kWavesPerBlock][kWave];
+  constexpr int kIdx = MODE == kCand ? kListFloats : 1;
+  __shared__ float s_list[kWavesPerBlock][kListFloats];
+  __shared__ int s_idx[kWavesPerBlock][kIdx];
   __shared__ double s_wsum[kWavesPerBlock];
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+  const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;   // this wavefront's rows: w + k*stride
+  const int nrows = w < N ? (int)((N - 1 - w) / stride + 1) : 0;   // <= kRowsPerWave (host grid)
+  const uint32_t row_bytes = 4u * (uint32_t)C;
+  auto row_rsrc = [&](int k) {
+    return k < nrows ? make_rsrc(z + (w + (int64_t)k * stride) * C, row_bytes) : make_rsrc(z, 0u);
+  };
+  const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
+  float my_H = 0.0f, my_loss = 0.0f;
+  int my_kappa = 0;
   double lsum = 0.0;
-  float x[E], nx[E];
-  int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  if (r < N) load_row<NV, V4>(z, r, C, lane, x);
-  for (; r < N; r += stride) {
-    const int64_t rn = r + stride;
-    if (rn < N) load_row<NV, V4>(z, rn, C, lane, nx);   // next row in flight while this one runs
-    lsum += (double)process_row<MODE, NV, V4>(z, tgt, r, C, lane, x, s_cand[wid], o);
-#pragma unroll
-    for (int i = 0; i < E; ++i) x[i] = nx[i];
+  float x[E];
+  if (nrows > 0) {
+    load_row<NV, V4>(row_rsrc(0), lane, x);
+    __builtin_amdgcn_sched_barrier(0);   // keep the mirror stores after the loads
+    mirror_row_stores<MODE, NV, V4>(lane);
+    __builtin_amdgcn_sched_barrier(0);
+    int k = 0;
+    do {
+      const int64_t y = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
+      const RowResult res = process_row<MODE, NV, V4>(w + (int64_t)k * stride, row_rsrc(k + 1), y, C, lane, x,
+                                                      s_list[wid], s_idx[wid], o);
+      lsum += (double)res.loss;
+      if (lane == k) {
+        my_H = res.H;
+        my_loss = res.loss;
+        my_kappa = res.kappa;
+      }
+    } while (++k < nrows);
+  }
+  if (lane < nrows) {
+    const int64_t r = w + (int64_t)lane * stride;
+    if (o.H) o.H[r] = my_H;
+    if (o.loss) o.loss[r] = my_loss;
+    if (o.kappa) o.kappa[r] = my_kappa;
+    if constexpr (MODE == kCand) o.ccnt[r] = my_kappa;
   }
   if (lane == 0) s_wsum[wid] = lsum;
   __syncthreads();
@@ -559,22 +735,6 @@ template <int MODE>
 __device__ __forceinline__ void write_zero(const Outs& o, int64_t r, int C, int j) {
   if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + j] = 0.0f;
   else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + j] = 0;
-}
-
-// sum/count over the first n entries of one wavefront's list, entries > thr
-__device__ __forceinline__ void list_sum_count(const float* bv, int n, float thr, int lane, double& s,
-                                               int& c) {
-  double acc = 0.0;
-  int cnt = 0;
-  for (int p0 = 0; p0 < n; p0 += kWave) {
-    const int p = p0 + lane;
-    const float v = p < n ? bv[p] : -INFINITY;
-    const bool k = v > thr;
-    acc += k ? (double)v : 0.0;
-    cnt += __popcll(ballot(k));
-  }
-  s = wave_sum_f64(acc);
-  c = cnt;
 }
 
 // Raise the wavefront's lower bound t with a few fixed-point steps on its list, then drop the
@@ -796,8 +956,8 @@ __device__ void generic_row(const float* __restrict__ row, int64_t r, int C, int
       block_sum_count(row, C, rd32(tau), sh, lane, wid, s3, kappa);
     }
   }
-  // outputs written while streaming must land before these rewrites
-  __threadfence();
+  // outputs written while streaming must land before these rewrites (same block, so the same L2)
+  wait_vmem();
   __syncthreads();
   const float Hf = rd32(tau);
   const float inv = (float)(o.scale / (double)kappa);
@@ -1067,8 +1227,9 @@ __global__ __launch_bounds__(kBlock) void fwl_cand_to_grad(
     } else {
       for (int j = threadIdx.x; j < C; j += kBlock) __builtin_nontemporal_store(0.0f, gr + j);
     }
-    // the zeros must land before the scattered values below (same addresses, other threads)
-    __threadfence();
+    // the zeros must land before the scattered values below (same addresses, other threads of
+    // this block, hence the same L2)
+    wait_vmem();
     __syncthreads();
     const int64_t y64 = tgt[r];
     const int yr = (y64 >= 0 && y64 < C) ? (int)y64 : -1;
@@ -1125,13 +1286,54 @@ int blocks_wave(int64_t N) {
 }
 int blocks_row(int64_t N) { return (int)(N < kMaxBlocksRow ? (N > 0 ? N : 1) : kMaxBlocksRow); }
 
+// Blocks of `kernel` that fit on the current device at once (cached per device and kernel).
+int resident_blocks(const void* kernel) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, kernel);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  const int nb = per_cu * cus;
+  cache.emplace(key, nb);
+  return nb;
+}
+
+// Persistent grid: at most one resident set of blocks (and at most `cap`), with the rows spread
+// so that every unit of work (wavefront or block) gets the same number of rows, +-1 at the end.
+int persistent_grid(int64_t units, int units_per_block, int resident, int cap) {
+  int64_t max_blocks = resident > 0 ? (resident < cap ? resident : cap) : cap;
+  const int64_t max_units = max_blocks * units_per_block;
+  const int64_t per_unit = (units + max_units - 1) / max_units;
+  const int64_t used = (units + per_unit - 1) / per_unit;
+  const int64_t blocks = (used + units_per_block - 1) / units_per_block;
+  return (int)(blocks > 0 ? blocks : 1);
+}
+
+// Grid of fwl_wave_rows: one resident set of blocks when that leaves each wavefront at most
+// kRowsPerWave rows, more blocks (queued) otherwise.
+int wave_grid(int64_t N, int resident) {
+  const int64_t min_blocks = (N + (int64_t)kWavesPerBlock * kRowsPerWave - 1) / ((int64_t)kWavesPerBlock * kRowsPerWave);
+  const int cap = (int)(min_blocks > kMaxBlocksWave ? min_blocks : kMaxBlocksWave);
+  const int64_t g = persistent_grid(N, kWavesPerBlock, resident, cap);
+  return (int)(g > min_blocks ? g : min_blocks);
+}
+
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 int launch_status() { return hipGetLastError() == hipSuccess ? FWL_OK : FWL_ERR_LAUNCH; }
 
 template <int MODE, int NV, bool V4>
 void launch_wave(const float* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
-  hipLaunchKernelGGL((fwl_wave_rows<MODE, NV, V4>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, y, N, C, o);
+  const void* k = reinterpret_cast<const void*>(&fwl_wave_rows<MODE, NV, V4>);
+  const int grid = wave_grid(N, resident_blocks(k));
+  hipLaunchKernelGGL((fwl_wave_rows<MODE, NV, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
 }
 
 template <int MODE>
@@ -1150,13 +1352,18 @@ void dispatch_wave(const float* z, const int64_t* y, int64_t N, int C, bool v4, 
   }
 }
 
+template <int MODE, bool V4>
+void launch_block(const float* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+  const void* k = reinterpret_cast<const void*>(&fwl_block_rows<MODE, V4>);
+  const int grid = persistent_grid(N, 1, resident_blocks(k), kMaxBlocksRow);
+  hipLaunchKernelGGL((fwl_block_rows<MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+}
+
 template <int MODE>
 void dispatch_block(const float* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
                     hipStream_t s) {
-  if (v4)
-    hipLaunchKernelGGL((fwl_block_rows<MODE, true>), dim3(blocks_row(N)), dim3(kBlock), 0, s, z, y, N, C, o);
-  else
-    hipLaunchKernelGGL((fwl_block_rows<MODE, false>), dim3(blocks_row(N)), dim3(kBlock), 0, s, z, y, N, C, o);
+  if (v4) launch_block<MODE, true>(z, y, N, C, o, s);
+  else launch_block<MODE, false>(z, y, N, C, o, s);
 }
 
 bool bad_shape(int64_t N, int64_t C) { return N < 0 || C < 1 || C >= (int64_t)INT32_MAX - 64; }
@@ -1212,7 +1419,10 @@ const char* fwl_status_string(int status) {
 
 size_t fwl_workspace_bytes(int64_t N, int64_t C) {
   (void)C;
-  const int64_t b = blocks_wave(N) > blocks_row(N) ? blocks_wave(N) : blocks_row(N);
+  // one fp64 partial per block of the largest grid any forward launches for N rows
+  const int64_t wave_max = (N + (int64_t)kWavesPerBlock * kRowsPerWave - 1) / ((int64_t)kWavesPerBlock * kRowsPerWave);
+  int64_t b = kMaxBlocksRow > kMaxBlocksWave ? kMaxBlocksRow : kMaxBlocksWave;
+  if (wave_max > b) b = wave_max;
   return kWsHeader + sizeof(double) * (size_t)b;
 }
 

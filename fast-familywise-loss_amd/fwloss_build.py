@@ -27,6 +27,7 @@ HIP_FLAGS = [
     # no packed-FP32 instructions (build notes)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
+    "-flax-vector-conversions=none",   # no implicit reinterpretation between vector types
 ]
 
 
