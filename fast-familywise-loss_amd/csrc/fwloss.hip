@@ -1316,12 +1316,35 @@ int persistent_grid(int64_t units, int units_per_block, int resident, int cap) {
   return (int)(blocks > 0 ? blocks : 1);
 }
 
-// Grid of fwl_wave_rows: one resident set of blocks when that leaves each wavefront at most
-// kRowsPerWave rows, more blocks (queued) otherwise.
-int wave_grid(int64_t N, int resident) {
+int device_cus() {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
+  cache.emplace(dev, cus);
+  return cus;
+}
+
+// Grid of fwl_wave_rows.  Each wavefront keeps one row load and one row of stores in flight, so
+// the blocks per CU set the number of concurrent row streams.  Measured on MI355X at C = 1000: two
+// blocks per CU (8 wavefronts, ~64 KB in flight per CU) stream best; more concurrent streams over
+// a wider address window lose DRAM efficiency.  Shorter rows get proportionally more blocks, up to
+// the resident limit.  At most kRowsPerWave rows per wavefront: larger N gets more (queued) blocks.
+int wave_grid(int64_t N, int C, int resident) {
+  const int cus = device_cus();
+  const int per_cu_resident = cus > 0 && resident > 0 ? resident / cus : 0;
+  int per_cu = (int)((2000 + C - 1) / (C > 0 ? C : 1));
+  if (per_cu < 2) per_cu = 2;
+  if (per_cu_resident > 0 && per_cu > per_cu_resident) per_cu = per_cu_resident;
+  const int target = cus > 0 ? per_cu * cus : (resident > 0 ? resident : kMaxBlocksWave);
   const int64_t min_blocks = (N + (int64_t)kWavesPerBlock * kRowsPerWave - 1) / ((int64_t)kWavesPerBlock * kRowsPerWave);
   const int cap = (int)(min_blocks > kMaxBlocksWave ? min_blocks : kMaxBlocksWave);
-  const int64_t g = persistent_grid(N, kWavesPerBlock, resident, cap);
+  const int64_t g = persistent_grid(N, kWavesPerBlock, target, cap);
   return (int)(g > min_blocks ? g : min_blocks);
 }
 
@@ -1332,7 +1355,7 @@ int launch_status() { return hipGetLastError() == hipSuccess ? FWL_OK : FWL_ERR_
 template <int MODE, int NV, bool V4>
 void launch_wave(const float* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   const void* k = reinterpret_cast<const void*>(&fwl_wave_rows<MODE, NV, V4>);
-  const int grid = wave_grid(N, resident_blocks(k));
+  const int grid = wave_grid(N, C, resident_blocks(k));
   hipLaunchKernelGGL((fwl_wave_rows<MODE, NV, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
 }
 

@@ -1,0 +1,182 @@
+"""Host-side checks that need no GPU: the C ABI library and its header, argument validation
+(every entry point validates before it touches a device), the torch extension's argument errors,
+the synthetic-data generators and the package's separation from the oracle.
+"""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import fwloss_capi as capi
+import fwloss_data as data
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "fast-familywise-loss_amd")
+
+# fake device addresses: validation rejects the call before any of them is dereferenced
+A16 = 0x10000          # 16-byte aligned
+A4 = 0x10004           # 4-byte aligned only
+A2 = 0x10002           # misaligned for everything
+
+
+def P(x):
+    return ctypes.c_void_p(x)
+
+
+def test_library_exports_every_declared_function():
+    L = capi.lib()
+    declared = capi.declared_functions()
+    assert len(declared) == 10
+    for name in declared:
+        assert hasattr(L, name), name
+    # the ctypes signature table covers exactly the header
+    assert sorted(capi.SIGNATURES) == declared
+    out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r" T (fwl_\w+)$", out.stdout, re.M))
+    assert exported == set(declared)
+
+
+def test_header_is_plain_c():
+    # the boundary must be usable from C (cgo/JNI/ctypes): compile the header alone as C99
+    src = '#include "fwloss.h"\nint main(void) { int p, c; return fwl_get_params(&p, &c); }\n'
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-I", os.path.join(ROOT, "include"),
+                        "-x", "c", "-"], input=src, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_status_strings():
+    texts = [capi.status_string(i) for i in range(6)]
+    assert texts[0] == "ok"
+    assert len(set(texts)) == 6
+    assert capi.status_string(99) == "unknown fwloss status"
+
+
+def test_workspace_bytes():
+    L = capi.lib()
+    base = L.fwl_workspace_bytes(0, 1)
+    assert base >= 256 + 8 * 4096
+    assert L.fwl_workspace_bytes(65536, 1000) == base
+    # grows with N once the row-per-wave grid exceeds the fixed caps, one fp64 partial per block
+    big = L.fwl_workspace_bytes(1 << 22, 10)
+    assert big == 256 + 8 * ((1 << 22) // 256)
+    assert L.fwl_workspace_bytes(1 << 22, 10) >= L.fwl_workspace_bytes((1 << 22) - 1, 10)
+
+
+def test_forward_backward_argument_errors():
+    L = capi.lib()
+    ws_need = L.fwl_workspace_bytes(8, 16)
+
+    def call(z=A16, y=A16, N=8, C=16, H=A16, loss=A16, mean=A16, kappa=A16, grad=A16, ws=A16, wsb=ws_need):
+        return L.fwl_forward_backward(P(z), P(y), N, C, 1.0, 1.0, P(H), P(loss), P(mean), P(kappa), P(grad),
+                                      P(ws), wsb, None)
+    assert call(z=None) == 1
+    assert call(y=None) == 1
+    assert call(grad=None) == 1
+    assert call(N=-1) == 1
+    assert call(C=0) == 1
+    assert call(C=2 ** 31) == 1
+    assert call(z=A2) == 3
+    assert call(y=A4) == 3
+    assert call(grad=A2) == 3
+    assert call(ws=None) == 2
+    assert call(wsb=ws_need - 1) == 2
+    assert call(ws=A4 + 2) == 2
+
+
+def test_other_entry_point_argument_errors():
+    L = capi.lib()
+    ws_need = L.fwl_workspace_bytes(8, 16)
+    assert L.fwl_forward_small(P(A16), P(A16), 8, 16, P(A16), P(A16), P(A16), P(A16), None, P(A16), ws_need,
+                               None) == 1
+    assert L.fwl_forward_small(P(A16), P(A16), 8, 16, P(A16), P(A16), P(A16), P(A16), P(A16), P(A16), 8,
+                               None) == 2
+    assert L.fwl_forward_large(P(A16), P(A16), 8, 16, P(A16), P(A16), P(A16), P(A16), P(A16), None, P(A16),
+                               P(A16), ws_need, None) == 1
+    assert L.fwl_forward_large(P(A16), P(A16), 8, 16, P(A16), P(A16), P(A16), P(A16), P(A2), P(A16), P(A16),
+                               P(A16), ws_need, None) == 3
+    assert L.fwl_backward_small(P(A16), P(A16), None, 8, 16, P(A16), None) == 1
+    assert L.fwl_backward_small(P(A4), P(A16), P(A16), 8, 16, P(A16), None) == 3
+    assert L.fwl_backward_large(P(A16), P(A16), P(A16), P(A16), P(A16), P(A16), None, 8, 16, P(A16), None) == 1
+    assert L.fwl_backward_large(P(A16), P(A16), P(A16), P(A16), P(A16), P(A16), P(A16), 8, 16, P(A2), None) == 3
+    assert L.fwl_scale_grad(P(A16), P(A16), -1, 8, 16, None) == 1
+    assert L.fwl_scale_grad(P(A16), None, 0, 8, 16, None) == 1
+    assert L.fwl_scale_grad(P(A2), P(A16), 0, 8, 16, None) == 3
+    # empty batches return before any launch for the backward entry points
+    assert L.fwl_backward_small(None, None, None, 0, 16, None, None) == 0
+    assert L.fwl_scale_grad(None, None, 0, 0, 16, None) == 0
+
+
+def test_set_params_validation_and_round_trip():
+    L = capi.lib()
+    p, c = ctypes.c_int(-1), ctypes.c_int(-1)
+    assert L.fwl_get_params(ctypes.byref(p), ctypes.byref(c)) == 0
+    saved = (p.value, c.value)
+    try:
+        assert L.fwl_set_params(4, 512) == 1
+        assert L.fwl_set_params(-1, 512) == 1
+        assert L.fwl_set_params(2, 63) == 1
+        assert L.fwl_set_params(2, 513) == 1
+        assert L.fwl_set_params(2, 64) == 0
+        L.fwl_get_params(ctypes.byref(p), ctypes.byref(c))
+        assert (p.value, c.value) == (2, 64)
+    finally:
+        L.fwl_set_params(*saved)
+
+
+def test_extension_rejects_cpu_and_bad_inputs():
+    import fwloss
+    z = torch.zeros(4, 6)
+    y = torch.zeros(4, dtype=torch.long)
+    for op in (fwloss.fw_forward_small, fwloss.fw_forward, fwloss.fw_forward_backward):
+        with pytest.raises(RuntimeError, match="logits must be a CUDA tensor"):
+            op(z, y)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        fwloss.familywise_loss(z, y)
+    with pytest.raises(ValueError, match="Invalid reduction mode"):
+        fwloss.familywise_loss(z, y, reduction="max")
+    with pytest.raises(RuntimeError):
+        fwloss.set_params(7, 512)
+    assert tuple(fwloss.get_params()) == (0, 512)
+    libs = fwloss.native_libraries()
+    assert any(p.endswith("libfwloss.so") for p in libs) and any("fw_radix_cuda" in p for p in libs)
+
+
+@pytest.mark.parametrize("cfg", sorted(data.CONFIGS))
+def test_generators(cfg):
+    z, y = data.make(cfg, N=16, seed=5)
+    C = data.CONFIGS[cfg]["C"]
+    assert z.shape == (16, C) and z.dtype == np.float32 and z.flags.c_contiguous
+    assert y.shape == (16,) and y.dtype == np.int64 and y.min() >= 0 and y.max() < C
+    z2, y2 = data.make(cfg, N=16, seed=5)
+    np.testing.assert_array_equal(z, z2)
+    np.testing.assert_array_equal(y, y2)
+    assert not np.array_equal(z, data.make(cfg, N=16, seed=6)[0])
+
+
+def test_edge_rows():
+    z, y = data.edge_rows()
+    assert z.dtype == np.float32 and z.shape[0] == y.shape[0] >= 10
+    assert (y >= 0).all() and (y < z.shape[1]).all()
+    assert np.isneginf(z).any() and (np.abs(z) >= 2.0 ** 53).any()
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_product_never_touches_the_oracle():
+    """Only tests, smoke() and bench.py's CPU baseline may use oracle/; the package never does."""
+    for dirpath, _, files in os.walk(PKG):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".h")):
+                with open(os.path.join(dirpath, f)) as fh:
+                    text = fh.read()
+                assert not re.search(r"^\s*(import|from)\s+oracle\b", text, re.M), f
+                assert "fwl_oracle" not in text and "oracle/" not in text, f
