@@ -10,7 +10,7 @@ rotated between steps so the 256 MB Infinity Cache cannot hold a step's data fro
 Prints one JSON line.  ``roofline.achieved`` = algorithmic bytes per launch (read logits once,
 write the gradient once, read labels, write H/loss/kappa: 8*N*C + 20*N bytes) / the kernel's mean
 duration measured with HIP events on the stream the kernel runs on.  ``roofline.traffic`` is the
-HBM bytes per launch measured with rocprofv3 counters (profiles/traffic_*.json), or null.
+HBM bytes per launch measured with rocprofv3 counters (profiles/<kernel>_<config>.md), or null.
 ``cpu_baseline`` times the reference's own CPU path (compiled into oracle/_ref) on this host's cores,
 on the same host-generated inputs, as loss + full gradient per call (benchmarks/cpu_benchmarks/
 bench_cpu_e2e.py:13-15); without oracle/_ref the C restatement is timed instead.
@@ -18,6 +18,7 @@ bench_cpu_e2e.py:13-15); without oracle/_ref the C restatement is timed instead.
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -53,12 +54,14 @@ def parse():
 
 
 def traffic_for(kernel_tag, cfg):
-    path = os.path.join(ROOT, "profiles", f"traffic_{kernel_tag}_{cfg}.json")
+    """HBM bytes per launch of the fused kernel, from the rocprofv3 summary committed under profiles/
+    (FETCH_SIZE and WRITE_SIZE passes, each scaled by what the counter reads for a plain copy)."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_{cfg}.md")
     if not os.path.isfile(path):
         return None
     with open(path) as f:
-        d = json.load(f)
-    return d.get("hbm_bytes_per_launch")
+        m = re.search(r"^hbm_bytes_per_launch: (\d+)$", f.read(), re.M)
+    return int(m.group(1)) if m else None
 
 
 def cpu_baseline(z_np, y_np, seconds):
