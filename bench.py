@@ -89,7 +89,7 @@ def cpu_baseline(z_np, y_np, seconds):
     call()
     times = []
     t_end = time.perf_counter() + seconds
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 5000):
         t0 = time.perf_counter()
         call()
         times.append(time.perf_counter() - t0)

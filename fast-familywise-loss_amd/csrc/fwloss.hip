@@ -9,12 +9,14 @@
 //     a lower bound that may be used to discard entries early (fw_cpu.cpp:201-211).
 //
 // Kernels
-//   fwl_wave_rows   C <= 1024: one wavefront per row, the row held in VGPRs (128-bit loads),
-//                   candidates z > max-1 compacted into LDS with ballot/mbcnt, then sorted across
-//                   the wavefront (bitonic network over DPP / ds_swizzle), prefix-summed in fp64
-//                   (DPP row_shr + row_bcast scan) and tau = max_k (S_k - 1)/k.  Rows with more
-//                   than 64 candidates use fixed-point (Michelot) iterations on the register row.
-//                   The epilogue writes H, loss, kappa and the gradient / mask / candidate list.
+//   fwl_wave_rows   C <= 1024: one wavefront per row, the row held in VGPRs (128-bit buffer loads),
+//                   the next row's loads issued as soon as this row's candidates z > max-1 are
+//                   compacted into an LDS list (prefix sum of per-lane counts, branch-free
+//                   writes).  Up to 64 candidates are sorted across the wavefront (bitonic network
+//                   over DPP and permlane swaps), prefix-summed in fp64 (DPP row_shr + row_bcast
+//                   scan) and tau = max_k (S_k - 1)/k; longer lists use fixed-point (Michelot)
+//                   iterations.  The epilogue writes the gradient / mask / candidate list; H, loss
+//                   and kappa of a wavefront's rows are stored once after its last row.
 //   fwl_block_rows  C > 1024: one block (4 wavefronts) per row.  Each wavefront streams its share
 //                   of the row once with a running lower bound t = (its max so far) - 1, keeps
 //                   the entries z > t in an LDS list (value, index) and writes the output of every

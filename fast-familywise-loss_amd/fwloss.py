@@ -41,6 +41,14 @@ get_params = _ext.get_params
 _REDUCTIONS = ("mean", "sum", "none")
 
 
+class ReductionError(KeyError, ValueError):
+    """Unknown reduction name.  The reference looks the name up in a dict (src/cpu/fwcpp.py:19) and
+    so raises KeyError; this is also a ValueError, the usual type for a bad argument value."""
+
+    def __str__(self):
+        return str(self.args[0]) if self.args else ""
+
+
 class FWFunction(torch.autograd.Function):
     """Eager-gradient autograd Function (the GPU counterpart of fw_cpu.cpp:721-741)."""
 
@@ -71,19 +79,21 @@ def familywise_loss(logits, target, reduction="mean"):
     accepts 'sum' and 'mean'; 'none' returns the per-row losses (reference_impl.py:30-33).
     """
     if reduction not in _REDUCTIONS:
-        raise ValueError(f"Invalid reduction mode: {reduction}")
+        raise ReductionError(f"Invalid reduction mode: {reduction!r} (expected 'mean', 'sum' or 'none')")
     if not logits.is_cuda:
         raise RuntimeError("familywise_loss: logits must be a CUDA (ROCm) tensor; this package has no CPU path")
     return FWFunction.apply(logits, target, reduction)
 
 
-def fw_loss_grad(Z, y, scale=1.0):
-    """(per-row loss [N] float32, scale * gradient [N, C], kappa [N] int32), as fwcpp.fw_loss_grad
-    (src/cpu/fwcpp.py:21-23) returns (loss, scale * gradient, kappa) for the CPU path."""
+def fw_loss_grad(Z, y, scale=1.0, flat_kmax=None, serial_below=None, use_chunked=None):
+    """(per-row loss [N] float64, scale * gradient [N, C] float32, kappa [N] int64), the outputs and
+    dtypes of fwcpp.fw_loss_grad (src/cpu/fwcpp.py:21-23).  flat_kmax, serial_below and use_chunked
+    tune the reference's CPU branches (fw_cpu.cpp:750-757); they are accepted and have no effect
+    here.  The losses are computed in fp64 and rounded to fp32 on the device, then widened."""
     if not Z.is_cuda:
         raise RuntimeError("fw_loss_grad: Z must be a CUDA (ROCm) tensor")
     _, losses, _, kappa, grad = _ext.fw_forward_backward(Z, y, float(scale), 1.0)
-    return losses, grad, kappa
+    return losses.double(), grad, kappa.long()
 
 
 def native_libraries():

@@ -281,6 +281,19 @@ def test_autograd(ext, dev, reduction):
     assert bits_equal(zt.grad.cpu().numpy(), expect.astype(np.float32))
 
 
+def test_fw_loss_grad_api(ext, dev):
+    """fwloss.fw_loss_grad: the outputs and dtypes of the reference's fwcpp.fw_loss_grad."""
+    z, y = data.make("cfg3", N=200, seed=8)
+    zt, yt = to_dev(dev, z, y)
+    L, G, k = ext.fw_loss_grad(zt, yt, 0.25, 2 ** 62, 100000, True)
+    assert L.dtype == torch.float64 and G.dtype == torch.float32 and k.dtype == torch.int64
+    ref = oracle.definition(z, y, scale=0.25)
+    np.testing.assert_array_equal(k.cpu().numpy(), ref["kappa"])
+    np.testing.assert_array_equal(L.cpu().numpy(), ref["loss"].astype(np.float64))
+    np.testing.assert_allclose(L.cpu().numpy(), ref["loss64"], rtol=1e-6, atol=1e-6)
+    assert bits_equal(G.cpu().numpy(), ref["grad"])
+
+
 def test_c_abi_direct(ext, dev):
     z, y = data.make("cfg2", N=256, seed=6)
     zt, yt = to_dev(dev, z, y)

@@ -139,6 +139,8 @@ def test_extension_rejects_cpu_and_bad_inputs():
         fwloss.familywise_loss(z, y)
     with pytest.raises(ValueError, match="Invalid reduction mode"):
         fwloss.familywise_loss(z, y, reduction="max")
+    with pytest.raises(KeyError):   # what the reference's dict lookup raises (src/cpu/fwcpp.py:19)
+        fwloss.familywise_loss(z, y, reduction="max")
     with pytest.raises(RuntimeError):
         fwloss.set_params(7, 512)
     assert tuple(fwloss.get_params()) == (0, 512)
