@@ -18,11 +18,13 @@
 //                   iterations.  The epilogue writes the gradient / mask / candidate list; H, loss
 //                   and kappa of a wavefront's rows are stored once after its last row.
 //   fwl_block_rows  C > 1024: one block (4 wavefronts) per row.  Each wavefront streams its share
-//                   of the row once with a running lower bound t = (its max so far) - 1, keeps
-//                   the entries z > t in an LDS list (value, index) and writes the output of every
-//                   other entry immediately (they are <= t <= tau).  A full list is tightened by
-//                   fixed-point iterations on the list; a list that cannot be tightened sends the
-//                   row to the generic multi-pass path.
+//                   of the row once, its loads one round ahead, with a running lower bound
+//                   t = (its max so far) - 1; it keeps the entries z > t in an LDS list (value,
+//                   index) and writes a zero placeholder for every output element as it goes.
+//                   After the selection only the support entries and the label are rewritten,
+//                   so almost every 128-byte line is written exactly once, whole.  A full list is
+//                   tightened by fixed-point iterations on the list; a list that cannot be
+//                   tightened sends the row to the generic multi-pass path.
 //   fwl_mask_to_grad, fwl_cand_to_grad   the two-op backward of the drop-in interface.
 // The mean loss is reduced in fp64 in a fixed order: per-block partial sums, then the last block
 // to finish (ticket counter in the caller's workspace) sums the partials and resets the counter.
@@ -62,7 +64,8 @@ constexpr int kMaxWaveC = 1024;        // longest row held in registers by one w
 constexpr int kCapMax = 512;           // LDS candidate slots per wavefront in fwl_block_rows
 constexpr int kMaxBlocksWave = 2048;   // grid cap of fwl_wave_rows (4 rows in flight per block)
 constexpr int kMaxBlocksRow = 4096;    // grid cap of fwl_block_rows
-constexpr int kStreamUnroll = 4;       // 128-bit loads in flight per lane per streaming round
+constexpr int kStreamUnroll = 4;       // 128-bit loads per lane per streaming round
+constexpr int kRoundSlotsV1 = 16;      // 32-bit loads per lane per streaming round (unaligned rows)
 constexpr size_t kWsHeader = 256;      // ticket counter, then fp64 partial sums
 
 enum Mode : int { kGrad = 0, kMask = 1, kCand = 2 };
@@ -733,17 +736,9 @@ struct BlockShared {
   int kappa;
 };
 
-template <int MODE>
-__device__ __forceinline__ void write_zero(const Outs& o, int64_t r, int C, int j) {
-  if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + j] = 0.0f;
-  else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + j] = 0;
-}
-
 // Raise the wavefront's lower bound t with a few fixed-point steps on its list, then drop the
-// entries <= t (their output is written now: they are not in the support).
-template <int MODE>
-__device__ void tighten(float* bv, int* bi, int& n, float& t, const Outs& o, int64_t r, int C,
-                        int yr, int lane) {
+// entries <= t (not in the support: their output stays the zero written while streaming).
+__device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, int lane) {
   float tf = t;
   for (int it = 0; it < 8; ++it) {
     double s;
@@ -769,8 +764,6 @@ __device__ void tighten(float* bv, int* bi, int& n, float& t, const Outs& o, int
       const int pos = w + rank_in(b);
       bv[pos] = v;
       bi[pos] = id;
-    } else if (p < n && id != yr) {
-      write_zero<MODE>(o, r, C, id);
     }
     w += __popcll(b);
     __builtin_amdgcn_wave_barrier();
@@ -778,118 +771,151 @@ __device__ void tighten(float* bv, int* bi, int& n, float& t, const Outs& o, int
   n = w;
 }
 
-// Stream this wavefront's share of row r once.  Returns false if its list overflowed.
-template <int MODE, bool V4>
-__device__ bool stream_row(const float* __restrict__ row, int64_t r, int C, int yr, int lane,
-                           int wid, float* bv, int* bi, const Outs& o, int& n, float& m, float& t) {
-  constexpr int U = kStreamUnroll;
-  const int cap = o.cap;
+// One streaming round of a wavefront: kRoundSlots values per lane.  With 128-bit access slot
+// 4u+e is element 4*q_u + e, q_u = wid*64 + lane + kBlock*(round*kStreamUnroll + u) (a float4
+// index); otherwise slot u is element wid*64 + lane + kBlock*(round*kRoundSlots + u).
+template <bool V4>
+struct Round {
+  static constexpr int kSlots = V4 ? 4 * kStreamUnroll : kRoundSlotsV1;
+  float x[kSlots];
+};
+
+template <bool V4>
+__device__ __forceinline__ int round_slot_index(int round, int slot, int wid, int lane) {
   if constexpr (V4) {
-    const int nvec = C >> 2;
-    const v4f* row4 = reinterpret_cast<const v4f*>(row);
-    for (int k0 = 0; k0 * kBlock < nvec; k0 += U) {
-      v4f v[U];
-      int q[U];
+    const int q = wid * kWave + lane + kBlock * (round * kStreamUnroll + (slot >> 2));
+    return 4 * q + (slot & 3);
+  } else {
+    return wid * kWave + lane + kBlock * (round * kRoundSlotsV1 + slot);
+  }
+}
+
+// loads of one round, unconditional: offsets past the row read 0 (masked to -inf when used)
+template <bool V4>
+__device__ __forceinline__ void load_round(rsrc_t row, int round, int wid, int lane, Round<V4>& a) {
+  if constexpr (V4) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        q[u] = wid * kWave + lane + kBlock * (k0 + u);
-        v[u] = v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        if (q[u] < nvec) v[u] = __builtin_nontemporal_load(row4 + q[u]);
-      }
-      float lm = -INFINITY;
-#pragma unroll
-      for (int u = 0; u < U; ++u) lm = fmaxf(fmaxf(lm, fmaxf(v[u].x, v[u].y)), fmaxf(v[u].z, v[u].w));
-      m = fmaxf(m, wave_max_f32(lm));
-      t = fmaxf(t, bound_below_max(m));
-      unsigned defer = 0;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float xv = v[u][e];
-          bool p = xv > t;
-          uint64_t b = ballot(p);
-          if (b) {
-            int cnt = __popcll(b);
-            if (n + cnt > cap) {
-              tighten<MODE>(bv, bi, n, t, o, r, C, yr, lane);
-              p = xv > t;
-              b = ballot(p);
-              cnt = __popcll(b);
-              if (n + cnt > cap) return false;
-            }
-            if (p) {
-              const int pos = n + rank_in(b);
-              bv[pos] = xv;
-              bi[pos] = 4 * q[u] + e;
-            }
-            n += cnt;
-          }
-          defer |= (unsigned)p << (4 * u + e);
-        }
-      }
-      if constexpr (MODE != kCand) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          if (q[u] < nvec) {
-            const int j0 = 4 * q[u];
-            unsigned dm = (defer >> (4 * u)) & 0xFu;
-            if (yr >= j0 && yr < j0 + 4) dm |= 1u << (yr - j0);
-            if (dm == 0) {
-              if constexpr (MODE == kGrad)
-                __builtin_nontemporal_store(v4f{0.0f, 0.0f, 0.0f, 0.0f},
-                                            reinterpret_cast<v4f*>(o.grad + r * (int64_t)C) + q[u]);
-              else
-                __builtin_nontemporal_store(0u, reinterpret_cast<unsigned*>(o.mask + r * (int64_t)C) + q[u]);
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (!((dm >> e) & 1u)) write_zero<MODE>(o, r, C, j0 + e);
-            }
-          }
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
+    for (int u = 0; u < kStreamUnroll; ++u) {
+      const uint32_t q = (uint32_t)(wid * kWave + lane + kBlock * (round * kStreamUnroll + u));
+      const v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(row, 16u * q, 0, kNonTemporal));
+      a.x[4 * u + 0] = v.x;
+      a.x[4 * u + 1] = v.y;
+      a.x[4 * u + 2] = v.z;
+      a.x[4 * u + 3] = v.w;
     }
   } else {
-    for (int k0 = 0; k0 * kBlock < C; k0 += U) {
-      float v[U];
-      int jj[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        jj[u] = wid * kWave + lane + kBlock * (k0 + u);
-        v[u] = jj[u] < C ? __builtin_nontemporal_load(row + jj[u]) : -INFINITY;
-      }
-      float lm = v[0];
-#pragma unroll
-      for (int u = 1; u < U; ++u) lm = fmaxf(lm, v[u]);
-      m = fmaxf(m, wave_max_f32(lm));
-      t = fmaxf(t, bound_below_max(m));
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        bool p = v[u] > t;
-        uint64_t b = ballot(p);
-        if (b) {
-          int cnt = __popcll(b);
-          if (n + cnt > cap) {
-            tighten<MODE>(bv, bi, n, t, o, r, C, yr, lane);
-            p = v[u] > t;
-            b = ballot(p);
-            cnt = __popcll(b);
-            if (n + cnt > cap) return false;
-          }
-          if (p) {
-            const int pos = n + rank_in(b);
-            bv[pos] = v[u];
-            bi[pos] = jj[u];
-          }
-          n += cnt;
-        }
-        if constexpr (MODE != kCand)
-          if (jj[u] < C && !p && jj[u] != yr) write_zero<MODE>(o, r, C, jj[u]);
-      }
-      __builtin_amdgcn_wave_barrier();
+    for (int u = 0; u < kRoundSlotsV1; ++u) {
+      const uint32_t j = (uint32_t)(wid * kWave + lane + kBlock * (round * kRoundSlotsV1 + u));
+      a.x[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(row, 4u * j, 0, kNonTemporal));
     }
+  }
+}
+
+// zero placeholders for every output element of one round (support entries are rewritten at
+// the end of the row); offsets past the row end are dropped by the range check
+template <int MODE, bool V4>
+__device__ __forceinline__ void zero_round(rsrc_t out, int round, int wid, int lane) {
+  if constexpr (MODE == kGrad) {
+    if constexpr (V4) {
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const uint32_t q = (uint32_t)(wid * kWave + lane + kBlock * (round * kStreamUnroll + u));
+        __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, out, 16u * q, 0, kNonTemporal);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kRoundSlotsV1; ++u) {
+        const uint32_t j = (uint32_t)(wid * kWave + lane + kBlock * (round * kRoundSlotsV1 + u));
+        __builtin_amdgcn_raw_buffer_store_b32(0u, out, 4u * j, 0, kNonTemporal);
+      }
+    }
+  } else if constexpr (MODE == kMask) {
+    if constexpr (V4) {
+#pragma unroll
+      for (int u = 0; u < kStreamUnroll; ++u) {
+        const uint32_t q = (uint32_t)(wid * kWave + lane + kBlock * (round * kStreamUnroll + u));
+        __builtin_amdgcn_raw_buffer_store_b32(0u, out, 4u * q, 0, kNonTemporal);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kRoundSlotsV1; ++u) {
+        const uint32_t j = (uint32_t)(wid * kWave + lane + kBlock * (round * kRoundSlotsV1 + u));
+        __builtin_amdgcn_raw_buffer_store_b8((unsigned char)0, out, j, 0, kNonTemporal);
+      }
+    }
+  }
+}
+
+// Candidates of one round: the running maximum m gives the bound t = (m - 1 rounded down), and
+// the entries z > t are appended to the wavefront's list.  Returns false on list overflow.
+template <bool V4>
+__device__ __forceinline__ bool scan_round(Round<V4>& a, int round, int C, int wid, int lane, float* bv,
+                                           int* bi, int cap, int& n, float& m, float& t) {
+  constexpr int S = Round<V4>::kSlots;
+  float lm = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const int j = round_slot_index<V4>(round, i, wid, lane);
+    a.x[i] = j < C ? a.x[i] : -INFINITY;
+    lm = fmaxf(lm, a.x[i]);
+  }
+  m = fmaxf(m, wave_max_f32(lm));
+  t = fmaxf(t, bound_below_max(m));
+  if (ballot(lm > t) == 0) return true;   // no candidate in this round (the common case)
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > t));
+  if (n + cnt > cap) {
+    tighten(bv, bi, n, t, lane);
+    cnt = 0;
+#pragma unroll
+    for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > t));
+    if (n + cnt > cap) return false;
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const bool p = a.x[i] > t;
+    const uint64_t b = ballot(p);
+    if (p) {
+      const int pos = n + rank_in(b);
+      bv[pos] = a.x[i];
+      bi[pos] = round_slot_index<V4>(round, i, wid, lane);
+    }
+    n += __popcll(b);
+  }
+  return true;
+}
+
+// Stream this wavefront's share of row r once: loads run one round ahead of the candidate scan,
+// and every output element gets its zero placeholder.  Returns false if the list overflowed.
+template <int MODE, bool V4>
+__device__ bool stream_row(const float* __restrict__ row, int64_t r, int C, int lane, int wid, float* bv,
+                           int* bi, const Outs& o, int& n, float& m, float& t) {
+  constexpr int per_round = kBlock * Round<V4>::kSlots;   // elements per block-wide round
+  const int rounds = (C + per_round - 1) / per_round;
+  const rsrc_t in = make_rsrc(row, 4u * (uint32_t)C);
+  rsrc_t out = make_rsrc(nullptr, 0u);
+  if constexpr (MODE == kGrad) out = make_rsrc(o.grad + r * (int64_t)C, 4u * (uint32_t)C);
+  else if constexpr (MODE == kMask) out = make_rsrc(o.mask + r * (int64_t)C, (uint32_t)C);
+  const int cap = o.cap;
+  Round<V4> a, b;
+  load_round<V4>(in, 0, wid, lane, a);
+  // stores to a zero-size resource (no traffic) so that the wait counts on entry match those of
+  // the loop's back edge (a round's loads, then a round's stores)
+  __builtin_amdgcn_sched_barrier(0);
+  zero_round<MODE, V4>(make_rsrc(nullptr, 0u), 0, wid, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  int k = 0;
+  while (true) {
+    load_round<V4>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
+    zero_round<MODE, V4>(out, k, wid, lane);
+    if (!scan_round<V4>(a, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
+    if (++k >= rounds) break;
+    load_round<V4>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
+    zero_round<MODE, V4>(out, k, wid, lane);
+    if (!scan_round<V4>(b, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
+    if (++k >= rounds) break;
   }
   return true;
 }
@@ -1014,12 +1040,14 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict
     int n = 0;
     float m = -INFINITY, t = -INFINITY;
     bool ok = !o.force_generic;
-    if (ok) ok = stream_row<MODE, V4>(row, r, C, yr, lane, wid, bv, bi, o, n, m, t);
+    if (ok) ok = stream_row<MODE, V4>(row, r, C, lane, wid, bv, bi, o, n, m, t);
     if (lane == 0) {
       sh.wmax[wid] = m;
       sh.wn[wid] = n;
       sh.ovf[wid] = !ok;
     }
+    // every wavefront's zero placeholders have landed before any support entry is rewritten
+    wait_vmem();
     __syncthreads();
     const bool overflow = sh.ovf[0] | sh.ovf[1] | sh.ovf[2] | sh.ovf[3];
 
@@ -1113,12 +1141,12 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict
       const float Hf = rd32(tau);
       const float inv = (float)(o.scale / (double)kappa);
       if constexpr (MODE == kGrad || MODE == kMask) {
+        // the zero placeholders stand for every other entry
         for (int p = lane; p < n; p += kWave) {
           const int id = bi[p];
-          if (id == yr) continue;
-          const bool s = bv[p] > Hf;
-          if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + id] = s ? inv : 0.0f;
-          else o.mask[r * (int64_t)C + id] = (uint8_t)s;
+          if (id == yr || !(bv[p] > Hf)) continue;
+          if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + id] = inv;
+          else o.mask[r * (int64_t)C + id] = 1;
         }
       } else {
         int ns = 0;
@@ -1391,7 +1419,10 @@ void dispatch_block(const float* z, const int64_t* y, int64_t N, int C, bool v4,
   else launch_block<MODE, false>(z, y, N, C, o, s);
 }
 
-bool bad_shape(int64_t N, int64_t C) { return N < 0 || C < 1 || C >= (int64_t)INT32_MAX - 64; }
+// rows are addressed through buffer resources with 32-bit byte ranges and offsets (one round
+// past the row end included), hence the bound on C
+constexpr int64_t kMaxC = (int64_t)1 << 29;
+bool bad_shape(int64_t N, int64_t C) { return N < 0 || C < 1 || C > kMaxC; }
 
 // shared forward driver; `out_v4_ok` says whether the mode's dense output allows 128-bit access
 template <int MODE>

@@ -42,7 +42,7 @@ typedef struct ihipStream_t* hipStream_t;
 
 enum fwl_status {
   FWL_OK = 0,
-  FWL_ERR_INVALID_ARG = 1,  /* null pointer, N < 0, C < 1, C >= 2^31 - 64 */
+  FWL_ERR_INVALID_ARG = 1,  /* null pointer, N < 0, C < 1, C > 2^29 */
   FWL_ERR_WORKSPACE = 2,    /* workspace missing or smaller than fwl_workspace_bytes(N, C) */
   FWL_ERR_ALIGNMENT = 3,    /* logits/grad not 4-byte aligned, or targets not 8-byte aligned */
   FWL_ERR_LAUNCH = 4,       /* the HIP runtime rejected a launch */

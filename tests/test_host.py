@@ -80,6 +80,7 @@ def test_forward_backward_argument_errors():
     assert call(N=-1) == 1
     assert call(C=0) == 1
     assert call(C=2 ** 31) == 1
+    assert call(C=2 ** 29 + 1) == 1
     assert call(z=A2) == 3
     assert call(y=A4) == 3
     assert call(grad=A2) == 3
