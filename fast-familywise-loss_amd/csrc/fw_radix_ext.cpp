@@ -224,7 +224,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("fw_forward_backward", &fw_forward_backward, "Fused FW loss forward + backward (MI355X)",
         py::arg("logits"), py::arg("targets"), py::arg("scale") = -1.0, py::arg("reduce_div") = -1.0);
   m.def("fw_scale_grad", &fw_scale_grad, "In-place grad *= grad_output (device-side skip when 1)");
-  m.def("set_params", &set_params, "Dispatch switches: path (0 auto, 1 wave, 2 block, 3 generic), cand_cap",
+  m.def("set_params", &set_params, "Dispatch switches: path (0 auto, 1 wave registers, 2 block stream, 3 block generic, "
+        "4 wave stream, 5 wave generic), cand_cap",
         py::arg("path"), py::arg("cand_cap") = 512);
   m.def("get_params", &get_params);
 }

@@ -9,7 +9,8 @@
 //     a lower bound that may be used to discard entries early (fw_cpu.cpp:201-211).
 //
 // Kernels
-//   fwl_wave_rows   C <= 1024: one wavefront per row, the row held in VGPRs (128-bit buffer loads),
+//   fwl_wave_rows   C <= 2048 (1024 for rows that are not 16-byte aligned): one wavefront per
+//                   row, the row held in VGPRs (128-bit buffer loads),
 //                   the next row's loads issued as soon as this row's candidates z > max-1 are
 //                   compacted into an LDS list (prefix sum of per-lane counts, branch-free
 //                   writes).  Up to 64 candidates are sorted across the wavefront (bitonic network
@@ -17,7 +18,9 @@
 //                   scan) and tau = max_k (S_k - 1)/k; longer lists use fixed-point (Michelot)
 //                   iterations.  The epilogue writes the gradient / mask / candidate list; H, loss
 //                   and kappa of a wavefront's rows are stored once after its last row.
-//   fwl_block_rows  C > 1024: one block (4 wavefronts) per row.  Each wavefront streams its share
+//   fwl_wave_stream_rows  mid-range C (up to 8192): one wavefront per row, streamed as below with
+//                   a single wavefront's list; no block-wide barrier.
+//   fwl_block_rows  C > 8192: one block (4 wavefronts) per row.  Each wavefront streams its share
 //                   of the row once, its loads one round ahead, with a running lower bound
 //                   t = (its max so far) - 1; it keeps the entries z > t in an LDS list (value,
 //                   index) and writes a zero placeholder for every output element as it goes.
@@ -60,7 +63,9 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 constexpr int kWave = 64;
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlock = kWave * kWavesPerBlock;
-constexpr int kMaxWaveC = 1024;        // longest row held in registers by one wavefront
+constexpr int kMaxWaveC = 2048;        // longest row held in registers by one wavefront (128-bit rows)
+constexpr int kMaxWaveC1 = 1024;       // the same for rows accessed 32 bits at a time
+constexpr int kMaxStreamC = 8192;      // longest row streamed by one wavefront (longer: one block per row)
 constexpr int kCapMax = 512;           // LDS candidate slots per wavefront in fwl_block_rows
 constexpr int kMaxBlocksWave = 2048;   // grid cap of fwl_wave_rows (4 rows in flight per block)
 constexpr int kMaxBlocksRow = 4096;    // grid cap of fwl_block_rows
@@ -454,16 +459,57 @@ __device__ __forceinline__ int wave_excl_scan_i32(int v, int& total) {
   return s - v;
 }
 
+// tau, kappa and (for n <= 64) the support bits of a candidate list cl[0, n) that holds every row
+// entry > t0 (t0 <= tau, e.g. the largest float <= max - 1) and whose largest entry is the row
+// maximum m.  Up to 64 entries: one per lane, sorted across the wavefront, fp64 prefix sums,
+// tau = max_k (S_k - 1)/k.  Longer lists: fixed-point iterations t <- H({z > t}) from t0 (each
+// iterate is <= tau and the set shrinks every step until it is {z > tau}).
+__device__ __forceinline__ void resolve_list(const float* cl, int n, float t0, float m, int lane, double& tau,
+                                             int& kappa, uint64_t& support) {
+  tau = NAN;
+  kappa = 0;
+  support = 0;
+  if (n > 0 && n <= kWave) {
+    const float c = lane < n ? cl[lane] : -INFINITY;
+    tau = clamp_below_max(select_small(c, n, lane), m);
+    support = ballot(lane < n && c > rd32(tau));
+    kappa = __popcll(support);
+  } else if (n > kWave) {
+    double t = (double)t0, s;
+    int c;
+    list_sum_count(cl, n, t0, lane, s, c);
+    for (int it = 0; it <= n + 1; ++it) {
+      const double tn = (s - 1.0) / (double)c;
+      double s2;
+      int c2;
+      list_sum_count(cl, n, rd32(tn), lane, s2, c2);
+      if (c2 == c || !(tn > t)) {
+        tau = tn;
+        kappa = c2;
+        break;
+      }
+      t = tn;
+      s = s2;
+      c = c2;
+    }
+    const double tc = clamp_below_max(tau, m);
+    if (tc != tau) {
+      double s3;
+      tau = tc;
+      list_sum_count(cl, n, rd32(tau), lane, s3, kappa);
+    }
+  }
+}
+
 struct RowResult {
   float H;
   float loss;
   int kappa;
 };
 
-// LDS candidate list of one wavefront: kMaxWaveC entries, then one spare slot per lane (the target
-// of the branch-free writes of non-candidates); the candidate-list mode keeps the indices alongside
-constexpr int kListCap = kMaxWaveC;
-constexpr int kListFloats = kListCap + kWave;
+// The LDS candidate list of a wavefront holds up to a whole register row (E values per lane),
+// then one spare slot per lane: the target of the branch-free writes of non-candidates.  The
+// candidate-list mode keeps the element indices alongside.
 constexpr int kRowsPerWave = kWave;   // rows of one wavefront per launch (labels/results: one lane each)
 
 // One row: x holds it (E values per lane).  Once its candidates are in the LDS list, the loads of
@@ -496,7 +542,7 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
 #pragma unroll
     for (int i = 0; i < E; ++i) {
       const int bit = (cm >> i) & 1;
-      const int at = bit ? pos : kListCap + lane;
+      const int at = bit ? pos : E * kWave + lane;
       cl[at] = x[i];
       if constexpr (MODE == kCand) ci_lds[at] = slot_index<V4>(i, lane);
       pos += bit;
@@ -506,41 +552,10 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
   __builtin_amdgcn_wave_barrier();
   load_row<NV, V4>(next, lane, x);
 
-  double tau = NAN;
-  int kappa = 0;
-  uint64_t support = 0;   // n <= 64: bit p set <=> list entry p is in the support
-  if (n > 0 && n <= kWave) {
-    const float c = lane < n ? cl[lane] : -INFINITY;
-    tau = clamp_below_max(select_small(c, n, lane), m);
-    support = ballot(lane < n && c > rd32(tau));
-    kappa = __popcll(support);
-  } else if (n > kWave) {
-    // fixed-point iteration t <- H({z > t}) over the list, from t = max - 1 (each iterate is
-    // <= tau; the set shrinks every step until it is {z > tau})
-    double t = (double)t0, s;
-    int c;
-    list_sum_count(cl, n, t0, lane, s, c);
-    for (int it = 0; it <= n + 1; ++it) {
-      const double tn = (s - 1.0) / (double)c;
-      double s2;
-      int c2;
-      list_sum_count(cl, n, rd32(tn), lane, s2, c2);
-      if (c2 == c || !(tn > t)) {
-        tau = tn;
-        kappa = c2;
-        break;
-      }
-      t = tn;
-      s = s2;
-      c = c2;
-    }
-    const double tc = clamp_below_max(tau, m);
-    if (tc != tau) {
-      double s3;
-      tau = tc;
-      list_sum_count(cl, n, rd32(tau), lane, s3, kappa);
-    }
-  }
+  double tau;
+  int kappa;
+  uint64_t support;   // n <= 64: bit p set <=> list entry p is in the support
+  resolve_list(cl, n, t0, m, lane, tau, kappa, support);
   const float Hf = rd32(tau);
 
   // support bit of every register slot of this lane (supports are subsets of the candidates)
@@ -668,6 +683,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const float* __restrict_
                                                         const int64_t* __restrict__ tgt, int64_t N,
                                                         int C, Outs o) {
   constexpr int E = V4 ? 4 * NV : NV;
+  constexpr int kListFloats = (E + 1) * kWave;   // a whole register row, then one spare slot per lane
   constexpr int kIdx = MODE == kCand ? kListFloats : 1;
   __shared__ float s_list[kWavesPerBlock][kListFloats];
   __shared__ int s_idx[kWavesPerBlock][kIdx];
@@ -771,32 +787,35 @@ __device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, in
   n = w;
 }
 
-// One streaming round of a wavefront: kRoundSlots values per lane.  With 128-bit access slot
-// 4u+e is element 4*q_u + e, q_u = wid*64 + lane + kBlock*(round*kStreamUnroll + u) (a float4
-// index); otherwise slot u is element wid*64 + lane + kBlock*(round*kRoundSlots + u).
+// Streaming rounds.  A row is shared by W wavefronts (W = 4: one block per row; W = 1: one
+// wavefront per row).  In round `round`, slot group u of a lane covers unit
+//     (W > 1 ? wid*64 : 0) + lane + 64*W*(round*PER + u)
+// where a unit is a float4 (128-bit access, PER = kStreamUnroll, slot 4u+e = element 4*unit + e)
+// or a single element (PER = kRoundSlotsV1, slot u = element unit).
+template <int W, int PER>
+__device__ __forceinline__ int lane_unit(int round, int u, int wid, int lane) {
+  return (W > 1 ? wid * kWave : 0) + lane + kWave * W * (round * PER + u);
+}
+
 template <bool V4>
 struct Round {
   static constexpr int kSlots = V4 ? 4 * kStreamUnroll : kRoundSlotsV1;
   float x[kSlots];
 };
 
-template <bool V4>
+template <int W, bool V4>
 __device__ __forceinline__ int round_slot_index(int round, int slot, int wid, int lane) {
-  if constexpr (V4) {
-    const int q = wid * kWave + lane + kBlock * (round * kStreamUnroll + (slot >> 2));
-    return 4 * q + (slot & 3);
-  } else {
-    return wid * kWave + lane + kBlock * (round * kRoundSlotsV1 + slot);
-  }
+  if constexpr (V4) return 4 * lane_unit<W, kStreamUnroll>(round, slot >> 2, wid, lane) + (slot & 3);
+  else return lane_unit<W, kRoundSlotsV1>(round, slot, wid, lane);
 }
 
 // loads of one round, unconditional: offsets past the row read 0 (masked to -inf when used)
-template <bool V4>
+template <int W, bool V4>
 __device__ __forceinline__ void load_round(rsrc_t row, int round, int wid, int lane, Round<V4>& a) {
   if constexpr (V4) {
 #pragma unroll
     for (int u = 0; u < kStreamUnroll; ++u) {
-      const uint32_t q = (uint32_t)(wid * kWave + lane + kBlock * (round * kStreamUnroll + u));
+      const uint32_t q = (uint32_t)lane_unit<W, kStreamUnroll>(round, u, wid, lane);
       const v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(row, 16u * q, 0, kNonTemporal));
       a.x[4 * u + 0] = v.x;
       a.x[4 * u + 1] = v.y;
@@ -806,7 +825,7 @@ __device__ __forceinline__ void load_round(rsrc_t row, int round, int wid, int l
   } else {
 #pragma unroll
     for (int u = 0; u < kRoundSlotsV1; ++u) {
-      const uint32_t j = (uint32_t)(wid * kWave + lane + kBlock * (round * kRoundSlotsV1 + u));
+      const uint32_t j = (uint32_t)lane_unit<W, kRoundSlotsV1>(round, u, wid, lane);
       a.x[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(row, 4u * j, 0, kNonTemporal));
     }
   }
@@ -814,19 +833,19 @@ __device__ __forceinline__ void load_round(rsrc_t row, int round, int wid, int l
 
 // zero placeholders for every output element of one round (support entries are rewritten at
 // the end of the row); offsets past the row end are dropped by the range check
-template <int MODE, bool V4>
+template <int W, int MODE, bool V4>
 __device__ __forceinline__ void zero_round(rsrc_t out, int round, int wid, int lane) {
   if constexpr (MODE == kGrad) {
     if constexpr (V4) {
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u) {
-        const uint32_t q = (uint32_t)(wid * kWave + lane + kBlock * (round * kStreamUnroll + u));
+        const uint32_t q = (uint32_t)lane_unit<W, kStreamUnroll>(round, u, wid, lane);
         __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, out, 16u * q, 0, kNonTemporal);
       }
     } else {
 #pragma unroll
       for (int u = 0; u < kRoundSlotsV1; ++u) {
-        const uint32_t j = (uint32_t)(wid * kWave + lane + kBlock * (round * kRoundSlotsV1 + u));
+        const uint32_t j = (uint32_t)lane_unit<W, kRoundSlotsV1>(round, u, wid, lane);
         __builtin_amdgcn_raw_buffer_store_b32(0u, out, 4u * j, 0, kNonTemporal);
       }
     }
@@ -834,13 +853,13 @@ __device__ __forceinline__ void zero_round(rsrc_t out, int round, int wid, int l
     if constexpr (V4) {
 #pragma unroll
       for (int u = 0; u < kStreamUnroll; ++u) {
-        const uint32_t q = (uint32_t)(wid * kWave + lane + kBlock * (round * kStreamUnroll + u));
+        const uint32_t q = (uint32_t)lane_unit<W, kStreamUnroll>(round, u, wid, lane);
         __builtin_amdgcn_raw_buffer_store_b32(0u, out, 4u * q, 0, kNonTemporal);
       }
     } else {
 #pragma unroll
       for (int u = 0; u < kRoundSlotsV1; ++u) {
-        const uint32_t j = (uint32_t)(wid * kWave + lane + kBlock * (round * kRoundSlotsV1 + u));
+        const uint32_t j = (uint32_t)lane_unit<W, kRoundSlotsV1>(round, u, wid, lane);
         __builtin_amdgcn_raw_buffer_store_b8((unsigned char)0, out, j, 0, kNonTemporal);
       }
     }
@@ -849,14 +868,14 @@ __device__ __forceinline__ void zero_round(rsrc_t out, int round, int wid, int l
 
 // Candidates of one round: the running maximum m gives the bound t = (m - 1 rounded down), and
 // the entries z > t are appended to the wavefront's list.  Returns false on list overflow.
-template <bool V4>
+template <int W, bool V4>
 __device__ __forceinline__ bool scan_round(Round<V4>& a, int round, int C, int wid, int lane, float* bv,
                                            int* bi, int cap, int& n, float& m, float& t) {
   constexpr int S = Round<V4>::kSlots;
   float lm = -INFINITY;
 #pragma unroll
   for (int i = 0; i < S; ++i) {
-    const int j = round_slot_index<V4>(round, i, wid, lane);
+    const int j = round_slot_index<W, V4>(round, i, wid, lane);
     a.x[i] = j < C ? a.x[i] : -INFINITY;
     lm = fmaxf(lm, a.x[i]);
   }
@@ -880,7 +899,7 @@ __device__ __forceinline__ bool scan_round(Round<V4>& a, int round, int C, int w
     if (p) {
       const int pos = n + rank_in(b);
       bv[pos] = a.x[i];
-      bi[pos] = round_slot_index<V4>(round, i, wid, lane);
+      bi[pos] = round_slot_index<W, V4>(round, i, wid, lane);
     }
     n += __popcll(b);
   }
@@ -889,10 +908,10 @@ __device__ __forceinline__ bool scan_round(Round<V4>& a, int round, int C, int w
 
 // Stream this wavefront's share of row r once: loads run one round ahead of the candidate scan,
 // and every output element gets its zero placeholder.  Returns false if the list overflowed.
-template <int MODE, bool V4>
+template <int W, int MODE, bool V4>
 __device__ bool stream_row(const float* __restrict__ row, int64_t r, int C, int lane, int wid, float* bv,
                            int* bi, const Outs& o, int& n, float& m, float& t) {
-  constexpr int per_round = kBlock * Round<V4>::kSlots;   // elements per block-wide round
+  constexpr int per_round = kWave * W * Round<V4>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
   const rsrc_t in = make_rsrc(row, 4u * (uint32_t)C);
   rsrc_t out = make_rsrc(nullptr, 0u);
@@ -900,21 +919,21 @@ __device__ bool stream_row(const float* __restrict__ row, int64_t r, int C, int 
   else if constexpr (MODE == kMask) out = make_rsrc(o.mask + r * (int64_t)C, (uint32_t)C);
   const int cap = o.cap;
   Round<V4> a, b;
-  load_round<V4>(in, 0, wid, lane, a);
+  load_round<W, V4>(in, 0, wid, lane, a);
   // stores to a zero-size resource (no traffic) so that the wait counts on entry match those of
   // the loop's back edge (a round's loads, then a round's stores)
   __builtin_amdgcn_sched_barrier(0);
-  zero_round<MODE, V4>(make_rsrc(nullptr, 0u), 0, wid, lane);
+  zero_round<W, MODE, V4>(make_rsrc(nullptr, 0u), 0, wid, lane);
   __builtin_amdgcn_sched_barrier(0);
   int k = 0;
   while (true) {
-    load_round<V4>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
-    zero_round<MODE, V4>(out, k, wid, lane);
-    if (!scan_round<V4>(a, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
+    load_round<W, V4>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
+    zero_round<W, MODE, V4>(out, k, wid, lane);
+    if (!scan_round<W, V4>(a, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
     if (++k >= rounds) break;
-    load_round<V4>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
-    zero_round<MODE, V4>(out, k, wid, lane);
-    if (!scan_round<V4>(b, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
+    load_round<W, V4>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
+    zero_round<W, MODE, V4>(out, k, wid, lane);
+    if (!scan_round<W, V4>(b, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
     if (++k >= rounds) break;
   }
   return true;
@@ -1040,7 +1059,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict
     int n = 0;
     float m = -INFINITY, t = -INFINITY;
     bool ok = !o.force_generic;
-    if (ok) ok = stream_row<MODE, V4>(row, r, C, lane, wid, bv, bi, o, n, m, t);
+    if (ok) ok = stream_row<kWavesPerBlock, MODE, V4>(row, r, C, lane, wid, bv, bi, o, n, m, t);
     if (lane == 0) {
       sh.wmax[wid] = m;
       sh.wn[wid] = n;
@@ -1195,6 +1214,193 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict
     }
     __syncthreads();
   }
+  mean_epilogue(bsum, o);
+}
+
+// ------------------------------------------------------------------------------------------------
+// fwl_wave_stream_rows: one wavefront per row for mid-range C.  The row is streamed once (loads
+// one round ahead, zero placeholders for every output), its candidates kept in the wavefront's
+// LDS list, which is then cut at the final bound max - 1 and resolved like a register row; only
+// the support entries and the label are rewritten.  No block-wide barrier: each wavefront runs
+// its own rows, as in fwl_wave_rows.
+
+// fp64 sum and count of the row entries > thr, over the wavefront (fixed order)
+__device__ void wave_row_sum_count(const float* __restrict__ row, int C, float thr, int lane, double& s, int& c) {
+  double acc = 0.0;
+  int cnt = 0;
+  for (int j = lane; j < C; j += kWave) {
+    const float v = row[j];
+    if (v > thr) {
+      acc += (double)v;
+      ++cnt;
+    }
+  }
+  s = wave_sum_f64(acc);
+  c = (int)wave_sum_f64((double)cnt);
+}
+
+// generic solve of one row by one wavefront: fixed-point iterations over the row in memory
+__device__ void wave_generic_solve(const float* __restrict__ row, int C, int lane, float& m, double& tau,
+                                   int& kappa) {
+  float lm = -INFINITY;
+  for (int j = lane; j < C; j += kWave) lm = fmaxf(lm, row[j]);
+  m = wave_max_f32(lm);
+  const float t0 = bound_below_max(m);
+  double t = (double)t0, s;
+  int c;
+  wave_row_sum_count(row, C, t0, lane, s, c);
+  tau = NAN;
+  kappa = 0;
+  if (c == 0) return;
+  for (int it = 0; it <= C + 1; ++it) {
+    const double tn = (s - 1.0) / (double)c;
+    double s2;
+    int c2;
+    wave_row_sum_count(row, C, rd32(tn), lane, s2, c2);
+    if (c2 == c || !(tn > t)) {
+      tau = tn;
+      kappa = c2;
+      break;
+    }
+    t = tn;
+    s = s2;
+    c = c2;
+  }
+  const double tc = clamp_below_max(tau, m);
+  if (tc != tau) {
+    double s3;
+    tau = tc;
+    wave_row_sum_count(row, C, rd32(tau), lane, s3, kappa);
+  }
+}
+
+template <int MODE, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const float* __restrict__ z,
+                                                               const int64_t* __restrict__ tgt, int64_t N,
+                                                               int C, Outs o) {
+  __shared__ float s_val[kWavesPerBlock][kCapMax];
+  __shared__ int s_idx[kWavesPerBlock][kCapMax];
+  __shared__ double s_wsum[kWavesPerBlock];
+  const int lane = lane_id();
+  const int wid = uniform((int)(threadIdx.x >> 6));
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+  const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;   // this wavefront's rows: w + k*stride
+  const int nrows = w < N ? (int)((N - 1 - w) / stride + 1) : 0;   // <= kRowsPerWave (host grid)
+  float* bv = s_val[wid];
+  int* bi = s_idx[wid];
+  const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
+  float my_H = 0.0f, my_loss = 0.0f;
+  int my_kappa = 0;
+  double lsum = 0.0;
+  for (int k = 0; k < nrows; ++k) {
+    const int64_t r = w + (int64_t)k * stride;
+    const float* row = z + r * (int64_t)C;
+    const int64_t y64 = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
+    const bool yok = y64 >= 0 && y64 < C;
+    const int yr = yok ? (int)y64 : -1;
+
+    int n = 0;
+    float m = -INFINITY, t = -INFINITY;
+    const bool ok = !o.force_generic && stream_row<1, MODE, V4>(row, r, C, lane, 0, bv, bi, o, n, m, t);
+    double tau;
+    int kappa;
+    uint64_t support = 0;
+    if (ok) {
+      // keep the entries above the final bound (every support entry is among them)
+      const float tb = bound_below_max(m);
+      int kept = 0;
+      for (int p0 = 0; p0 < n; p0 += kWave) {
+        const int p = p0 + lane;
+        const float v = p < n ? bv[p] : -INFINITY;
+        const int id = p < n ? bi[p] : -1;
+        const bool keep = v > tb;
+        const uint64_t b = ballot(keep);
+        __builtin_amdgcn_wave_barrier();
+        if (keep) {
+          bv[kept + rank_in(b)] = v;
+          bi[kept + rank_in(b)] = id;
+        }
+        kept += __popcll(b);
+        __builtin_amdgcn_wave_barrier();
+      }
+      n = kept;
+      resolve_list(bv, n, tb, m, lane, tau, kappa, support);
+    } else {
+      wave_generic_solve(row, C, lane, m, tau, kappa);
+    }
+    const float Hf = rd32(tau);
+    const float inv = (float)(o.scale / (double)kappa);
+    // this wavefront's zero placeholders have landed before any entry is rewritten
+    wait_vmem();
+    if (ok) {
+      if constexpr (MODE == kGrad || MODE == kMask) {
+        for (int p = lane; p < n; p += kWave) {
+          const int id = bi[p];
+          if (id == yr || !(bv[p] > Hf)) continue;
+          if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + id] = inv;
+          else o.mask[r * (int64_t)C + id] = 1;
+        }
+      } else {
+        int out = 0;
+        for (int p0 = 0; p0 < n; p0 += kWave) {
+          const int p = p0 + lane;
+          const float v = p < n ? bv[p] : -INFINITY;
+          const bool sel = v > Hf;
+          const uint64_t b = ballot(sel);
+          if (sel) {
+            o.cval[r * (int64_t)C + out + rank_in(b)] = v;
+            o.cidx[r * (int64_t)C + out + rank_in(b)] = bi[p];
+          }
+          out += __popcll(b);
+        }
+      }
+    } else {
+      if constexpr (MODE == kGrad) {
+        for (int j = lane; j < C; j += kWave)
+          if (j != yr) o.grad[r * (int64_t)C + j] = row[j] > Hf ? inv : 0.0f;
+      } else if constexpr (MODE == kMask) {
+        for (int j = lane; j < C; j += kWave)
+          if (j != yr) o.mask[r * (int64_t)C + j] = (uint8_t)(row[j] > Hf);
+      } else {
+        int out = 0;
+        for (int j0 = 0; j0 < C; j0 += kWave) {
+          const int j = j0 + lane;
+          const float v = j < C ? row[j] : -INFINITY;
+          const bool sel = v > Hf;
+          const uint64_t b = ballot(sel);
+          if (sel) {
+            o.cval[r * (int64_t)C + out + rank_in(b)] = v;
+            o.cidx[r * (int64_t)C + out + rank_in(b)] = j;
+          }
+          out += __popcll(b);
+        }
+      }
+    }
+    const float zy = yok ? row[yr] : NAN;
+    if (lane == 0 && yok) {
+      if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + yr] = (zy > Hf ? inv : 0.0f) - o.scale_f;
+      else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
+    }
+    const float loss = (float)((1.0 - (double)zy) + tau);
+    lsum += (double)loss;
+    if (lane == k) {
+      my_H = Hf;
+      my_loss = loss;
+      my_kappa = kappa;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (lane < nrows) {
+    const int64_t r = w + (int64_t)lane * stride;
+    if (o.H) o.H[r] = my_H;
+    if (o.loss) o.loss[r] = my_loss;
+    if (o.kappa) o.kappa[r] = my_kappa;
+    if constexpr (MODE == kCand) o.ccnt[r] = my_kappa;
+  }
+  if (lane == 0) s_wsum[wid] = lsum;
+  __syncthreads();
+  const double bsum = (s_wsum[0] + s_wsum[1]) + (s_wsum[2] + s_wsum[3]);
   mean_epilogue(bsum, o);
 }
 
@@ -1395,7 +1601,8 @@ void dispatch_wave(const float* z, const int64_t* y, int64_t N, int C, bool v4, 
   if (v4) {
     if (C <= 256) launch_wave<MODE, 1, true>(z, y, N, C, o, s);
     else if (C <= 512) launch_wave<MODE, 2, true>(z, y, N, C, o, s);
-    else launch_wave<MODE, 4, true>(z, y, N, C, o, s);
+    else if (C <= 1024) launch_wave<MODE, 4, true>(z, y, N, C, o, s);
+    else launch_wave<MODE, 8, true>(z, y, N, C, o, s);
   } else {
     if (C <= 64) launch_wave<MODE, 1, false>(z, y, N, C, o, s);
     else if (C <= 128) launch_wave<MODE, 2, false>(z, y, N, C, o, s);
@@ -1410,6 +1617,20 @@ void launch_block(const float* z, const int64_t* y, int64_t N, int C, const Outs
   const void* k = reinterpret_cast<const void*>(&fwl_block_rows<MODE, V4>);
   const int grid = persistent_grid(N, 1, resident_blocks(k), kMaxBlocksRow);
   hipLaunchKernelGGL((fwl_block_rows<MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+}
+
+template <int MODE, bool V4>
+void launch_wave_stream(const float* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+  const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<MODE, V4>);
+  const int grid = wave_grid(N, C, resident_blocks(k));
+  hipLaunchKernelGGL((fwl_wave_stream_rows<MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+}
+
+template <int MODE>
+void dispatch_wave_stream(const float* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
+                          hipStream_t s) {
+  if (v4) launch_wave_stream<MODE, true>(z, y, N, C, o, s);
+  else launch_wave_stream<MODE, false>(z, y, N, C, o, s);
 }
 
 template <int MODE>
@@ -1435,7 +1656,7 @@ int forward(const float* z, const int64_t* y, int64_t N, int64_t C64, double sca
   o.reduce_div = reduce_div;
   o.scale_f = (float)scale;
   o.cap = g_cap;
-  o.force_generic = g_path == 3;
+  o.force_generic = g_path == 3 || g_path == 5;
   if (o.mean != nullptr) {
     if (ws == nullptr || ws_bytes < fwl_workspace_bytes(N, C64) || !aligned(ws, 8)) return FWL_ERR_WORKSPACE;
     o.ticket = static_cast<unsigned*>(ws);
@@ -1447,9 +1668,13 @@ int forward(const float* z, const int64_t* y, int64_t N, int64_t C64, double sca
   }
   const bool v4 = (C % 4) == 0 && aligned(z, 16) && out_v4_ok;
   int path = g_path;
-  if (path == 0) path = C <= kMaxWaveC ? 1 : 2;
-  if (path == 1 && C > kMaxWaveC) path = 2;
+  // measured on MI355X: registers win up to 2048 for 128-bit rows, up to 1024 for 32-bit rows;
+  // one streaming wavefront per row up to 8192; one block per row beyond
+  const int max_wave_c = v4 ? kMaxWaveC : kMaxWaveC1;
+  if (path == 0) path = C <= max_wave_c ? 1 : (C <= kMaxStreamC ? 4 : 2);
+  if (path == 1 && C > max_wave_c) path = 4;
   if (path == 1) dispatch_wave<MODE>(z, y, N, C, v4, o, s);
+  else if (path == 4 || path == 5) dispatch_wave_stream<MODE>(z, y, N, C, v4, o, s);
   else dispatch_block<MODE>(z, y, N, C, v4, o, s);
   return launch_status();
 }
@@ -1593,7 +1818,7 @@ int fwl_scale_grad(float* grad, const float* grad_output, int64_t go_stride, int
 }
 
 int fwl_set_params(int path, int cand_cap) {
-  if (path < 0 || path > 3 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
+  if (path < 0 || path > 5 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
   g_path = path;
   g_cap = cand_cap;
   return FWL_OK;

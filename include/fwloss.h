@@ -110,10 +110,16 @@ int fwl_scale_grad(float* grad, const float* grad_output, int64_t go_stride, int
 /* Process-wide dispatch switches, the GPU counterpart of the reference CPU path's set_params
  * (src/cpu/fw_cpu.cpp:758-763, used by its tests to force each branch).  Not thread-safe; meant
  * for tests and tuning.
- *   path:      0 = automatic, 1 = one wavefront per row (C <= 1024 only), 2 = one block per row
- *              with LDS candidate compaction, 3 = the generic multi-pass block path.
- *   cand_cap:  LDS candidate capacity per wavefront of path 2, in [64, 512] (512 = default);
- *              smaller values make rows overflow into the generic path sooner.
+ *   path:      0 = automatic (1 for C <= 2048, or C <= 1024 when rows are not 16-byte aligned;
+ *              4 for C <= 8192; else 2),
+ *              1 = one wavefront per row with the row in registers (C <= 2048, or 1024 for rows
+ *              that are not 16-byte aligned; larger C runs path 4),
+ *              2 = one block per row, streamed, with LDS candidate lists,
+ *              3 = path 2 with the generic multi-pass solve forced,
+ *              4 = one wavefront per row, streamed, with an LDS candidate list,
+ *              5 = path 4 with the generic multi-pass solve forced.
+ *   cand_cap:  LDS candidate capacity per wavefront of paths 2 and 4, in [64, 512] (512 =
+ *              default); smaller values make rows overflow into the generic solve sooner.
  * Returns FWL_ERR_INVALID_ARG for values out of range. */
 int fwl_set_params(int path, int cand_cap);
 int fwl_get_params(int* path, int* cand_cap);

@@ -58,21 +58,32 @@ def reset_params(ext):
 
 # ---------------------------------------------------------------- seeded configurations (reduced N)
 
-REDUCED = {"cfg1": 1024, "cfg2": 2048, "cfg3": 16384, "cfg4": 96, "cfg5": 24}
+REDUCED = {"cfg1": 1024, "cfg2": 2048, "cfg3": 16384, "cfg4": 96, "cfg5": 24, "mid3000": 256, "mid2999": 256}
+
+
+def make_case(name, N, seed):
+    """A seeded configuration, or "mid<C>": mid-range C rows (N(0,1), every 5th row flat)."""
+    if name.startswith("mid"):
+        C = int(name[3:])
+        rng = np.random.default_rng(seed)
+        z = rng.standard_normal((N, C)).astype(np.float32)
+        z[::5] *= np.float32(0.02)
+        return z, rng.integers(0, C, N)
+    return data.make(name, N=N, seed=seed)
 
 
 @pytest.mark.parametrize("cfg", sorted(REDUCED))
 def test_fused_matches_oracle(ext, dev, cfg):
-    z, y = data.make(cfg, N=REDUCED[cfg], seed=1)
+    z, y = make_case(cfg, REDUCED[cfg], 1)
     print(f"fused {cfg} N={z.shape[0]} C={z.shape[1]}", flush=True)
     ref = oracle.definition(z, y)
     out = fused(ext, *to_dev(dev, z, y))
     assert_parity(out, ref, z)
 
 
-@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3", "cfg4"])
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3", "cfg4", "mid3000", "mid2999"])
 def test_drop_in_small_ops(ext, dev, cfg):
-    z, y = data.make(cfg, N=min(REDUCED[cfg], 512), seed=2)
+    z, y = make_case(cfg, min(REDUCED[cfg], 512), 2)
     print(f"small ops {cfg} N={z.shape[0]}", flush=True)
     zt, yt = to_dev(dev, z, y)
     H, losses, mean, kappa, sel = ext.fw_forward_small(zt, yt)
@@ -87,9 +98,9 @@ def test_drop_in_small_ops(ext, dev, cfg):
     assert_parity(out, ref, z)
 
 
-@pytest.mark.parametrize("cfg", ["cfg2", "cfg3", "cfg4", "cfg5"])
+@pytest.mark.parametrize("cfg", ["cfg2", "cfg3", "cfg4", "cfg5", "mid3000", "mid2999"])
 def test_drop_in_large_ops(ext, dev, cfg):
-    z, y = data.make(cfg, N=min(REDUCED[cfg], 256), seed=3)
+    z, y = make_case(cfg, min(REDUCED[cfg], 256), 3)
     print(f"large ops {cfg} N={z.shape[0]}", flush=True)
     zt, yt = to_dev(dev, z, y)
     H, losses, mean, kappa, cbuf, cidx, ccnt = ext.fw_forward(zt, yt)
@@ -110,8 +121,8 @@ def test_drop_in_large_ops(ext, dev, cfg):
 
 # ---------------------------------------------------------------- every kernel path, same answers
 
-@pytest.mark.parametrize("path,cap", [(1, 512), (2, 512), (2, 64), (3, 512)])
-@pytest.mark.parametrize("C", [10, 100, 1000, 1024])
+@pytest.mark.parametrize("path,cap", [(1, 512), (2, 512), (2, 64), (3, 512), (4, 512), (4, 64), (5, 512)])
+@pytest.mark.parametrize("C", [10, 100, 1000, 1024, 2999, 3000])
 def test_forced_paths(ext, dev, reset_params, path, cap, C):
     rng = np.random.default_rng(C)
     z = rng.standard_normal((300, C)).astype(np.float32)
@@ -125,8 +136,9 @@ def test_forced_paths(ext, dev, reset_params, path, cap, C):
     assert_parity(out, ref, z)
 
 
+@pytest.mark.parametrize("path", [2, 4])
 @pytest.mark.parametrize("cap", [64, 512])
-def test_block_path_overflow_and_tighten(ext, dev, reset_params, cap):
+def test_streamed_overflow_and_tighten(ext, dev, reset_params, path, cap):
     # C = 4096 rows: a flat row overflows any list (generic path), a row with many candidates but a
     # short support exercises list tightening
     rng = np.random.default_rng(7)
@@ -137,15 +149,16 @@ def test_block_path_overflow_and_tighten(ext, dev, reset_params, cap):
     z[2, :] = np.float32(1e-3) * rng.standard_normal(C).astype(np.float32)
     z[3, ::2] = 5.0
     y = rng.integers(0, C, 64)
-    print(f"block overflow cap={cap}", flush=True)
-    ext.set_params(2, cap)
+    print(f"streamed overflow path={path} cap={cap}", flush=True)
+    ext.set_params(path, cap)
     ref = oracle.definition(z, y)
     assert_parity(fused(ext, *to_dev(dev, z, y)), ref, z)
 
 
 # ---------------------------------------------------------------- shapes, layouts, special values
 
-@pytest.mark.parametrize("C", [1, 2, 3, 5, 10, 37, 63, 64, 65, 255, 257, 999, 1001, 1023, 1025, 2049, 5000, 10001])
+@pytest.mark.parametrize("C", [1, 2, 3, 5, 10, 37, 63, 64, 65, 255, 257, 999, 1001, 1023, 1025, 2049, 5000, 10001,
+                               16384, 16385, 20000])
 def test_shapes(ext, dev, C):
     rng = np.random.default_rng(C + 11)
     N = 67
