@@ -34,9 +34,13 @@ METRIC = "rows/sec and achieved HBM GB/s (% of peak), fwd+bwd, N=65536 C=1000 fp
 HBM_PEAK_GBS = 8000.0
 
 
-def alg_bytes(N, C):
-    # logits read once + gradient written once + int64 labels + H, loss (f32) and kappa (i32)
-    return 8 * N * C + 8 * N + 12 * N
+ELEM_BYTES = {"f32": 4, "bf16": 2, "f16": 2}
+
+
+def alg_bytes(N, C, elem=4):
+    # logits read once + gradient written once (the logits' element type) + int64 labels + H, loss
+    # (f32) and kappa (i32)
+    return 2 * elem * N * C + 8 * N + 12 * N
 
 
 def parse():
@@ -46,6 +50,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
     ap.add_argument("--sets", type=int, default=3, help="rotated input/output buffer sets")
+    ap.add_argument("--dtype", default="f32", choices=["f32", "bf16", "f16"],
+                    help="element type of the logits and the gradient (decisions are fp32/fp64)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--copy-probe", action="store_true",
@@ -135,9 +141,10 @@ def main():
     dev = torch.device("cuda:0")
     z_np, y_np = fwloss_data.make(args.config, seed=0)
     N, C = z_np.shape
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[args.dtype]
     sets = []
     for s in range(args.sets):
-        zt = torch.from_numpy(z_np).to(dev) if s == 0 else sets[0][0].roll(s, dims=0).contiguous()
+        zt = torch.from_numpy(z_np).to(dev).to(tdt) if s == 0 else sets[0][0].roll(s, dims=0).contiguous()
         yt = torch.from_numpy(y_np).to(dev) if s == 0 else sets[0][1].roll(s, dims=0).contiguous()
         sets.append((zt, yt))
     torch.cuda.synchronize()
@@ -165,25 +172,28 @@ def main():
     wall = time.perf_counter() - t0
     kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
     ms_per_step = wall * 1e3 / args.steps
-    nbytes = alg_bytes(N, C)
+    nbytes = alg_bytes(N, C, ELEM_BYTES[args.dtype])
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
 
-    # the reference's two-op sequence (fw_forward_small + fw_backward_small), for comparison
+    # the reference's two-op sequence (fw_forward_small + fw_backward_small; fp32 only), for comparison
     def two_op(i):
         zt, yt = sets[i % len(sets)]
         H, losses, mean, kappa, sel = fwloss.fw_forward_small(zt, yt)
         return fwloss.fw_backward_small(yt, sel, kappa)
-    for i in range(5):
-        two_op(i)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    for i in range(args.steps):
-        two_op(i)
-    torch.cuda.synchronize()
-    two_op_ms = (time.perf_counter() - t1) * 1e3 / args.steps
+    two_op_ms = None
+    if args.dtype == "f32":
+        for i in range(5):
+            two_op(i)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for i in range(args.steps):
+            two_op(i)
+        torch.cuda.synchronize()
+        two_op_ms = (time.perf_counter() - t1) * 1e3 / args.steps
 
-    tag = "fwl_wave_rows" if C <= 1024 else "fwl_block_rows"
-    traffic = traffic_for(tag, args.config)
+    # the kernel the automatic dispatch runs for this row length (16-byte aligned rows)
+    tag = "fwl_wave_rows" if C <= 2048 else ("fwl_wave_stream_rows" if C <= 8192 else "fwl_block_rows")
+    traffic = traffic_for(tag, args.config if args.dtype == "f32" else f"{args.config}_{args.dtype}")
     result = {
         "metric": METRIC,
         "value": N * args.steps / wall,
@@ -195,9 +205,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": args.dtype,
         "data": "synthetic",
-        "config": {"workload": f"{args.config} fused FW loss forward+backward, N={N} C={C} fp32 logits N(0,1) "
+        "config": {"workload": f"{args.config} fused FW loss forward+backward, N={N} C={C} {args.dtype} logits "
                                "(fwloss_data.make), labels uniform int64, buffers rotated over "
                                f"{args.sets} sets", "N": N, "C": C, "op": "fw_forward_backward",
                    "parallelism": "single GPU"},
@@ -208,7 +218,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": tag, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "alg_bytes": nbytes},
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.dtype == "f32":
         result["cpu_baseline"] = cpu_baseline(z_np, y_np, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

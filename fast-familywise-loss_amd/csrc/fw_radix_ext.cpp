@@ -74,16 +74,37 @@ struct Common {
   at::Tensor logits, targets, H, losses, mean, kappa, ws;
 };
 
-Common prepare(const at::Tensor& logits_in, const at::Tensor& targets_in) {
-  check_logits(logits_in);
+// element type of 16-bit or fp32 logits for the typed entry points
+int fwl_dtype_of(const at::Tensor& t) {
+  switch (t.scalar_type()) {
+    case torch::kFloat32: return FWL_FLOAT32;
+    case torch::kBFloat16: return FWL_BFLOAT16;
+    case torch::kFloat16: return FWL_FLOAT16;
+    default: TORCH_CHECK(false, "logits must be float32, bfloat16 or float16");
+  }
+  return -1;
+}
+
+// checks, contiguous copies and the fp32/int32 per-row outputs; the reference ops take fp32
+// logits only, the fused op also 16-bit ones
+Common prepare(const at::Tensor& logits_in, const at::Tensor& targets_in, bool any_float = false) {
+  if (any_float) {
+    TORCH_CHECK(logits_in.is_cuda(), "logits must be a CUDA tensor");
+    TORCH_CHECK(logits_in.dim() == 2, "logits must have shape [N, K]");
+    fwl_dtype_of(logits_in);
+    TORCH_CHECK(logits_in.size(1) >= 1, "logits must have K >= 1 classes");
+  } else {
+    check_logits(logits_in);
+  }
   check_rows(targets_in, logits_in, torch::kInt64, "targets");
   Common c;
   c.logits = logits_in.contiguous();
   c.targets = targets_in.contiguous();
   const int64_t N = c.logits.size(0), K = c.logits.size(1);
-  c.H = torch::empty({N}, c.logits.options());
-  c.losses = torch::empty({N}, c.logits.options());
-  c.mean = torch::empty({}, c.logits.options());
+  const auto f32 = c.logits.options().dtype(torch::kFloat32);
+  c.H = torch::empty({N}, f32);
+  c.losses = torch::empty({N}, f32);
+  c.mean = torch::empty({}, f32);
   c.kappa = torch::empty({N}, c.logits.options().dtype(torch::kInt32));
   c.ws = workspace(c.logits, fwl_workspace_bytes(N, K));
   return c;
@@ -166,19 +187,20 @@ at::Tensor fw_backward(at::Tensor logits, at::Tensor targets, at::Tensor H, at::
 }
 
 // fw_forward_backward(logits, targets, scale=1/N, reduce_div=N) -> [H, losses, reduced, kappa, grad]
-// The fused hot path: one launch, logits read once, dense gradient written once.
+// The fused hot path: one launch, logits read once, dense gradient written once.  Logits may be
+// float32, bfloat16 or float16; grad has the logits' dtype, H, losses and reduced are float32.
 std::vector<at::Tensor> fw_forward_backward(at::Tensor logits, at::Tensor targets, double scale,
                                             double reduce_div) {
   c10::DeviceGuard guard(logits.device());
-  Common c = prepare(logits, targets);
+  Common c = prepare(logits, targets, true);
   const int64_t N = c.logits.size(0), K = c.logits.size(1);
   if (scale < 0) scale = N > 0 ? 1.0 / (double)N : 1.0;
   if (reduce_div < 0) reduce_div = (double)N;
   at::Tensor grad = torch::empty({N, K}, c.logits.options());
-  const int rc = fwl_forward_backward(
-      c.logits.data_ptr<float>(), c.targets.data_ptr<int64_t>(), N, K, scale, reduce_div,
+  const int rc = fwl_forward_backward_typed(
+      fwl_dtype_of(c.logits), c.logits.data_ptr(), c.targets.data_ptr<int64_t>(), N, K, scale, reduce_div,
       c.H.data_ptr<float>(), c.losses.data_ptr<float>(), c.mean.data_ptr<float>(),
-      c.kappa.data_ptr<int32_t>(), grad.data_ptr<float>(), c.ws.data_ptr(), (size_t)c.ws.numel(),
+      c.kappa.data_ptr<int32_t>(), grad.data_ptr(), c.ws.data_ptr(), (size_t)c.ws.numel(),
       current_stream(c.logits));
   check_status(rc, "fw_forward_backward");
   return {c.H, c.losses, c.mean, c.kappa, grad};
@@ -187,8 +209,9 @@ std::vector<at::Tensor> fw_forward_backward(at::Tensor logits, at::Tensor target
 // grad *= grad_output (a 0-dim factor, or one factor per row), in place; rows whose factor is 1
 // are skipped on the device (src/cpu/fw_cpu.cpp:734-740)
 at::Tensor fw_scale_grad(at::Tensor grad, at::Tensor grad_output) {
-  TORCH_CHECK(grad.is_cuda() && grad.dim() == 2 && grad.scalar_type() == torch::kFloat32 && grad.is_contiguous(),
-              "grad must be a contiguous float32 CUDA tensor [N, K]");
+  TORCH_CHECK(grad.is_cuda() && grad.dim() == 2 && grad.is_contiguous(),
+              "grad must be a contiguous CUDA tensor [N, K]");
+  const int dtype = fwl_dtype_of(grad);
   c10::DeviceGuard guard(grad.device());
   TORCH_CHECK(grad_output.device() == grad.device(), "grad_output must be on the device of grad");
   at::Tensor go = grad_output.to(torch::kFloat32).contiguous();
@@ -198,8 +221,8 @@ at::Tensor fw_scale_grad(at::Tensor grad, at::Tensor grad_output) {
     TORCH_CHECK(go.dim() == 1 && go.size(0) == grad.size(0), "grad_output must be a scalar or have shape [N]");
     stride = 1;
   }
-  const int rc = fwl_scale_grad(grad.data_ptr<float>(), go.data_ptr<float>(), stride, grad.size(0), grad.size(1),
-                                current_stream(grad));
+  const int rc = fwl_scale_grad_typed(dtype, grad.data_ptr(), go.data_ptr<float>(), stride, grad.size(0),
+                                      grad.size(1), current_stream(grad));
   check_status(rc, "fw_scale_grad");
   return grad;
 }

@@ -39,6 +39,7 @@
 #include <stdint.h>
 
 #include <map>
+#include <type_traits>
 #include <mutex>
 #include <utility>
 
@@ -58,6 +59,121 @@ constexpr int kRsrcFlags = 0x00020000;
 constexpr int kNonTemporal = 2;   // cache-policy bits of the buffer instructions: nt
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kRsrcFlags);
+}
+
+// Element types of the logits (and of the gradient of the fused op): float, or the 16-bit tags
+// below.  Values are widened to fp32 exactly when loaded; every decision is taken in fp32/fp64;
+// gradient values are computed in fp32 and rounded to nearest-even when stored.
+struct bf16_t {};   // bfloat16, stored as uint16
+struct f16_t {};    // IEEE binary16, stored as uint16
+template <typename T> constexpr int kElemBytes = 2;
+template <> constexpr int kElemBytes<float> = 4;
+template <typename T> using Storage = typename std::conditional<std::is_same<T, float>::value, float, uint16_t>::type;
+
+// elements per lane access: a 128-bit unit (VEC) or a single element
+template <typename T, bool VEC> constexpr int kUnit = VEC ? 16 / kElemBytes<T> : 1;
+
+template <typename T>
+__device__ __forceinline__ float widen16(uint32_t h) {
+  if constexpr (std::is_same<T, bf16_t>::value) return __uint_as_float(h << 16);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t narrow16(float f) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;   // NaN stays NaN (quiet)
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;                     // round to nearest even
+  } else {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+}
+
+// unit `u` of a row (elements kUnit*u ...) as fp32; offsets past the resource read 0
+template <typename T, bool VEC>
+__device__ __forceinline__ void load_unit(rsrc_t r, uint32_t u, float* out) {
+  if constexpr (VEC) {
+    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, 16u * u, 0, kNonTemporal);
+    if constexpr (std::is_same<T, float>::value) {
+      out[0] = __uint_as_float(v.x);
+      out[1] = __uint_as_float(v.y);
+      out[2] = __uint_as_float(v.z);
+      out[3] = __uint_as_float(v.w);
+    } else {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out[2 * i] = widen16<T>(w[i] & 0xFFFFu);
+        out[2 * i + 1] = widen16<T>(w[i] >> 16);
+      }
+    }
+  } else if constexpr (std::is_same<T, float>::value) {
+    out[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, 4u * u, 0, kNonTemporal));
+  } else {
+    out[0] = widen16<T>(__builtin_amdgcn_raw_buffer_load_b16(r, 2u * u, 0, kNonTemporal));
+  }
+}
+
+// store unit `u` (kUnit values, rounded to T); offsets past the resource are dropped
+template <typename T, bool VEC>
+__device__ __forceinline__ void store_unit(rsrc_t r, uint32_t u, const float* v) {
+  if constexpr (VEC) {
+    v4u w;
+    if constexpr (std::is_same<T, float>::value) {
+      w = v4u{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+    } else {
+      w = v4u{narrow16<T>(v[0]) | (narrow16<T>(v[1]) << 16), narrow16<T>(v[2]) | (narrow16<T>(v[3]) << 16),
+              narrow16<T>(v[4]) | (narrow16<T>(v[5]) << 16), narrow16<T>(v[6]) | (narrow16<T>(v[7]) << 16)};
+    }
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, 16u * u, 0, kNonTemporal);
+  } else if constexpr (std::is_same<T, float>::value) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, 4u * u, 0, kNonTemporal);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)narrow16<T>(v[0]), r, 2u * u, 0, kNonTemporal);
+  }
+}
+
+// bit pattern of an fp32 value in element type T (16-bit types: in the low half)
+template <typename T>
+__device__ __forceinline__ uint32_t encode(float f) {
+  if constexpr (std::is_same<T, float>::value) return __float_as_uint(f);
+  else return narrow16<T>(f);
+}
+
+// store unit `u` from already-encoded element bit patterns
+template <typename T, bool VEC>
+__device__ __forceinline__ void store_unit_bits(rsrc_t r, uint32_t u, const uint32_t* b) {
+  if constexpr (VEC) {
+    v4u w;
+    if constexpr (std::is_same<T, float>::value) w = v4u{b[0], b[1], b[2], b[3]};
+    else w = v4u{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, 16u * u, 0, kNonTemporal);
+  } else if constexpr (std::is_same<T, float>::value) {
+    __builtin_amdgcn_raw_buffer_store_b32(b[0], r, 4u * u, 0, kNonTemporal);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)b[0], r, 2u * u, 0, kNonTemporal);
+  }
+}
+
+// a zero unit (all-zero bits are +0 in every element type)
+template <typename T, bool VEC>
+__device__ __forceinline__ void store_zero_unit(rsrc_t r, uint32_t u) {
+  if constexpr (VEC) __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, r, 16u * u, 0, kNonTemporal);
+  else if constexpr (std::is_same<T, float>::value) __builtin_amdgcn_raw_buffer_store_b32(0u, r, 4u * u, 0, kNonTemporal);
+  else __builtin_amdgcn_raw_buffer_store_b16((uint16_t)0, r, 2u * u, 0, kNonTemporal);
+}
+
+// scalar element access through plain pointers (element index j)
+template <typename T>
+__device__ __forceinline__ float load_elem(const void* base, int64_t j) {
+  if constexpr (std::is_same<T, float>::value) return static_cast<const float*>(base)[j];
+  else return widen16<T>(static_cast<const uint16_t*>(base)[j]);
+}
+template <typename T>
+__device__ __forceinline__ void store_elem(void* base, int64_t j, float v) {
+  if constexpr (std::is_same<T, float>::value) static_cast<float*>(base)[j] = v;
+  else static_cast<uint16_t*>(base)[j] = (uint16_t)narrow16<T>(v);
 }
 
 constexpr int kWave = 64;
@@ -80,7 +196,7 @@ struct Outs {
   float* loss;
   int32_t* kappa;
   float* mean;
-  float* grad;
+  void* grad;   // element type of the logits
   uint8_t* mask;
   float* cval;
   int32_t* cidx;
@@ -361,50 +477,35 @@ __device__ void mean_epilogue(double bsum, const Outs& o) {
 // ------------------------------------------------------------------------------------------------
 // fwl_wave_rows: one wavefront per row, C <= 64 * E (E elements per lane)
 
-template <int NV, bool V4>
+// Register rows: lane `lane` holds units lane + 64*k, k < NV, i.e. E = kUnit*NV elements in
+// slots kUnit*k + e.
+template <typename T, int NV, bool VEC>
 __device__ __forceinline__ void load_row(rsrc_t row, int lane, float* x) {
   // all lanes load unconditionally; offsets past the row (or a zero-size resource: no row) read 0
-  if constexpr (V4) {
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(row, 16 * (lane + kWave * k), 0, kNonTemporal));
-      x[4 * k + 0] = v.x;
-      x[4 * k + 1] = v.y;
-      x[4 * k + 2] = v.z;
-      x[4 * k + 3] = v.w;
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < NV; ++k)
-      x[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(row, 4 * (lane + kWave * k), 0, kNonTemporal));
-  }
+  for (int k = 0; k < NV; ++k) load_unit<T, VEC>(row, (uint32_t)(lane + kWave * k), x + kUnit<T, VEC> * k);
 }
 
-// set the register slots past the row end to -inf (only the last partial slots need it)
-template <int NV, bool V4>
+// set the register slots past the row end to -inf (only the last partial units need it)
+template <typename T, int NV, bool VEC>
 __device__ __forceinline__ void mask_tail(float* x, int C, int lane) {
-  if constexpr (V4) {
-    const int nvec = C >> 2;
+  constexpr int U = kUnit<T, VEC>;
+  const int units = C / U;   // C is a multiple of U
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      if (kWave * (k + 1) > nvec) {
-        const bool ok = lane + kWave * k < nvec;
+  for (int k = 0; k < NV; ++k) {
+    if (kWave * (k + 1) > units) {
+      const bool ok = lane + kWave * k < units;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[4 * k + e] = ok ? x[4 * k + e] : -INFINITY;
-      }
+      for (int e = 0; e < U; ++e) x[U * k + e] = ok ? x[U * k + e] : -INFINITY;
     }
-  } else {
-#pragma unroll
-    for (int k = 0; k < NV; ++k)
-      if (kWave * (k + 1) > C) x[k] = lane + kWave * k < C ? x[k] : -INFINITY;
   }
 }
 
 // element index of register slot i of this lane
-template <bool V4>
+template <typename T, bool VEC>
 __device__ __forceinline__ int slot_index(int i, int lane) {
-  if constexpr (V4) return 4 * (lane + kWave * (i >> 2)) + (i & 3);
-  else return lane + kWave * i;
+  constexpr int U = kUnit<T, VEC>;
+  return U * (lane + kWave * (i / U)) + (i % U);
 }
 
 // sum/count over the first n entries of one wavefront's list, entries > thr
@@ -423,27 +524,14 @@ __device__ __forceinline__ void list_sum_count(const float* bv, int n, float thr
   c = cnt;
 }
 
-// element j of the register row (j wavefront-uniform, 0 <= j < C)
-template <int NV, bool V4>
+// element j of the register row (j wavefront-uniform, 0 <= j < C): the uniform slot index makes
+// the register array access an indexed register move (s_set_gpr_idx), then one lane read
+template <typename T, int NV, bool VEC>
 __device__ __forceinline__ float element_at(const float* x, int j) {
-  constexpr int E = V4 ? 4 * NV : NV;
-  int slot, owner;
-  if constexpr (V4) {
-    slot = 4 * ((j >> 2) >> 6) + (j & 3);
-    owner = (j >> 2) & 63;
-  } else {
-    slot = j >> 6;
-    owner = j & 63;
-  }
-  // read the owner lane of every slot and pick with scalar selects (a vector select chain would be
-  // turned back into a dynamically indexed array, which lives in scratch memory)
-  int v = __builtin_amdgcn_readlane(__float_as_int(x[0]), owner);
-#pragma unroll
-  for (int i = 1; i < E; ++i) {
-    const int w = __builtin_amdgcn_readlane(__float_as_int(x[i]), owner);
-    v = i == slot ? w : v;
-  }
-  return __int_as_float(v);
+  constexpr int U = kUnit<T, VEC>;
+  const int slot = uniform(U * ((j / U) >> 6) + (j % U));
+  const int owner = uniform((j / U) & 63);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[slot]), owner));
 }
 
 // exclusive prefix sum of v over the wavefront; `total` receives the sum of all lanes
@@ -515,14 +603,16 @@ constexpr int kRowsPerWave = kWave;   // rows of one wavefront per launch (label
 // One row: x holds it (E values per lane).  Once its candidates are in the LDS list, the loads of
 // the next row (resource `next`, zero-size if there is none) are issued into x, so they are in
 // flight during the selection and the stores of this row; no second row buffer is needed.
-template <int MODE, int NV, bool V4>
+template <typename T, int MODE, int NV, bool V4>
 __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t y64, int C, int lane,
                                                  float* x, float* cl, int* ci_lds, const Outs& o) {
-  constexpr int E = V4 ? 4 * NV : NV;
+  constexpr int U = kUnit<T, V4>;
+  constexpr int E = U * NV;
   static_assert(E <= 32, "one mask bit per register slot");
+  static_assert(std::is_same<T, float>::value || MODE == kGrad, "16-bit logits: fused op only");
   const bool yok = y64 >= 0 && y64 < C;
   const int yr = yok ? (int)y64 : -1;
-  mask_tail<NV, V4>(x, C, lane);
+  mask_tail<T, NV, V4>(x, C, lane);
 
   // row maximum and the first lower bound max - 1 (rounded down: every support entry passes)
   float lm = x[0];
@@ -544,13 +634,13 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
       const int bit = (cm >> i) & 1;
       const int at = bit ? pos : E * kWave + lane;
       cl[at] = x[i];
-      if constexpr (MODE == kCand) ci_lds[at] = slot_index<V4>(i, lane);
+      if constexpr (MODE == kCand) ci_lds[at] = slot_index<T, V4>(i, lane);
       pos += bit;
     }
   }
-  const float zy = yok ? element_at<NV, V4>(x, yr) : NAN;
+  const float zy = yok ? element_at<T, NV, V4>(x, yr) : NAN;
   __builtin_amdgcn_wave_barrier();
-  load_row<NV, V4>(next, lane, x);
+  load_row<T, NV, V4>(next, lane, x);
 
   double tau;
   int kappa;
@@ -582,33 +672,22 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
 
   const float inv = (float)(o.scale / (double)kappa);
   if constexpr (MODE == kGrad) {
-    const rsrc_t out = make_rsrc(o.grad + r * (int64_t)C, 4u * (uint32_t)C);
-    if constexpr (V4) {
-      const int qy = yr >> 2, ky = yr >= 0 ? qy >> 6 : -1, ly = qy & 63, ey = yr & 3;
+    const rsrc_t out = make_rsrc(static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>,
+                                 (uint32_t)(kElemBytes<T> * C));
+    const int qy = yr / U, ky = yr >= 0 ? qy >> 6 : -1, ly = qy & 63, ey = yr % U;
+    // the four values a gradient element can take, encoded once per row
+    const uint32_t b_inv = encode<T>(inv), b_lab_in = encode<T>(inv - o.scale_f);
+    const uint32_t b_lab_out = encode<T>(0.0f - o.scale_f);
 #pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        const unsigned b4 = (sm >> (4 * k)) & 0xFu;
-        v4f g;
-        g.x = (b4 & 1u) ? inv : 0.0f;
-        g.y = (b4 & 2u) ? inv : 0.0f;
-        g.z = (b4 & 4u) ? inv : 0.0f;
-        g.w = (b4 & 8u) ? inv : 0.0f;
-        if (k == ky && lane == ly) {
-          if (ey == 0) g.x -= o.scale_f;
-          else if (ey == 1) g.y -= o.scale_f;
-          else if (ey == 2) g.z -= o.scale_f;
-          else g.w -= o.scale_f;
-        }
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, g), out, 16 * (lane + kWave * k), 0, kNonTemporal);
-      }
-    } else {
-      const int ky = yr >= 0 ? yr >> 6 : -1, ly = yr & 63;
+    for (int k = 0; k < NV; ++k) {
+      uint32_t g[U];
 #pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        float g = ((sm >> k) & 1u) ? inv : 0.0f;
-        if (k == ky && lane == ly) g -= o.scale_f;
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(g), out, 4 * (lane + kWave * k), 0, kNonTemporal);
+      for (int e = 0; e < U; ++e) g[e] = ((sm >> (U * k + e)) & 1u) ? b_inv : 0u;
+      if (k == ky && lane == ly) {
+#pragma unroll
+        for (int e = 0; e < U; ++e) g[e] = e == ey ? (((sm >> (U * k + e)) & 1u) ? b_lab_in : b_lab_out) : g[e];
       }
+      store_unit_bits<T, V4>(out, (uint32_t)(lane + kWave * k), g);
     }
   } else if constexpr (MODE == kMask) {
     const rsrc_t out = make_rsrc(o.mask + r * (int64_t)C, (uint32_t)C);
@@ -655,17 +734,12 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
 // first row's loads so that the wait counts at the top of the row loop are the same on entry as on
 // every later iteration (4 row loads followed by the row's stores); with a different mix on entry
 // the compiler waits for every outstanding store at the top of each row.
-template <int MODE, int NV, bool V4>
+template <typename T, int MODE, int NV, bool V4>
 __device__ __forceinline__ void mirror_row_stores(int lane) {
   const rsrc_t none = make_rsrc(nullptr, 0u);
   if constexpr (MODE == kGrad) {
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      if constexpr (V4)
-        __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, none, 16 * (lane + kWave * k), 0, kNonTemporal);
-      else
-        __builtin_amdgcn_raw_buffer_store_b32(0u, none, 4 * (lane + kWave * k), 0, kNonTemporal);
-    }
+    for (int k = 0; k < NV; ++k) store_zero_unit<T, V4>(none, (uint32_t)(lane + kWave * k));
   } else if constexpr (MODE == kMask) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -678,11 +752,11 @@ __device__ __forceinline__ void mirror_row_stores(int lane) {
 // A wavefront handles rows w + k*stride, k < nrows <= 64.  Their labels arrive in one gather load
 // before the first row, and their H, loss and kappa stay in registers (row k in lane k) until the
 // last row, so the only memory instructions inside the row loop are the row loads and stores.
-template <int MODE, int NV, bool V4>
-__global__ __launch_bounds__(kBlock) void fwl_wave_rows(const float* __restrict__ z,
+template <typename T, int MODE, int NV, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__ z,
                                                         const int64_t* __restrict__ tgt, int64_t N,
                                                         int C, Outs o) {
-  constexpr int E = V4 ? 4 * NV : NV;
+  constexpr int E = kUnit<T, V4> * NV;
   constexpr int kListFloats = (E + 1) * kWave;   // a whole register row, then one spare slot per lane
   constexpr int kIdx = MODE == kCand ? kListFloats : 1;
   __shared__ float s_list[kWavesPerBlock][kListFloats];
@@ -693,9 +767,10 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const float* __restrict_
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
   const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;   // this wavefront's rows: w + k*stride
   const int nrows = w < N ? (int)((N - 1 - w) / stride + 1) : 0;   // <= kRowsPerWave (host grid)
-  const uint32_t row_bytes = 4u * (uint32_t)C;
+  const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
   auto row_rsrc = [&](int k) {
-    return k < nrows ? make_rsrc(z + (w + (int64_t)k * stride) * C, row_bytes) : make_rsrc(z, 0u);
+    return k < nrows ? make_rsrc(static_cast<const char*>(z) + (w + (int64_t)k * stride) * C * kElemBytes<T>, row_bytes)
+                     : make_rsrc(z, 0u);
   };
   const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
   float my_H = 0.0f, my_loss = 0.0f;
@@ -703,15 +778,15 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const float* __restrict_
   double lsum = 0.0;
   float x[E];
   if (nrows > 0) {
-    load_row<NV, V4>(row_rsrc(0), lane, x);
+    load_row<T, NV, V4>(row_rsrc(0), lane, x);
     __builtin_amdgcn_sched_barrier(0);   // keep the mirror stores after the loads
-    mirror_row_stores<MODE, NV, V4>(lane);
+    mirror_row_stores<T, MODE, NV, V4>(lane);
     __builtin_amdgcn_sched_barrier(0);
     int k = 0;
     do {
       const int64_t y = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
                         (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
-      const RowResult res = process_row<MODE, NV, V4>(w + (int64_t)k * stride, row_rsrc(k + 1), y, C, lane, x,
+      const RowResult res = process_row<T, MODE, NV, V4>(w + (int64_t)k * stride, row_rsrc(k + 1), y, C, lane, x,
                                                       s_list[wid], s_idx[wid], o);
       lsum += (double)res.loss;
       if (lane == k) {
@@ -788,94 +863,66 @@ __device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, in
 }
 
 // Streaming rounds.  A row is shared by W wavefronts (W = 4: one block per row; W = 1: one
-// wavefront per row).  In round `round`, slot group u of a lane covers unit
+// wavefront per row).  In round `round`, access group u of a lane covers unit
 //     (W > 1 ? wid*64 : 0) + lane + 64*W*(round*PER + u)
-// where a unit is a float4 (128-bit access, PER = kStreamUnroll, slot 4u+e = element 4*unit + e)
-// or a single element (PER = kRoundSlotsV1, slot u = element unit).
+// where a unit is kUnit<T, VEC> elements (a 128-bit access, PER = kStreamUnroll groups per round)
+// or a single element (PER = kRoundSlotsV1); slot kUnit*u + e holds element kUnit*unit + e.
 template <int W, int PER>
 __device__ __forceinline__ int lane_unit(int round, int u, int wid, int lane) {
   return (W > 1 ? wid * kWave : 0) + lane + kWave * W * (round * PER + u);
 }
 
-template <bool V4>
+template <typename T, bool VEC>
 struct Round {
-  static constexpr int kSlots = V4 ? 4 * kStreamUnroll : kRoundSlotsV1;
+  static constexpr int kPer = VEC ? kStreamUnroll : kRoundSlotsV1;   // access groups per round
+  static constexpr int kSlots = kUnit<T, VEC> * kPer;
   float x[kSlots];
 };
 
-template <int W, bool V4>
+template <int W, typename T, bool VEC>
 __device__ __forceinline__ int round_slot_index(int round, int slot, int wid, int lane) {
-  if constexpr (V4) return 4 * lane_unit<W, kStreamUnroll>(round, slot >> 2, wid, lane) + (slot & 3);
-  else return lane_unit<W, kRoundSlotsV1>(round, slot, wid, lane);
+  constexpr int U = kUnit<T, VEC>;
+  return U * lane_unit<W, Round<T, VEC>::kPer>(round, slot / U, wid, lane) + (slot % U);
 }
 
 // loads of one round, unconditional: offsets past the row read 0 (masked to -inf when used)
-template <int W, bool V4>
-__device__ __forceinline__ void load_round(rsrc_t row, int round, int wid, int lane, Round<V4>& a) {
-  if constexpr (V4) {
+template <int W, typename T, bool VEC>
+__device__ __forceinline__ void load_round(rsrc_t row, int round, int wid, int lane, Round<T, VEC>& a) {
+  constexpr int PER = Round<T, VEC>::kPer;
 #pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) {
-      const uint32_t q = (uint32_t)lane_unit<W, kStreamUnroll>(round, u, wid, lane);
-      const v4f v = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(row, 16u * q, 0, kNonTemporal));
-      a.x[4 * u + 0] = v.x;
-      a.x[4 * u + 1] = v.y;
-      a.x[4 * u + 2] = v.z;
-      a.x[4 * u + 3] = v.w;
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < kRoundSlotsV1; ++u) {
-      const uint32_t j = (uint32_t)lane_unit<W, kRoundSlotsV1>(round, u, wid, lane);
-      a.x[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(row, 4u * j, 0, kNonTemporal));
-    }
-  }
+  for (int u = 0; u < PER; ++u)
+    load_unit<T, VEC>(row, (uint32_t)lane_unit<W, PER>(round, u, wid, lane), a.x + kUnit<T, VEC> * u);
 }
 
 // zero placeholders for every output element of one round (support entries are rewritten at
 // the end of the row); offsets past the row end are dropped by the range check
-template <int W, int MODE, bool V4>
+template <int W, typename T, int MODE, bool VEC>
 __device__ __forceinline__ void zero_round(rsrc_t out, int round, int wid, int lane) {
+  constexpr int PER = Round<T, VEC>::kPer;
   if constexpr (MODE == kGrad) {
-    if constexpr (V4) {
 #pragma unroll
-      for (int u = 0; u < kStreamUnroll; ++u) {
-        const uint32_t q = (uint32_t)lane_unit<W, kStreamUnroll>(round, u, wid, lane);
-        __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, out, 16u * q, 0, kNonTemporal);
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < kRoundSlotsV1; ++u) {
-        const uint32_t j = (uint32_t)lane_unit<W, kRoundSlotsV1>(round, u, wid, lane);
-        __builtin_amdgcn_raw_buffer_store_b32(0u, out, 4u * j, 0, kNonTemporal);
-      }
-    }
+    for (int u = 0; u < PER; ++u) store_zero_unit<T, VEC>(out, (uint32_t)lane_unit<W, PER>(round, u, wid, lane));
   } else if constexpr (MODE == kMask) {
-    if constexpr (V4) {
+    // float rows only: one mask byte per element
 #pragma unroll
-      for (int u = 0; u < kStreamUnroll; ++u) {
-        const uint32_t q = (uint32_t)lane_unit<W, kStreamUnroll>(round, u, wid, lane);
-        __builtin_amdgcn_raw_buffer_store_b32(0u, out, 4u * q, 0, kNonTemporal);
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < kRoundSlotsV1; ++u) {
-        const uint32_t j = (uint32_t)lane_unit<W, kRoundSlotsV1>(round, u, wid, lane);
-        __builtin_amdgcn_raw_buffer_store_b8((unsigned char)0, out, j, 0, kNonTemporal);
-      }
+    for (int u = 0; u < PER; ++u) {
+      const uint32_t q = (uint32_t)lane_unit<W, PER>(round, u, wid, lane);
+      if constexpr (VEC) __builtin_amdgcn_raw_buffer_store_b32(0u, out, 4u * q, 0, kNonTemporal);
+      else __builtin_amdgcn_raw_buffer_store_b8((unsigned char)0, out, q, 0, kNonTemporal);
     }
   }
 }
 
 // Candidates of one round: the running maximum m gives the bound t = (m - 1 rounded down), and
 // the entries z > t are appended to the wavefront's list.  Returns false on list overflow.
-template <int W, bool V4>
-__device__ __forceinline__ bool scan_round(Round<V4>& a, int round, int C, int wid, int lane, float* bv,
+template <int W, typename T, bool VEC>
+__device__ __forceinline__ bool scan_round(Round<T, VEC>& a, int round, int C, int wid, int lane, float* bv,
                                            int* bi, int cap, int& n, float& m, float& t) {
-  constexpr int S = Round<V4>::kSlots;
+  constexpr int S = Round<T, VEC>::kSlots;
   float lm = -INFINITY;
 #pragma unroll
   for (int i = 0; i < S; ++i) {
-    const int j = round_slot_index<W, V4>(round, i, wid, lane);
+    const int j = round_slot_index<W, T, VEC>(round, i, wid, lane);
     a.x[i] = j < C ? a.x[i] : -INFINITY;
     lm = fmaxf(lm, a.x[i]);
   }
@@ -899,7 +946,7 @@ __device__ __forceinline__ bool scan_round(Round<V4>& a, int round, int C, int w
     if (p) {
       const int pos = n + rank_in(b);
       bv[pos] = a.x[i];
-      bi[pos] = round_slot_index<W, V4>(round, i, wid, lane);
+      bi[pos] = round_slot_index<W, T, VEC>(round, i, wid, lane);
     }
     n += __popcll(b);
   }
@@ -908,44 +955,46 @@ __device__ __forceinline__ bool scan_round(Round<V4>& a, int round, int C, int w
 
 // Stream this wavefront's share of row r once: loads run one round ahead of the candidate scan,
 // and every output element gets its zero placeholder.  Returns false if the list overflowed.
-template <int W, int MODE, bool V4>
-__device__ bool stream_row(const float* __restrict__ row, int64_t r, int C, int lane, int wid, float* bv,
+template <int W, typename T, int MODE, bool VEC>
+__device__ bool stream_row(const void* __restrict__ row, int64_t r, int C, int lane, int wid, float* bv,
                            int* bi, const Outs& o, int& n, float& m, float& t) {
-  constexpr int per_round = kWave * W * Round<V4>::kSlots;   // elements per round of the row
+  constexpr int per_round = kWave * W * Round<T, VEC>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
-  const rsrc_t in = make_rsrc(row, 4u * (uint32_t)C);
+  const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
+  const rsrc_t in = make_rsrc(row, row_bytes);
   rsrc_t out = make_rsrc(nullptr, 0u);
-  if constexpr (MODE == kGrad) out = make_rsrc(o.grad + r * (int64_t)C, 4u * (uint32_t)C);
+  if constexpr (MODE == kGrad) out = make_rsrc(static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>, row_bytes);
   else if constexpr (MODE == kMask) out = make_rsrc(o.mask + r * (int64_t)C, (uint32_t)C);
   const int cap = o.cap;
-  Round<V4> a, b;
-  load_round<W, V4>(in, 0, wid, lane, a);
+  Round<T, VEC> a, b;
+  load_round<W, T, VEC>(in, 0, wid, lane, a);
   // stores to a zero-size resource (no traffic) so that the wait counts on entry match those of
   // the loop's back edge (a round's loads, then a round's stores)
   __builtin_amdgcn_sched_barrier(0);
-  zero_round<W, MODE, V4>(make_rsrc(nullptr, 0u), 0, wid, lane);
+  zero_round<W, T, MODE, VEC>(make_rsrc(nullptr, 0u), 0, wid, lane);
   __builtin_amdgcn_sched_barrier(0);
   int k = 0;
   while (true) {
-    load_round<W, V4>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
-    zero_round<W, MODE, V4>(out, k, wid, lane);
-    if (!scan_round<W, V4>(a, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
+    load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
+    zero_round<W, T, MODE, VEC>(out, k, wid, lane);
+    if (!scan_round<W, T, VEC>(a, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
     if (++k >= rounds) break;
-    load_round<W, V4>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
-    zero_round<W, MODE, V4>(out, k, wid, lane);
-    if (!scan_round<W, V4>(b, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
+    load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
+    zero_round<W, T, MODE, VEC>(out, k, wid, lane);
+    if (!scan_round<W, T, VEC>(b, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
     if (++k >= rounds) break;
   }
   return true;
 }
 
 // block-wide fp64 sum and count of the row entries > thr (fixed order)
-__device__ void block_sum_count(const float* __restrict__ row, int C, float thr, BlockShared& sh,
+template <typename T>
+__device__ void block_sum_count(const void* __restrict__ row, int C, float thr, BlockShared& sh,
                                 int lane, int wid, double& s, int& c) {
   double acc = 0.0;
   int cnt = 0;
   for (int j = threadIdx.x; j < C; j += kBlock) {
-    const float v = row[j];
+    const float v = load_elem<T>(row, j);
     if (v > thr) {
       acc += (double)v;
       ++cnt;
@@ -965,11 +1014,11 @@ __device__ void block_sum_count(const float* __restrict__ row, int C, float thr,
 
 // Generic path: fixed-point iterations over the row in global memory, then every output is
 // (re)written.  Used when a candidate list overflows and when forced by fwl_set_params(3, .).
-template <int MODE>
-__device__ void generic_row(const float* __restrict__ row, int64_t r, int C, int yr, int lane,
+template <typename T, int MODE>
+__device__ void generic_row(const void* __restrict__ row, int64_t r, int C, int yr, int lane,
                             int wid, BlockShared& sh, const Outs& o, double& tau, int& kappa) {
   float lm = -INFINITY;
-  for (int j = threadIdx.x; j < C; j += kBlock) lm = fmaxf(lm, row[j]);
+  for (int j = threadIdx.x; j < C; j += kBlock) lm = fmaxf(lm, load_elem<T>(row, j));
   const float wm = wave_max_f32(lm);
   __syncthreads();
   if (lane == 0) sh.red_m[wid] = wm;
@@ -978,7 +1027,7 @@ __device__ void generic_row(const float* __restrict__ row, int64_t r, int C, int
   const float t0 = bound_below_max(M);
   double t = (double)t0, s;
   int c;
-  block_sum_count(row, C, t0, sh, lane, wid, s, c);
+  block_sum_count<T>(row, C, t0, sh, lane, wid, s, c);
   tau = NAN;
   kappa = 0;
   if (c > 0) {
@@ -986,7 +1035,7 @@ __device__ void generic_row(const float* __restrict__ row, int64_t r, int C, int
       const double tn = (s - 1.0) / (double)c;
       double s2;
       int c2;
-      block_sum_count(row, C, rd32(tn), sh, lane, wid, s2, c2);
+      block_sum_count<T>(row, C, rd32(tn), sh, lane, wid, s2, c2);
       if (c2 == c || !(tn > t)) {
         tau = tn;
         kappa = c2;
@@ -1000,7 +1049,7 @@ __device__ void generic_row(const float* __restrict__ row, int64_t r, int C, int
     if (tc != tau) {
       double s3;
       tau = tc;
-      block_sum_count(row, C, rd32(tau), sh, lane, wid, s3, kappa);
+      block_sum_count<T>(row, C, rd32(tau), sh, lane, wid, s3, kappa);
     }
   }
   // outputs written while streaming must land before these rewrites (same block, so the same L2)
@@ -1009,20 +1058,19 @@ __device__ void generic_row(const float* __restrict__ row, int64_t r, int C, int
   const float Hf = rd32(tau);
   const float inv = (float)(o.scale / (double)kappa);
   if constexpr (MODE == kGrad) {
-    float* g = o.grad + r * (int64_t)C;
     for (int j = threadIdx.x; j < C; j += kBlock)
-      if (j != yr) g[j] = row[j] > Hf ? inv : 0.0f;
+      if (j != yr) store_elem<T>(o.grad, r * (int64_t)C + j, load_elem<T>(row, j) > Hf ? inv : 0.0f);
   } else if constexpr (MODE == kMask) {
     uint8_t* mk = o.mask + r * (int64_t)C;
     for (int j = threadIdx.x; j < C; j += kBlock)
-      if (j != yr) mk[j] = (uint8_t)(row[j] > Hf);
+      if (j != yr) mk[j] = (uint8_t)(load_elem<T>(row, j) > Hf);
   } else {
     float* cv = o.cval + r * (int64_t)C;
     int32_t* ci = o.cidx + r * (int64_t)C;
     int base = 0;
     for (int j0 = 0; j0 < C; j0 += kBlock) {
       const int j = j0 + (int)threadIdx.x;
-      const float v = j < C ? row[j] : -INFINITY;
+      const float v = j < C ? load_elem<T>(row, j) : -INFINITY;
       const bool p = v > Hf;
       const uint64_t b = ballot(p);
       __syncthreads();
@@ -1040,8 +1088,8 @@ __device__ void generic_row(const float* __restrict__ row, int64_t r, int C, int
   }
 }
 
-template <int MODE, bool V4>
-__global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict__ z,
+template <typename T, int MODE, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict__ z,
                                                          const int64_t* __restrict__ tgt, int64_t N,
                                                          int C, Outs o) {
   __shared__ BlockShared sh;
@@ -1049,7 +1097,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict
   const int wid = uniform((int)(threadIdx.x >> 6));
   double bsum = 0.0;
   for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
-    const float* row = z + r * (int64_t)C;
+    const void* row = static_cast<const char*>(z) + r * (int64_t)C * kElemBytes<T>;
     const int64_t y64 = tgt[r];
     const bool yok = y64 >= 0 && y64 < C;
     const int yr = yok ? (int)y64 : -1;
@@ -1059,7 +1107,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict
     int n = 0;
     float m = -INFINITY, t = -INFINITY;
     bool ok = !o.force_generic;
-    if (ok) ok = stream_row<kWavesPerBlock, MODE, V4>(row, r, C, lane, wid, bv, bi, o, n, m, t);
+    if (ok) ok = stream_row<kWavesPerBlock, T, MODE, V4>(row, r, C, lane, wid, bv, bi, o, n, m, t);
     if (lane == 0) {
       sh.wmax[wid] = m;
       sh.wn[wid] = n;
@@ -1164,7 +1212,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict
         for (int p = lane; p < n; p += kWave) {
           const int id = bi[p];
           if (id == yr || !(bv[p] > Hf)) continue;
-          if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + id] = inv;
+          if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + id, inv);
           else o.mask[r * (int64_t)C + id] = 1;
         }
       } else {
@@ -1194,15 +1242,15 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict
         }
       }
     } else {
-      generic_row<MODE>(row, r, C, yr, lane, wid, sh, o, tau, kappa);
+      generic_row<T, MODE>(row, r, C, yr, lane, wid, sh, o, tau, kappa);
     }
 
     if (threadIdx.x == 0) {
       const float Hf = rd32(tau);
       const float inv = (float)(o.scale / (double)kappa);
-      const float zy = yok ? row[yr] : NAN;
+      const float zy = yok ? load_elem<T>(row, yr) : NAN;
       if (yok) {
-        if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + yr] = (zy > Hf ? inv : 0.0f) - o.scale_f;
+        if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + yr, (zy > Hf ? inv : 0.0f) - o.scale_f);
         else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
       }
       const float loss = (float)((1.0 - (double)zy) + tau);
@@ -1225,11 +1273,12 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const float* __restrict
 // its own rows, as in fwl_wave_rows.
 
 // fp64 sum and count of the row entries > thr, over the wavefront (fixed order)
-__device__ void wave_row_sum_count(const float* __restrict__ row, int C, float thr, int lane, double& s, int& c) {
+template <typename T>
+__device__ void wave_row_sum_count(const void* __restrict__ row, int C, float thr, int lane, double& s, int& c) {
   double acc = 0.0;
   int cnt = 0;
   for (int j = lane; j < C; j += kWave) {
-    const float v = row[j];
+    const float v = load_elem<T>(row, j);
     if (v > thr) {
       acc += (double)v;
       ++cnt;
@@ -1240,15 +1289,16 @@ __device__ void wave_row_sum_count(const float* __restrict__ row, int C, float t
 }
 
 // generic solve of one row by one wavefront: fixed-point iterations over the row in memory
-__device__ void wave_generic_solve(const float* __restrict__ row, int C, int lane, float& m, double& tau,
+template <typename T>
+__device__ void wave_generic_solve(const void* __restrict__ row, int C, int lane, float& m, double& tau,
                                    int& kappa) {
   float lm = -INFINITY;
-  for (int j = lane; j < C; j += kWave) lm = fmaxf(lm, row[j]);
+  for (int j = lane; j < C; j += kWave) lm = fmaxf(lm, load_elem<T>(row, j));
   m = wave_max_f32(lm);
   const float t0 = bound_below_max(m);
   double t = (double)t0, s;
   int c;
-  wave_row_sum_count(row, C, t0, lane, s, c);
+  wave_row_sum_count<T>(row, C, t0, lane, s, c);
   tau = NAN;
   kappa = 0;
   if (c == 0) return;
@@ -1256,7 +1306,7 @@ __device__ void wave_generic_solve(const float* __restrict__ row, int C, int lan
     const double tn = (s - 1.0) / (double)c;
     double s2;
     int c2;
-    wave_row_sum_count(row, C, rd32(tn), lane, s2, c2);
+    wave_row_sum_count<T>(row, C, rd32(tn), lane, s2, c2);
     if (c2 == c || !(tn > t)) {
       tau = tn;
       kappa = c2;
@@ -1270,12 +1320,12 @@ __device__ void wave_generic_solve(const float* __restrict__ row, int C, int lan
   if (tc != tau) {
     double s3;
     tau = tc;
-    wave_row_sum_count(row, C, rd32(tau), lane, s3, kappa);
+    wave_row_sum_count<T>(row, C, rd32(tau), lane, s3, kappa);
   }
 }
 
-template <int MODE, bool V4>
-__global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const float* __restrict__ z,
+template <typename T, int MODE, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __restrict__ z,
                                                                const int64_t* __restrict__ tgt, int64_t N,
                                                                int C, Outs o) {
   __shared__ float s_val[kWavesPerBlock][kCapMax];
@@ -1294,7 +1344,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const float* __re
   double lsum = 0.0;
   for (int k = 0; k < nrows; ++k) {
     const int64_t r = w + (int64_t)k * stride;
-    const float* row = z + r * (int64_t)C;
+    const void* row = static_cast<const char*>(z) + r * (int64_t)C * kElemBytes<T>;
     const int64_t y64 = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
                         (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
     const bool yok = y64 >= 0 && y64 < C;
@@ -1302,7 +1352,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const float* __re
 
     int n = 0;
     float m = -INFINITY, t = -INFINITY;
-    const bool ok = !o.force_generic && stream_row<1, MODE, V4>(row, r, C, lane, 0, bv, bi, o, n, m, t);
+    const bool ok = !o.force_generic && stream_row<1, T, MODE, V4>(row, r, C, lane, 0, bv, bi, o, n, m, t);
     double tau;
     int kappa;
     uint64_t support = 0;
@@ -1327,7 +1377,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const float* __re
       n = kept;
       resolve_list(bv, n, tb, m, lane, tau, kappa, support);
     } else {
-      wave_generic_solve(row, C, lane, m, tau, kappa);
+      wave_generic_solve<T>(row, C, lane, m, tau, kappa);
     }
     const float Hf = rd32(tau);
     const float inv = (float)(o.scale / (double)kappa);
@@ -1338,7 +1388,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const float* __re
         for (int p = lane; p < n; p += kWave) {
           const int id = bi[p];
           if (id == yr || !(bv[p] > Hf)) continue;
-          if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + id] = inv;
+          if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + id, inv);
           else o.mask[r * (int64_t)C + id] = 1;
         }
       } else {
@@ -1358,15 +1408,15 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const float* __re
     } else {
       if constexpr (MODE == kGrad) {
         for (int j = lane; j < C; j += kWave)
-          if (j != yr) o.grad[r * (int64_t)C + j] = row[j] > Hf ? inv : 0.0f;
+          if (j != yr) store_elem<T>(o.grad, r * (int64_t)C + j, load_elem<T>(row, j) > Hf ? inv : 0.0f);
       } else if constexpr (MODE == kMask) {
         for (int j = lane; j < C; j += kWave)
-          if (j != yr) o.mask[r * (int64_t)C + j] = (uint8_t)(row[j] > Hf);
+          if (j != yr) o.mask[r * (int64_t)C + j] = (uint8_t)(load_elem<T>(row, j) > Hf);
       } else {
         int out = 0;
         for (int j0 = 0; j0 < C; j0 += kWave) {
           const int j = j0 + lane;
-          const float v = j < C ? row[j] : -INFINITY;
+          const float v = j < C ? load_elem<T>(row, j) : -INFINITY;
           const bool sel = v > Hf;
           const uint64_t b = ballot(sel);
           if (sel) {
@@ -1377,9 +1427,9 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const float* __re
         }
       }
     }
-    const float zy = yok ? row[yr] : NAN;
+    const float zy = yok ? load_elem<T>(row, yr) : NAN;
     if (lane == 0 && yok) {
-      if constexpr (MODE == kGrad) o.grad[r * (int64_t)C + yr] = (zy > Hf ? inv : 0.0f) - o.scale_f;
+      if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + yr, (zy > Hf ? inv : 0.0f) - o.scale_f);
       else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
     }
     const float loss = (float)((1.0 - (double)zy) + tau);
@@ -1483,25 +1533,26 @@ __global__ __launch_bounds__(kBlock) void fwl_cand_to_grad(
   }
 }
 
-template <bool V4>
-__global__ __launch_bounds__(kBlock) void fwl_scale_rows(float* __restrict__ grad,
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kBlock) void fwl_scale_rows(void* __restrict__ grad,
                                                          const float* __restrict__ go,
                                                          int64_t go_stride, int64_t N, int C) {
+  constexpr int U = kUnit<T, VEC>;
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+  const int units = (C + U - 1) / U;
   for (int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid; r < N; r += stride) {
     const float s = go[r * go_stride];
     if (s == 1.0f) continue;
-    float* gr = grad + r * (int64_t)C;
-    if constexpr (V4) {
-      for (int q = lane; q < (C >> 2); q += kWave) {
-        v4f g = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(gr) + q);
-        g *= s;
-        __builtin_nontemporal_store(g, reinterpret_cast<v4f*>(gr) + q);
-      }
-    } else {
-      for (int j = lane; j < C; j += kWave) gr[j] *= s;
+    const rsrc_t row = make_rsrc(static_cast<char*>(grad) + r * (int64_t)C * kElemBytes<T>,
+                                 (uint32_t)(kElemBytes<T> * C));
+    for (int u = lane; u < units; u += kWave) {
+      float v[U];
+      load_unit<T, VEC>(row, (uint32_t)u, v);
+#pragma unroll
+      for (int e = 0; e < U; ++e) v[e] *= s;
+      store_unit<T, VEC>(row, (uint32_t)u, v);
     }
   }
 }
@@ -1567,14 +1618,15 @@ int device_cus() {
 }
 
 // Grid of fwl_wave_rows.  Each wavefront keeps one row load and one row of stores in flight, so
-// the blocks per CU set the number of concurrent row streams.  Measured on MI355X at C = 1000: two
-// blocks per CU (8 wavefronts, ~64 KB in flight per CU) stream best; more concurrent streams over
-// a wider address window lose DRAM efficiency.  Shorter rows get proportionally more blocks, up to
-// the resident limit.  At most kRowsPerWave rows per wavefront: larger N gets more (queued) blocks.
-int wave_grid(int64_t N, int C, int resident) {
+// the blocks per CU set the number of concurrent row streams.  Measured on MI355X with 4000-byte
+// rows: two blocks per CU (8 wavefronts, ~64 KB in flight per CU) stream best; more concurrent
+// streams over a wider address window lose DRAM efficiency.  Shorter rows (in bytes) get
+// proportionally more blocks, up to the resident limit.  At most kRowsPerWave rows per wavefront:
+// larger N gets more (queued) blocks.
+int wave_grid(int64_t N, int64_t row_bytes, int resident) {
   const int cus = device_cus();
   const int per_cu_resident = cus > 0 && resident > 0 ? resident / cus : 0;
-  int per_cu = (int)((2000 + C - 1) / (C > 0 ? C : 1));
+  int per_cu = (int)((8000 + row_bytes - 1) / (row_bytes > 0 ? row_bytes : 1));
   if (per_cu < 2) per_cu = 2;
   if (per_cu_resident > 0 && per_cu > per_cu_resident) per_cu = per_cu_resident;
   const int target = cus > 0 ? per_cu * cus : (resident > 0 ? resident : kMaxBlocksWave);
@@ -1588,56 +1640,45 @@ bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0;
 
 int launch_status() { return hipGetLastError() == hipSuccess ? FWL_OK : FWL_ERR_LAUNCH; }
 
-template <int MODE, int NV, bool V4>
-void launch_wave(const float* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
-  const void* k = reinterpret_cast<const void*>(&fwl_wave_rows<MODE, NV, V4>);
-  const int grid = wave_grid(N, C, resident_blocks(k));
-  hipLaunchKernelGGL((fwl_wave_rows<MODE, NV, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+template <typename T, int MODE, int NV, bool V4>
+void launch_wave(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+  const void* k = reinterpret_cast<const void*>(&fwl_wave_rows<T, MODE, NV, V4>);
+  const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
+  hipLaunchKernelGGL((fwl_wave_rows<T, MODE, NV, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
 }
 
-template <int MODE>
-void dispatch_wave(const float* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
+// register rows: NV units per lane, the smallest power of two that covers the row (E <= 32)
+template <typename T, int MODE>
+void dispatch_wave(const void* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
                    hipStream_t s) {
   if (v4) {
-    if (C <= 256) launch_wave<MODE, 1, true>(z, y, N, C, o, s);
-    else if (C <= 512) launch_wave<MODE, 2, true>(z, y, N, C, o, s);
-    else if (C <= 1024) launch_wave<MODE, 4, true>(z, y, N, C, o, s);
-    else launch_wave<MODE, 8, true>(z, y, N, C, o, s);
+    constexpr int U = kUnit<T, true>;
+    const int units = (C + U - 1) / U;
+    if (units <= 64) launch_wave<T, MODE, 1, true>(z, y, N, C, o, s);
+    else if (units <= 128) launch_wave<T, MODE, 2, true>(z, y, N, C, o, s);
+    else if (units <= 256) launch_wave<T, MODE, 4, true>(z, y, N, C, o, s);
+    else if constexpr (U == 4) launch_wave<T, MODE, 8, true>(z, y, N, C, o, s);
   } else {
-    if (C <= 64) launch_wave<MODE, 1, false>(z, y, N, C, o, s);
-    else if (C <= 128) launch_wave<MODE, 2, false>(z, y, N, C, o, s);
-    else if (C <= 256) launch_wave<MODE, 4, false>(z, y, N, C, o, s);
-    else if (C <= 512) launch_wave<MODE, 8, false>(z, y, N, C, o, s);
-    else launch_wave<MODE, 16, false>(z, y, N, C, o, s);
+    if (C <= 64) launch_wave<T, MODE, 1, false>(z, y, N, C, o, s);
+    else if (C <= 128) launch_wave<T, MODE, 2, false>(z, y, N, C, o, s);
+    else if (C <= 256) launch_wave<T, MODE, 4, false>(z, y, N, C, o, s);
+    else if (C <= 512) launch_wave<T, MODE, 8, false>(z, y, N, C, o, s);
+    else launch_wave<T, MODE, 16, false>(z, y, N, C, o, s);
   }
 }
 
-template <int MODE, bool V4>
-void launch_block(const float* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
-  const void* k = reinterpret_cast<const void*>(&fwl_block_rows<MODE, V4>);
+template <typename T, int MODE, bool V4>
+void launch_block(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+  const void* k = reinterpret_cast<const void*>(&fwl_block_rows<T, MODE, V4>);
   const int grid = persistent_grid(N, 1, resident_blocks(k), kMaxBlocksRow);
-  hipLaunchKernelGGL((fwl_block_rows<MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+  hipLaunchKernelGGL((fwl_block_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
 }
 
-template <int MODE, bool V4>
-void launch_wave_stream(const float* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
-  const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<MODE, V4>);
-  const int grid = wave_grid(N, C, resident_blocks(k));
-  hipLaunchKernelGGL((fwl_wave_stream_rows<MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
-}
-
-template <int MODE>
-void dispatch_wave_stream(const float* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
-                          hipStream_t s) {
-  if (v4) launch_wave_stream<MODE, true>(z, y, N, C, o, s);
-  else launch_wave_stream<MODE, false>(z, y, N, C, o, s);
-}
-
-template <int MODE>
-void dispatch_block(const float* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
-                    hipStream_t s) {
-  if (v4) launch_block<MODE, true>(z, y, N, C, o, s);
-  else launch_block<MODE, false>(z, y, N, C, o, s);
+template <typename T, int MODE, bool V4>
+void launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+  const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<T, MODE, V4>);
+  const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
+  hipLaunchKernelGGL((fwl_wave_stream_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
 }
 
 // rows are addressed through buffer resources with 32-bit byte ranges and offsets (one round
@@ -1646,11 +1687,11 @@ constexpr int64_t kMaxC = (int64_t)1 << 29;
 bool bad_shape(int64_t N, int64_t C) { return N < 0 || C < 1 || C > kMaxC; }
 
 // shared forward driver; `out_v4_ok` says whether the mode's dense output allows 128-bit access
-template <int MODE>
-int forward(const float* z, const int64_t* y, int64_t N, int64_t C64, double scale, double reduce_div,
+template <typename T, int MODE>
+int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scale, double reduce_div,
             Outs o, bool out_v4_ok, void* ws, size_t ws_bytes, hipStream_t s) {
   if (bad_shape(N, C64) || (N > 0 && (z == nullptr || y == nullptr))) return FWL_ERR_INVALID_ARG;
-  if (!aligned(z, 4) || !aligned(y, 8)) return FWL_ERR_ALIGNMENT;
+  if (!aligned(z, kElemBytes<T>) || !aligned(y, 8)) return FWL_ERR_ALIGNMENT;
   const int C = (int)C64;
   o.scale = scale;
   o.reduce_div = reduce_div;
@@ -1666,16 +1707,38 @@ int forward(const float* z, const int64_t* y, int64_t N, int64_t C64, double sca
     if (o.mean != nullptr) hipLaunchKernelGGL(fwl_empty_mean, dim3(1), dim3(1), 0, s, o.mean, reduce_div);
     return launch_status();
   }
-  const bool v4 = (C % 4) == 0 && aligned(z, 16) && out_v4_ok;
+  const bool v4 = (C % kUnit<T, true>) == 0 && aligned(z, 16) && out_v4_ok;
   int path = g_path;
-  // measured on MI355X: registers win up to 2048 for 128-bit rows, up to 1024 for 32-bit rows;
-  // one streaming wavefront per row up to 8192; one block per row beyond
+  // measured on MI355X: registers win up to 2048 for 128-bit rows, up to 1024 for rows accessed
+  // one element at a time; one streaming wavefront per row up to 8192; one block per row beyond
   const int max_wave_c = v4 ? kMaxWaveC : kMaxWaveC1;
   if (path == 0) path = C <= max_wave_c ? 1 : (C <= kMaxStreamC ? 4 : 2);
   if (path == 1 && C > max_wave_c) path = 4;
-  if (path == 1) dispatch_wave<MODE>(z, y, N, C, v4, o, s);
-  else if (path == 4 || path == 5) dispatch_wave_stream<MODE>(z, y, N, C, v4, o, s);
-  else dispatch_block<MODE>(z, y, N, C, v4, o, s);
+  if (path == 1) {
+    dispatch_wave<T, MODE>(z, y, N, C, v4, o, s);
+  } else if (path == 4 || path == 5) {
+    if (v4) launch_wave_stream<T, MODE, true>(z, y, N, C, o, s);
+    else launch_wave_stream<T, MODE, false>(z, y, N, C, o, s);
+  } else {
+    if (v4) launch_block<T, MODE, true>(z, y, N, C, o, s);
+    else launch_block<T, MODE, false>(z, y, N, C, o, s);
+  }
+  return launch_status();
+}
+
+template <typename T>
+int scale_grad(void* grad, const float* grad_output, int64_t go_stride, int64_t N, int64_t C, hipStream_t stream) {
+  if (bad_shape(N, C) || go_stride < 0 || (N > 0 && (grad == nullptr || grad_output == nullptr)))
+    return FWL_ERR_INVALID_ARG;
+  if (!aligned(grad, kElemBytes<T>) || !aligned(grad_output, 4)) return FWL_ERR_ALIGNMENT;
+  if (N == 0) return FWL_OK;
+  const int Ci = (int)C;
+  if ((C % kUnit<T, true>) == 0 && aligned(grad, 16))
+    hipLaunchKernelGGL((fwl_scale_rows<T, true>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, grad, grad_output,
+                       go_stride, N, Ci);
+  else
+    hipLaunchKernelGGL((fwl_scale_rows<T, false>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, grad, grad_output,
+                       go_stride, N, Ci);
   return launch_status();
 }
 
@@ -1719,8 +1782,37 @@ int fwl_forward_backward(const float* logits, const int64_t* targets, int64_t N,
   o.mean = mean_loss;
   o.kappa = kappa;
   o.grad = grad;
-  return forward<kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
+  return forward<float, kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
                         workspace_bytes, stream);
+}
+
+int fwl_forward_backward_typed(int dtype, const void* logits, const int64_t* targets, int64_t N, int64_t C,
+                               double scale, double reduce_div, float* H, float* losses, float* mean_loss,
+                               int32_t* kappa, void* grad, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+  if (N > 0 && grad == nullptr) return FWL_ERR_INVALID_ARG;
+  Outs o = {};
+  o.H = H;
+  o.loss = losses;
+  o.mean = mean_loss;
+  o.kappa = kappa;
+  o.grad = grad;
+  switch (dtype) {
+    case FWL_FLOAT32:
+      if (!aligned(grad, 4)) return FWL_ERR_ALIGNMENT;
+      return forward<float, kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
+                                   workspace_bytes, stream);
+    case FWL_BFLOAT16:
+      if (!aligned(grad, 2)) return FWL_ERR_ALIGNMENT;
+      return forward<bf16_t, kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
+                                    workspace_bytes, stream);
+    case FWL_FLOAT16:
+      if (!aligned(grad, 2)) return FWL_ERR_ALIGNMENT;
+      return forward<f16_t, kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
+                                   workspace_bytes, stream);
+    default:
+      return FWL_ERR_INVALID_ARG;
+  }
 }
 
 int fwl_forward_small(const float* logits, const int64_t* targets, int64_t N, int64_t C,
@@ -1734,7 +1826,7 @@ int fwl_forward_small(const float* logits, const int64_t* targets, int64_t N, in
   o.mean = mean_loss;
   o.kappa = kappa;
   o.mask = selected;
-  return forward<kMask>(logits, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o,
+  return forward<float, kMask>(logits, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o,
                         aligned(selected, 4), workspace, workspace_bytes, stream);
 }
 
@@ -1754,7 +1846,7 @@ int fwl_forward_large(const float* logits, const int64_t* targets, int64_t N, in
   o.cval = cand_values;
   o.cidx = cand_indices;
   o.ccnt = cand_counts;
-  return forward<kCand>(logits, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o, true,
+  return forward<float, kCand>(logits, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o, true,
                         workspace, workspace_bytes, stream);
 }
 
@@ -1803,18 +1895,17 @@ int fwl_backward_large(const float* logits, const int64_t* targets, const float*
 
 int fwl_scale_grad(float* grad, const float* grad_output, int64_t go_stride, int64_t N, int64_t C,
                    hipStream_t stream) {
-  if (bad_shape(N, C) || go_stride < 0 || (N > 0 && (grad == nullptr || grad_output == nullptr)))
-    return FWL_ERR_INVALID_ARG;
-  if (!aligned(grad, 4) || !aligned(grad_output, 4)) return FWL_ERR_ALIGNMENT;
-  if (N == 0) return FWL_OK;
-  const int Ci = (int)C;
-  if ((C % 4) == 0 && aligned(grad, 16))
-    hipLaunchKernelGGL((fwl_scale_rows<true>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, grad, grad_output,
-                       go_stride, N, Ci);
-  else
-    hipLaunchKernelGGL((fwl_scale_rows<false>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, grad, grad_output,
-                       go_stride, N, Ci);
-  return launch_status();
+  return scale_grad<float>(grad, grad_output, go_stride, N, C, stream);
+}
+
+int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_t go_stride, int64_t N, int64_t C,
+                         hipStream_t stream) {
+  switch (dtype) {
+    case FWL_FLOAT32: return scale_grad<float>(grad, grad_output, go_stride, N, C, stream);
+    case FWL_BFLOAT16: return scale_grad<bf16_t>(grad, grad_output, go_stride, N, C, stream);
+    case FWL_FLOAT16: return scale_grad<f16_t>(grad, grad_output, go_stride, N, C, stream);
+    default: return FWL_ERR_INVALID_ARG;
+  }
 }
 
 int fwl_set_params(int path, int cand_cap) {

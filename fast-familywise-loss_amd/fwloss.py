@@ -61,7 +61,9 @@ class FWFunction(torch.autograd.Function):
             scale, rdiv = 1.0, 1.0
         _, losses, reduced, _, grad = _ext.fw_forward_backward(logits.detach(), target, scale, rdiv)
         ctx.save_for_backward(grad)
-        return losses if reduction == "none" else reduced
+        # the loss has the logits' dtype, as in the reference (fw_cpu.cpp:732); computed in fp32/fp64
+        out = losses if reduction == "none" else reduced
+        return out if out.dtype == logits.dtype else out.to(logits.dtype)
 
     @staticmethod
     def backward(ctx, grad_output):
@@ -73,7 +75,9 @@ class FWFunction(torch.autograd.Function):
 
 
 def familywise_loss(logits, target, reduction="mean"):
-    """FW loss of float32 logits [N, C] (GPU) and int64 targets [N]; reduction 'mean' | 'sum' | 'none'.
+    """FW loss of logits [N, C] (GPU; float32, bfloat16 or float16) and int64 targets [N];
+    reduction 'mean' | 'sum' | 'none'.  16-bit logits are widened to fp32 exactly; the loss and the
+    gradient are returned in the logits' dtype (the gradient rounded to nearest-even).
 
     Same call shape as the reference's ``fwcpp.familywise_loss`` (src/cpu/fwcpp.py:18-19), which
     accepts 'sum' and 'mean'; 'none' returns the per-row losses (reference_impl.py:30-33).

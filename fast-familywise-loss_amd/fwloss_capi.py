@@ -28,6 +28,9 @@ SIGNATURES = {
     "fwl_forward_large": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], ctypes.c_int),
     "fwl_backward_large": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P], ctypes.c_int),
     "fwl_scale_grad": ([_P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
+    "fwl_forward_backward_typed": ([ctypes.c_int, _P, _P, _I64, _I64, _D, _D, _P, _P, _P, _P, _P, _P,
+                                    ctypes.c_size_t, _P], ctypes.c_int),
+    "fwl_scale_grad_typed": ([ctypes.c_int, _P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
     "fwl_set_params": ([ctypes.c_int, ctypes.c_int], ctypes.c_int),
     "fwl_get_params": ([ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
 }
@@ -100,6 +103,26 @@ def forward_backward(z, y, scale=None, reduce_div=None, ws=None):
                                     _ptr(out["mean"]), _ptr(out["kappa"]), _ptr(out["grad"]), _ptr(buf),
                                     buf.numel(), _stream())
     _check(rc, "fwl_forward_backward")
+    return out
+
+
+DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}   # enum fwl_dtype
+
+
+def forward_backward_typed(z, y, scale=None, reduce_div=None, ws=None):
+    """fwl_forward_backward_typed for float32/bfloat16/float16 logits; grad has the logits' dtype."""
+    N, C = z.shape
+    scale = (1.0 / N if N else 1.0) if scale is None else scale
+    reduce_div = float(N) if reduce_div is None else reduce_div
+    ws = ws or Workspace(z.device)
+    buf = ws.get(N, C)
+    out = dict(H=torch.empty(N, device=z.device), loss=torch.empty(N, device=z.device),
+               mean=torch.empty((), device=z.device), kappa=torch.empty(N, dtype=torch.int32, device=z.device),
+               grad=torch.empty_like(z))
+    rc = lib().fwl_forward_backward_typed(DTYPES[z.dtype], _ptr(z), _ptr(y), N, C, scale, reduce_div, _ptr(out["H"]),
+                                          _ptr(out["loss"]), _ptr(out["mean"]), _ptr(out["kappa"]), _ptr(out["grad"]),
+                                          _ptr(buf), buf.numel(), _stream())
+    _check(rc, "fwl_forward_backward_typed")
     return out
 
 

@@ -44,9 +44,16 @@ enum fwl_status {
   FWL_OK = 0,
   FWL_ERR_INVALID_ARG = 1,  /* null pointer, N < 0, C < 1, C > 2^29 */
   FWL_ERR_WORKSPACE = 2,    /* workspace missing or smaller than fwl_workspace_bytes(N, C) */
-  FWL_ERR_ALIGNMENT = 3,    /* logits/grad not 4-byte aligned, or targets not 8-byte aligned */
+  FWL_ERR_ALIGNMENT = 3,    /* logits/grad not aligned to their element size, targets not to 8 bytes */
   FWL_ERR_LAUNCH = 4,       /* the HIP runtime rejected a launch */
   FWL_ERR_DEVICE = 5        /* no usable gfx950 device current */
+};
+
+/* Element types of the logits accepted by fwl_forward_backward_typed. */
+enum fwl_dtype {
+  FWL_FLOAT32 = 0,
+  FWL_BFLOAT16 = 1,   /* bfloat16 */
+  FWL_FLOAT16 = 2     /* IEEE binary16 */
 };
 
 /* Human-readable text of a status code (static storage). */
@@ -66,6 +73,18 @@ int fwl_forward_backward(const float* logits, const int64_t* targets, int64_t N,
                          double scale, double reduce_div, float* H, float* losses,
                          float* mean_loss, int32_t* kappa, float* grad, void* workspace,
                          size_t workspace_bytes, hipStream_t stream);
+
+/* fwl_forward_backward for logits of element type `dtype` (enum fwl_dtype); grad has the same
+ * element type.  16-bit logits are widened to fp32 exactly, every decision is the fp32 path's, and
+ * the gradient values of the fp32 path are rounded to nearest-even on store; H, losses, mean_loss
+ * and kappa are as for fp32 logits with the same values.  No reference counterpart: the reference
+ * GPU ops accept fp32 only (src/cuda/fw_radix_argmax.cu:1385, :1421); this extends the fused op of
+ * the CPU autograd path (src/cpu/fw_cpu.cpp:721-741), which dispatches on the logits' dtype
+ * (fw_cpu.cpp:697-703). */
+int fwl_forward_backward_typed(int dtype, const void* logits, const int64_t* targets, int64_t N,
+                               int64_t C, double scale, double reduce_div, float* H, float* losses,
+                               float* mean_loss, int32_t* kappa, void* grad, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream);
 
 /* Forward with the support mask: selected[r,j] = (z_j > tau) as bytes 0/1 (torch.bool layout).
  * Replaces fw_radix_forward_small (src/cuda/fw_radix_argmax.cu:1381-1414; binding.cpp:11):
@@ -106,6 +125,12 @@ int fwl_backward_large(const float* logits, const int64_t* targets, const float*
  * which skips the multiply when grad_output == 1. */
 int fwl_scale_grad(float* grad, const float* grad_output, int64_t go_stride, int64_t N, int64_t C,
                    hipStream_t stream);
+
+/* fwl_scale_grad for a gradient of element type `dtype` (enum fwl_dtype): each element is widened
+ * to fp32, multiplied, and rounded to nearest-even.  The backward of fwl_forward_backward_typed
+ * (src/cpu/fw_cpu.cpp:734-740 scales in the logits' dtype). */
+int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_t go_stride, int64_t N,
+                         int64_t C, hipStream_t stream);
 
 /* Process-wide dispatch switches, the GPU counterpart of the reference CPU path's set_params
  * (src/cpu/fw_cpu.cpp:758-763, used by its tests to force each branch).  Not thread-safe; meant

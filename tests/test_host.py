@@ -31,7 +31,7 @@ def P(x):
 def test_library_exports_every_declared_function():
     L = capi.lib()
     declared = capi.declared_functions()
-    assert len(declared) == 10
+    assert len(declared) == 12
     for name in declared:
         assert hasattr(L, name), name
     # the ctypes signature table covers exactly the header
@@ -110,6 +110,24 @@ def test_other_entry_point_argument_errors():
     # empty batches return before any launch for the backward entry points
     assert L.fwl_backward_small(None, None, None, 0, 16, None, None) == 0
     assert L.fwl_scale_grad(None, None, 0, 0, 16, None) == 0
+
+
+def test_typed_entry_point_argument_errors():
+    L = capi.lib()
+    ws_need = L.fwl_workspace_bytes(8, 16)
+
+    def call(dtype=1, z=A16, grad=A16, N=8, C=16):
+        return L.fwl_forward_backward_typed(dtype, P(z), P(A16), N, C, 1.0, 1.0, P(A16), P(A16), P(A16), P(A16),
+                                            P(grad), P(A16), ws_need, None)
+    assert call(dtype=3) == 1
+    assert call(dtype=-1) == 1
+    assert call(grad=None) == 1
+    assert call(z=A16 + 1) == 3               # 16-bit logits need 2-byte alignment
+    assert call(grad=A16 + 1) == 3
+    assert call(dtype=0, z=A16 + 2) == 3       # fp32 logits need 4
+    assert L.fwl_scale_grad_typed(5, P(A16), P(A16), 0, 8, 16, None) == 1
+    assert L.fwl_scale_grad_typed(2, P(A16 + 1), P(A16), 0, 8, 16, None) == 3
+    assert L.fwl_scale_grad_typed(1, None, None, 0, 0, 16, None) == 0
 
 
 def test_set_params_validation_and_round_trip():
