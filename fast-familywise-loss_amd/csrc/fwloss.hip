@@ -810,6 +810,403 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
 }
 
 // ------------------------------------------------------------------------------------------------
+// fwl_seg_rows: short rows, R = 64/L rows per wavefront iteration, one row per aligned group
+// ("segment") of L = 16 or 32 lanes.  Every cross-lane step of fwl_wave_rows works inside the
+// segments at once (DPP within rows of 16 lanes, v_permlane16_swap between the two rows of a
+// 32-lane segment), so R rows share each instruction of the selection.
+
+// butterfly reductions inside segments: every lane receives its segment's result
+template <int L>
+__device__ __forceinline__ float seg_max_f32(float v, int lane) {
+  v = fmaxf(v, xor_lane<1>(v, lane));
+  v = fmaxf(v, xor_lane<2>(v, lane));
+  v = fmaxf(v, __int_as_float(dpp_mov<kRowHalfMirror>(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_mov<kRowMirror>(__float_as_int(v))));
+  if constexpr (L == 32) v = fmaxf(v, xor_lane<16>(v, lane));
+  return v;
+}
+
+template <int L>
+__device__ __forceinline__ double seg_max_f64(double v, int lane) {
+  v = fmax(v, dpp_mov_f64<kQuadXor1>(v));
+  v = fmax(v, dpp_mov_f64<kQuadXor2>(v));
+  v = fmax(v, dpp_mov_f64<kRowHalfMirror>(v));
+  v = fmax(v, dpp_mov_f64<kRowMirror>(v));
+  if constexpr (L == 32) {
+    const int64_t b = __double_as_longlong(v);
+    const float lo = xor_lane<16>(__int_as_float((int)b), lane);
+    const float hi = xor_lane<16>(__int_as_float((int)(b >> 32)), lane);
+    v = fmax(v, __longlong_as_double((int64_t)(((uint64_t)(unsigned)__float_as_int(hi) << 32) |
+                                               (unsigned)__float_as_int(lo))));
+  }
+  return v;
+}
+
+// (all lanes of a segment get bit-identical sums: every butterfly step adds two commuted operands)
+template <int L>
+__device__ __forceinline__ double seg_sum_f64(double v, int lane) {
+  v += dpp_mov_f64<kQuadXor1>(v);
+  v += dpp_mov_f64<kQuadXor2>(v);
+  v += dpp_mov_f64<kRowHalfMirror>(v);
+  v += dpp_mov_f64<kRowMirror>(v);
+  if constexpr (L == 32) {
+    const int64_t b = __double_as_longlong(v);
+    const float lo = xor_lane<16>(__int_as_float((int)b), lane);
+    const float hi = xor_lane<16>(__int_as_float((int)(b >> 32)), lane);
+    v += __longlong_as_double((int64_t)(((uint64_t)(unsigned)__float_as_int(hi) << 32) |
+                                        (unsigned)__float_as_int(lo)));
+  }
+  return v;
+}
+
+template <int L>
+__device__ __forceinline__ int seg_sum_i32(int v, int lane) {
+  v += dpp_mov<kQuadXor1>(v);
+  v += dpp_mov<kQuadXor2>(v);
+  v += dpp_mov<kRowHalfMirror>(v);
+  v += dpp_mov<kRowMirror>(v);
+  if constexpr (L == 32) v += __float_as_int(xor_lane<16>(__int_as_float(v), lane));
+  return v;
+}
+
+// exclusive prefix sum inside segments
+template <int L>
+__device__ __forceinline__ int seg_excl_scan_i32(int v) {
+  int s = v;
+  s += dpp_or0<0x111, 0xF>(s);   // row_shr:1
+  s += dpp_or0<0x112, 0xF>(s);   // row_shr:2
+  s += dpp_or0<0x114, 0xF>(s);   // row_shr:4
+  s += dpp_or0<0x118, 0xF>(s);   // row_shr:8
+  if constexpr (L == 32) s += dpp_or0<kRowBcast15, 0xA>(s);   // rows 1, 3 += last lane of rows 0, 2
+  return s - v;
+}
+
+// bitonic sort of every segment, descending: stages below L alternate direction by lane bit K,
+// the last stage sorts every segment descending
+constexpr uint64_t seg_keep_max_mask(int K, int J, int L) {
+  uint64_t m = 0;
+  for (int i = 0; i < 64; ++i) {
+    const bool desc = K >= L || (i & K) == 0;
+    if (((i & J) == 0) == desc) m |= 1ull << i;
+  }
+  return m;
+}
+
+template <int K, int J, int L>
+__device__ __forceinline__ float seg_bitonic_step(float v, int lane) {
+  const float p = xor_lane<J>(v, lane);
+  return select_lanes(seg_keep_max_mask(K, J, L), fmaxf(v, p), fminf(v, p));
+}
+
+template <int K, int L>
+__device__ __forceinline__ float seg_bitonic_merge(float v, int lane) {
+  if constexpr (K >= 32) v = seg_bitonic_step<K, 16, L>(v, lane);
+  if constexpr (K >= 16) v = seg_bitonic_step<K, 8, L>(v, lane);
+  if constexpr (K >= 8) v = seg_bitonic_step<K, 4, L>(v, lane);
+  if constexpr (K >= 4) v = seg_bitonic_step<K, 2, L>(v, lane);
+  return seg_bitonic_step<K, 1, L>(v, lane);
+}
+
+template <int L>
+__device__ __forceinline__ float seg_sort_desc(float v, int lane) {
+  v = seg_bitonic_merge<2, L>(v, lane);
+  v = seg_bitonic_merge<4, L>(v, lane);
+  v = seg_bitonic_merge<8, L>(v, lane);
+  v = seg_bitonic_merge<16, L>(v, lane);
+  if constexpr (L == 32) v = seg_bitonic_merge<32, L>(v, lane);
+  return v;
+}
+
+// sum/count of the entries > thr among the first n of one segment's list (li = lane in segment;
+// nmax = the largest n of the wavefront's segments)
+template <int L>
+__device__ __forceinline__ void seg_list_sum_count(const float* cl, int n, int nmax, float thr, int li, int lane,
+                                                   double& s, int& c) {
+  double acc = 0.0;
+  int cnt = 0;
+  for (int p0 = 0; p0 < nmax; p0 += L) {
+    const int p = p0 + li;
+    const float v = p < n ? cl[p] : -INFINITY;
+    const bool k = v > thr;
+    acc += k ? (double)v : 0.0;
+    cnt += k ? 1 : 0;
+  }
+  s = seg_sum_f64<L>(acc, lane);
+  c = seg_sum_i32<L>(cnt, lane);
+}
+
+// one element (for z_y): unit-agnostic 32/16-bit buffer load at element offset j
+template <typename T>
+__device__ __forceinline__ float load_one(rsrc_t r, uint32_t byte_off) {
+  if constexpr (std::is_same<T, float>::value)
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+  else
+    return widen16<T>(__builtin_amdgcn_raw_buffer_load_b16(r, byte_off, 0, 0));
+}
+
+constexpr uint32_t kOffNone = 0x7FFFFFF0u;   // a buffer offset past every resource: access dropped
+
+// A wavefront handles groups g = w + k*stride of R consecutive rows (rows g*R + s, s < R); lane j
+// collects the results of the wavefront's row j = k*R + s.  The group's rows share one buffer
+// resource; units past a row's end are masked on load and dropped on store.
+template <typename T, int MODE, int L, int NV, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ z,
+                                                       const int64_t* __restrict__ tgt, int64_t N, int C,
+                                                       Outs o) {
+  constexpr int R = kWave / L;
+  constexpr int U = kUnit<T, V4>;
+  constexpr int E = U * NV;
+  static_assert(E <= 32, "one mask bit per register slot");
+  static_assert(MODE != kCand, "candidate lists: fwl_wave_rows");
+  static_assert(std::is_same<T, float>::value || MODE == kGrad, "16-bit logits: fused op only");
+  __shared__ float s_list[kWavesPerBlock][(E + 1) * kWave];
+  __shared__ double s_wsum[kWavesPerBlock];
+  const int lane = lane_id();
+  const int wid = uniform((int)(threadIdx.x >> 6));
+  const int seg = lane / L;          // segment of this lane
+  const int li = lane % L;           // lane within the segment
+  float* cl = s_list[wid];
+  const int64_t G = (N + R - 1) / R;                        // row groups
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+  const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;
+  const int ngroups = w < G ? (int)((G - 1 - w) / stride + 1) : 0;   // <= kGroupsPerWave (host grid)
+  const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
+  const int units_row = C / U;                               // V4 rows: C is a multiple of U
+  auto group_rows = [&](int k) -> int {
+    const int64_t r0 = (w + (int64_t)k * stride) * R;
+    return k < ngroups ? (int)(N - r0 < R ? N - r0 : R) : 0;
+  };
+  auto group_rsrc = [&](int k) {
+    const int rows = group_rows(k);
+    const char* base = static_cast<const char*>(z) + (w + (int64_t)(k < ngroups ? k : 0) * stride) * R * (int64_t)row_bytes;
+    return make_rsrc(base, (uint32_t)rows * row_bytes);
+  };
+  // labels: lane j holds the label of the wavefront's row j (group j / R, segment j % R)
+  int64_t my_y = 0;
+  {
+    const int kk = lane / R, ss = lane % R;
+    const int64_t r = (w + (int64_t)kk * stride) * R + ss;
+    if (kk < ngroups && r < N) my_y = tgt[r];
+  }
+  auto seg_label = [&](int k) -> int64_t {   // label of this lane's segment row in group k
+    int64_t y = 0;
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      const int src = (k * R + s) & 63;
+      const int64_t v = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), src) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((int)my_y, src);
+      y = s == seg ? v : y;
+    }
+    return y;
+  };
+  auto label_off = [&](int64_t y) -> uint32_t {
+    return (y >= 0 && y < C) ? (uint32_t)seg * row_bytes + (uint32_t)(y * kElemBytes<T>) : kOffNone;
+  };
+  float my_H = 0.0f, my_loss = 0.0f;
+  int my_kappa = 0;
+  double lsum = 0.0;
+  float x[E];
+  auto load_group = [&](rsrc_t rs, float* xx) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int u = li + L * k;
+      load_unit<T, V4>(rs, u < units_row ? (uint32_t)(seg * (row_bytes / (U * kElemBytes<T>)) + u) : (kOffNone >> 4),
+                       xx + U * k);
+    }
+  };
+  if (ngroups > 0) {
+    rsrc_t rs = group_rsrc(0);
+    load_group(rs, x);
+    float zy_next = load_one<T>(rs, label_off(seg_label(0)));
+    __builtin_amdgcn_sched_barrier(0);   // mirror of the loop's stores (see mirror_row_stores)
+    {
+      const rsrc_t none = make_rsrc(nullptr, 0u);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        if constexpr (MODE == kGrad) store_zero_unit<T, V4>(none, (uint32_t)(li + L * k));
+        else if constexpr (V4) __builtin_amdgcn_raw_buffer_store_b32(0u, none, 4u * (uint32_t)(li + L * k), 0, kNonTemporal);
+        else __builtin_amdgcn_raw_buffer_store_b8((unsigned char)0, none, (uint32_t)(li + L * k), 0, kNonTemporal);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    int k = 0;
+    do {
+      const int rows = group_rows(k);
+      const bool valid = seg < rows;
+      const int64_t y64 = seg_label(k);
+      const bool yok = y64 >= 0 && y64 < C;
+      const int yr = yok ? (int)y64 : -1;
+      const float zy = zy_next;
+      // mask units past the row end and phantom segments
+#pragma unroll
+      for (int kk = 0; kk < NV; ++kk) {
+        const bool ok = valid && li + L * kk < units_row;
+#pragma unroll
+        for (int e = 0; e < U; ++e) x[U * kk + e] = ok ? x[U * kk + e] : -INFINITY;
+      }
+      float lm = x[0];
+#pragma unroll
+      for (int i = 1; i < E; ++i) lm = fmaxf(lm, x[i]);
+      const float m = seg_max_f32<L>(lm, lane);
+      const float t0 = bound_below_max(m);
+      unsigned cm = 0;
+#pragma unroll
+      for (int i = 0; i < E; ++i) cm |= (unsigned)(x[i] > t0) << i;
+      const int cnt = __popc(cm);
+      const int base = seg_excl_scan_i32<L>(cnt);
+      const int n = seg_sum_i32<L>(cnt, lane);
+      float* cls = cl + seg * (L * E);   // this segment's list
+      {
+        int pos = base;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          const int bit = (cm >> i) & 1;
+          cl[bit ? seg * (L * E) + pos : E * kWave + lane] = x[i];
+          pos += bit;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      // next group's loads into the same registers
+      const rsrc_t rs_next = group_rsrc(k + 1 < ngroups ? k + 1 : 0);
+      const bool has_next = k + 1 < ngroups;
+      load_group(has_next ? rs_next : make_rsrc(z, 0u), x);
+      zy_next = load_one<T>(has_next ? rs_next : make_rsrc(z, 0u), label_off(seg_label(k + 1 < ngroups ? k + 1 : k)));
+
+      double tau = NAN;
+      int kappa = 0;
+      unsigned sm = 0;
+      const bool big = ballot(n > L) != 0;
+      if (!big) {
+        const float c = li < n ? cls[li] : -INFINITY;
+        float v = li < n ? c + 0.0f : -INFINITY;   // + 0.0f: -0.0 -> +0.0 before min/max
+        v = seg_sort_desc<L>(v, lane);
+        const double S = scan_f64<L>(li < n ? (double)v : 0.0);
+        const double f = (S - 1.0) / (double)(li + 1);
+        const double fmax_seg = seg_max_f64<L>(li < n ? f : -INFINITY, lane);   // every lane takes part
+        tau = n > 0 ? clamp_below_max(fmax_seg, m) : NAN;
+        const uint64_t sup = ballot(li < n && c > rd32(tau));
+        const unsigned segbits = (unsigned)((sup >> (seg * L)) & (L == 32 ? 0xFFFFFFFFull : 0xFFFFull));
+        kappa = __popc(segbits);
+        unsigned sb = base < L ? segbits >> base : 0u;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          const unsigned bit = (cm >> i) & 1u;
+          sm |= (bit & sb) << i;
+          sb >>= bit;
+        }
+      } else {
+        // fixed-point iterations per segment over its list, until every segment has converged
+        const int nmax = (int)wave_max_f32((float)n);
+        double t = (double)t0, s, s2;
+        int c, c2;
+        seg_list_sum_count<L>(cls, n, nmax, t0, li, lane, s, c);
+        bool done = n == 0;
+        for (int it = 0; it <= nmax + 1; ++it) {
+          if (ballot(!done) == 0) break;
+          const double tn = (s - 1.0) / (double)c;
+          seg_list_sum_count<L>(cls, n, nmax, rd32(tn), li, lane, s2, c2);
+          if (!done) {
+            if (c2 == c || !(tn > t)) {
+              tau = tn;
+              kappa = c2;
+              done = true;
+            } else {
+              t = tn;
+              s = s2;
+              c = c2;
+            }
+          }
+        }
+        const double tc = n > 0 ? clamp_below_max(tau, m) : tau;
+        const bool clamped = tc != tau && n > 0;
+        if (ballot(clamped) != 0) {
+          double s3;
+          int k3;
+          seg_list_sum_count<L>(cls, n, nmax, rd32(tc), li, lane, s3, k3);
+          if (clamped) kappa = k3;
+        }
+        tau = tc;
+        const float Hc = rd32(tau);
+        int pos = base;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          if ((cm >> i) & 1u) {
+            sm |= (unsigned)(cls[pos] > Hc) << i;
+            ++pos;
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      const float Hf = rd32(tau);
+      const float inv = (float)(o.scale / (double)kappa);
+      const int64_t row0 = (w + (int64_t)k * stride) * R;   // first row of this group
+      const int qy = yr / U, ky = yr >= 0 ? qy / L : -1, lyl = qy % L, ey = yr % U;
+      if constexpr (MODE == kGrad) {
+        const rsrc_t outr = make_rsrc(static_cast<char*>(o.grad) + row0 * (int64_t)row_bytes,
+                                      (uint32_t)rows * row_bytes);
+        const uint32_t b_inv = encode<T>(inv), b_lab_in = encode<T>(inv - o.scale_f);
+        const uint32_t b_lab_out = encode<T>(0.0f - o.scale_f);
+#pragma unroll
+        for (int kk = 0; kk < NV; ++kk) {
+          const int u = li + L * kk;
+          uint32_t g[U];
+#pragma unroll
+          for (int e = 0; e < U; ++e) g[e] = ((sm >> (U * kk + e)) & 1u) ? b_inv : 0u;
+          if (kk == ky && li == lyl) {
+#pragma unroll
+            for (int e = 0; e < U; ++e) g[e] = e == ey ? (((sm >> (U * kk + e)) & 1u) ? b_lab_in : b_lab_out) : g[e];
+          }
+          store_unit_bits<T, V4>(outr, u < units_row ? (uint32_t)(seg * units_row + u) : (kOffNone >> 4), g);
+        }
+      } else {
+        const rsrc_t outr = make_rsrc(o.mask + row0 * (int64_t)C, (uint32_t)(rows * C));
+#pragma unroll
+        for (int kk = 0; kk < NV; ++kk) {
+          const int u = li + L * kk;
+          if constexpr (V4) {
+            const unsigned b4 = (sm >> (4 * kk)) & 0xFu;
+            const unsigned mk = (b4 & 1u) | ((b4 & 2u) << 7) | ((b4 & 4u) << 14) | ((b4 & 8u) << 21);
+            __builtin_amdgcn_raw_buffer_store_b32(mk, outr, u < units_row ? (uint32_t)(seg * C + 4 * u) : kOffNone, 0,
+                                                  kNonTemporal);
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b8((unsigned char)((sm >> kk) & 1u), outr,
+                                                 u < units_row ? (uint32_t)(seg * C + u) : kOffNone, 0, kNonTemporal);
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      // per-row results: segment s of group k is the wavefront's row k*R + s, kept in that lane
+      const float loss = (float)((1.0 - (double)(yok ? zy : NAN)) + tau);
+#pragma unroll
+      for (int s = 0; s < R; ++s) {
+        const float Hs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Hf), s * L));
+        const float Ls = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(loss), s * L));
+        const int Ks = __builtin_amdgcn_readlane(kappa, s * L);
+        if (s < rows) lsum += (double)Ls;
+        if (lane == k * R + s) {
+          my_H = Hs;
+          my_loss = Ls;
+          my_kappa = Ks;
+        }
+      }
+    } while (++k < ngroups);
+  }
+  {
+    const int kk = lane / R, ss = lane % R;
+    const int64_t r = (w + (int64_t)kk * stride) * R + ss;
+    if (kk < ngroups && r < N) {
+      if (o.H) o.H[r] = my_H;
+      if (o.loss) o.loss[r] = my_loss;
+      if (o.kappa) o.kappa[r] = my_kappa;
+    }
+  }
+  if (lane == 0) s_wsum[wid] = lsum;
+  __syncthreads();
+  const double bsum = (s_wsum[0] + s_wsum[1]) + (s_wsum[2] + s_wsum[3]);
+  mean_epilogue(bsum, o);
+}
+
+// ------------------------------------------------------------------------------------------------
 // fwl_block_rows: one block per row, streaming with LDS candidate lists
 
 struct BlockShared {
@@ -1667,6 +2064,52 @@ void dispatch_wave(const void* z, const int64_t* y, int64_t N, int C, bool v4, c
   }
 }
 
+template <typename T, int MODE, int L, int NV, bool V4>
+void launch_seg(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+  constexpr int R = kWave / L;
+  const void* k = reinterpret_cast<const void*>(&fwl_seg_rows<T, MODE, L, NV, V4>);
+  const int64_t groups = (N + R - 1) / R;
+  // the wave grid over row groups (R rows each); a wavefront takes at most 64 / R groups
+  const int resident = resident_blocks(k);
+  const int cus = device_cus();
+  const int64_t group_bytes = (int64_t)R * C * kElemBytes<T>;
+  int per_cu = (int)((8000 + group_bytes - 1) / group_bytes);
+  if (per_cu < 2) per_cu = 2;
+  const int per_cu_resident = cus > 0 && resident > 0 ? resident / cus : 0;
+  if (per_cu_resident > 0 && per_cu > per_cu_resident) per_cu = per_cu_resident;
+  const int target = cus > 0 ? per_cu * cus : (resident > 0 ? resident : kMaxBlocksWave);
+  const int64_t per_block = (int64_t)kWavesPerBlock * (kWave / R);
+  const int64_t min_blocks = (groups + per_block - 1) / per_block;
+  const int cap = (int)(min_blocks > kMaxBlocksWave ? min_blocks : kMaxBlocksWave);
+  int64_t g = persistent_grid(groups, kWavesPerBlock, target, cap);
+  if (g < min_blocks) g = min_blocks;
+  hipLaunchKernelGGL((fwl_seg_rows<T, MODE, L, NV, V4>), dim3((int)g), dim3(kBlock), 0, s, z, y, N, C, o);
+}
+
+// short rows: segments of 16 or 32 lanes; returns false when the row is too long for them
+template <typename T, int MODE>
+bool dispatch_seg(const void* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o, hipStream_t s) {
+  if constexpr (MODE == kCand) {
+    return false;
+  } else {
+    if (v4) {
+      constexpr int U = kUnit<T, true>;
+      const int units = C / U;
+      if (units <= 16) launch_seg<T, MODE, 16, 1, true>(z, y, N, C, o, s);
+      else if (units <= 32) launch_seg<T, MODE, 16, 2, true>(z, y, N, C, o, s);
+      else if (units <= 64) launch_seg<T, MODE, 32, 2, true>(z, y, N, C, o, s);
+      else return false;
+    } else {
+      if (C <= 16) launch_seg<T, MODE, 16, 1, false>(z, y, N, C, o, s);
+      else if (C <= 32) launch_seg<T, MODE, 16, 2, false>(z, y, N, C, o, s);
+      else if (C <= 64) launch_seg<T, MODE, 16, 4, false>(z, y, N, C, o, s);
+      else if (C <= 128) launch_seg<T, MODE, 32, 4, false>(z, y, N, C, o, s);
+      else return false;
+    }
+    return true;
+  }
+}
+
 template <typename T, int MODE, bool V4>
 void launch_block(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   const void* k = reinterpret_cast<const void*>(&fwl_block_rows<T, MODE, V4>);
@@ -1712,9 +2155,10 @@ int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scal
   // measured on MI355X: registers win up to 2048 for 128-bit rows, up to 1024 for rows accessed
   // one element at a time; one streaming wavefront per row up to 8192; one block per row beyond
   const int max_wave_c = v4 ? kMaxWaveC : kMaxWaveC1;
-  if (path == 0) path = C <= max_wave_c ? 1 : (C <= kMaxStreamC ? 4 : 2);
-  if (path == 1 && C > max_wave_c) path = 4;
-  if (path == 1) {
+  if (path == 0) path = C <= max_wave_c ? 6 : (C <= kMaxStreamC ? 4 : 2);
+  if ((path == 1 || path == 6) && C > max_wave_c) path = 4;
+  if (path == 6 && dispatch_seg<T, MODE>(z, y, N, C, v4, o, s)) return launch_status();
+  if (path == 1 || path == 6) {
     dispatch_wave<T, MODE>(z, y, N, C, v4, o, s);
   } else if (path == 4 || path == 5) {
     if (v4) launch_wave_stream<T, MODE, true>(z, y, N, C, o, s);
@@ -1909,7 +2353,7 @@ int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_
 }
 
 int fwl_set_params(int path, int cand_cap) {
-  if (path < 0 || path > 5 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
+  if (path < 0 || path > 6 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
   g_path = path;
   g_cap = cand_cap;
   return FWL_OK;

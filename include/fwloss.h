@@ -135,14 +135,16 @@ int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_
 /* Process-wide dispatch switches, the GPU counterpart of the reference CPU path's set_params
  * (src/cpu/fw_cpu.cpp:758-763, used by its tests to force each branch).  Not thread-safe; meant
  * for tests and tuning.
- *   path:      0 = automatic (1 for C <= 2048, or C <= 1024 when rows are not 16-byte aligned;
- *              4 for C <= 8192; else 2),
+ *   path:      0 = automatic (6 for short rows, 1 for C <= 2048 or C <= 1024 when rows are not
+ *              16-byte aligned, 4 for C <= 8192, else 2),
  *              1 = one wavefront per row with the row in registers (C <= 2048, or 1024 for rows
  *              that are not 16-byte aligned; larger C runs path 4),
  *              2 = one block per row, streamed, with LDS candidate lists,
  *              3 = path 2 with the generic multi-pass solve forced,
  *              4 = one wavefront per row, streamed, with an LDS candidate list,
- *              5 = path 4 with the generic multi-pass solve forced.
+ *              5 = path 4 with the generic multi-pass solve forced,
+ *              6 = short rows: 16- or 32-lane segments of a wavefront, 4 or 2 rows per
+ *              iteration (rows of up to 64 units; longer rows and candidate lists run path 1).
  *   cand_cap:  LDS candidate capacity per wavefront of paths 2 and 4, in [64, 512] (512 =
  *              default); smaller values make rows overflow into the generic solve sooner.
  * Returns FWL_ERR_INVALID_ARG for values out of range. */

@@ -53,7 +53,7 @@ def check(ext, dev, z16, y, scale=-1.0, rdiv=-1.0):
 
 
 @pytest.mark.parametrize("name", sorted(DTYPES))
-@pytest.mark.parametrize("C", [1, 10, 100, 1000, 1024, 2048, 2999, 3000, 8200, 20000])
+@pytest.mark.parametrize("C", [1, 10, 64, 100, 128, 256, 512, 1000, 1024, 2048, 2999, 3000, 8200, 20000])
 def test_dtype_shapes(ext, dev, name, C):
     N = 96 if C >= 8192 else 300
     z16, y = case(C, N, C + 5, DTYPES[name])
@@ -62,7 +62,7 @@ def test_dtype_shapes(ext, dev, name, C):
 
 
 @pytest.mark.parametrize("name", sorted(DTYPES))
-@pytest.mark.parametrize("path,cap", [(1, 512), (2, 512), (2, 64), (3, 512), (4, 512), (4, 64), (5, 512)])
+@pytest.mark.parametrize("path,cap", [(1, 512), (2, 512), (2, 64), (3, 512), (4, 512), (4, 64), (5, 512), (6, 512)])
 def test_dtype_forced_paths(ext, dev, reset_params16, name, path, cap):
     z16, y = case(1000, 200, 77, DTYPES[name])
     print(f"{name} path={path} cap={cap}", flush=True)

@@ -121,8 +121,8 @@ def test_drop_in_large_ops(ext, dev, cfg):
 
 # ---------------------------------------------------------------- every kernel path, same answers
 
-@pytest.mark.parametrize("path,cap", [(1, 512), (2, 512), (2, 64), (3, 512), (4, 512), (4, 64), (5, 512)])
-@pytest.mark.parametrize("C", [10, 100, 1000, 1024, 2999, 3000])
+@pytest.mark.parametrize("path,cap", [(1, 512), (2, 512), (2, 64), (3, 512), (4, 512), (4, 64), (5, 512), (6, 512)])
+@pytest.mark.parametrize("C", [10, 64, 100, 256, 1000, 1024, 2999, 3000])
 def test_forced_paths(ext, dev, reset_params, path, cap, C):
     rng = np.random.default_rng(C)
     z = rng.standard_normal((300, C)).astype(np.float32)
@@ -166,6 +166,25 @@ def test_shapes(ext, dev, C):
     y = rng.integers(0, C, N)
     print(f"shape N={N} C={C}", flush=True)
     assert_parity(fused(ext, *to_dev(dev, z, y)), oracle.definition(z, y), z)
+
+
+@pytest.mark.parametrize("C", [4, 16, 17, 32, 33, 100, 128, 129, 256])
+@pytest.mark.parametrize("N", [1, 2, 3, 5, 131])
+def test_short_rows_groups(ext, dev, N, C):
+    # short rows run R = 2 or 4 rows per wavefront iteration: every remainder of N by R, flat rows
+    # (more candidates than lanes per row) and exact ties
+    rng = np.random.default_rng(N * 1000 + C)
+    z = rng.standard_normal((N, C)).astype(np.float32)
+    z[::3] *= np.float32(0.01)
+    z[1::4] = np.round(z[1::4] * 2) / 2
+    y = rng.integers(0, C, N)
+    print(f"short rows N={N} C={C}", flush=True)
+    assert_parity(fused(ext, *to_dev(dev, z, y)), oracle.definition(z, y), z)
+    zt, yt = to_dev(dev, z, y)
+    H, losses, mean, kappa, sel = ext.fw_forward_small(zt, yt)
+    torch.cuda.synchronize()
+    ref = oracle.definition(z, y)
+    np.testing.assert_array_equal(sel.cpu().numpy(), z > ref["tau"][:, None])
 
 
 def test_edge_rows(ext, dev):

@@ -136,7 +136,7 @@ def test_set_params_validation_and_round_trip():
     assert L.fwl_get_params(ctypes.byref(p), ctypes.byref(c)) == 0
     saved = (p.value, c.value)
     try:
-        assert L.fwl_set_params(6, 512) == 1
+        assert L.fwl_set_params(7, 512) == 1
         assert L.fwl_set_params(-1, 512) == 1
         assert L.fwl_set_params(2, 63) == 1
         assert L.fwl_set_params(2, 513) == 1
