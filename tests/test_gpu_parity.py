@@ -289,6 +289,27 @@ def test_full_size(ext, dev, cfg):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("N,C", [(1_000_003, 16), (300_001, 100), (65_537, 1025), (9_999, 8193)])
+def test_large_batches(ext, dev, N, C):
+    # grid limits of every kernel family: more than 2048 blocks of short rows, odd N, unaligned C
+    rng = np.random.default_rng(N + C)
+    z = rng.standard_normal((N, C), dtype=np.float32)
+    y = rng.integers(0, C, N)
+    print(f"large batch N={N} C={C}", flush=True)
+    zt, yt = to_dev(dev, z, y)
+    H, loss, mean, kappa, grad = ext.fw_forward_backward(zt, yt)
+    torch.cuda.synchronize()
+    _row_properties(zt, yt, H, loss, kappa, grad, 1.0 / N)
+    assert abs(mean.item() - loss.double().mean().item()) <= 1e-6 * max(1.0, abs(mean.item()))
+    rows = rng.choice(N, size=48, replace=False)
+    ref = oracle.definition(z[rows], y[rows], scale=1.0 / N)
+    sub = dict(H=H[rows].cpu().numpy(), loss=loss[rows].cpu().numpy(), kappa=kappa[rows].cpu().numpy(),
+               grad=grad[rows].cpu().numpy(), mean=None)
+    assert_parity(sub, ref, z[rows])
+    del zt, grad
+    torch.cuda.empty_cache()
+
+
 # ---------------------------------------------------------------- autograd API and the C ABI
 
 @pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
