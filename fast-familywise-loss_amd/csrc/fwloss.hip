@@ -1854,6 +1854,44 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
 // ------------------------------------------------------------------------------------------------
 // two-op backward kernels of the drop-in interface
 
+// grad = (mask ? inv : 0) - [j == y] * scale, one wavefront per row (rows w + k*stride, k < 64).
+// The wavefront's rows form one sequence of rounds (kMaskSlots mask units per lane, a unit being 4
+// mask bytes and 16 gradient bytes, or 1 and 4 for rows that are not 16-byte aligned); the mask
+// loads of the next round are issued before the gradient stores of the current one.
+constexpr int kMaskSlots = 4;
+
+template <bool V4>
+__device__ __forceinline__ void mask_round_load(rsrc_t m, int round, int lane, uint32_t* mk) {
+#pragma unroll
+  for (int u = 0; u < kMaskSlots; ++u) {
+    const uint32_t q = (uint32_t)(round * kWave * kMaskSlots + lane + kWave * u);
+    if constexpr (V4) mk[u] = __builtin_amdgcn_raw_buffer_load_b32(m, 4u * q, 0, kNonTemporal);
+    else mk[u] = __builtin_amdgcn_raw_buffer_load_b8(m, q, 0, kNonTemporal);
+  }
+}
+
+template <bool V4>
+__device__ __forceinline__ void mask_round_store(rsrc_t g, int round, int lane, const uint32_t* mk, int yr,
+                                                 uint32_t b_inv, uint32_t b_lab_in, uint32_t b_lab_out) {
+#pragma unroll
+  for (int u = 0; u < kMaskSlots; ++u) {
+    const int q = round * kWave * kMaskSlots + lane + kWave * u;
+    if constexpr (V4) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool sel = ((mk[u] >> (8 * e)) & 0xFFu) != 0u;
+        w[e] = 4 * q + e == yr ? (sel ? b_lab_in : b_lab_out) : (sel ? b_inv : 0u);
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(v4u{w[0], w[1], w[2], w[3]}, g, 16u * (uint32_t)q, 0, kNonTemporal);
+    } else {
+      const bool sel = (mk[u] & 0xFFu) != 0u;
+      const uint32_t w = q == yr ? (sel ? b_lab_in : b_lab_out) : (sel ? b_inv : 0u);
+      __builtin_amdgcn_raw_buffer_store_b32(w, g, 4u * (uint32_t)q, 0, kNonTemporal);
+    }
+  }
+}
+
 template <bool V4>
 __global__ __launch_bounds__(kBlock) void fwl_mask_to_grad(const int64_t* __restrict__ tgt,
                                                            const uint8_t* __restrict__ mask,
@@ -1863,36 +1901,41 @@ __global__ __launch_bounds__(kBlock) void fwl_mask_to_grad(const int64_t* __rest
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
-  for (int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid; r < N; r += stride) {
-    const int64_t y64 = tgt[r];
-    const int yr = (y64 >= 0 && y64 < C) ? (int)y64 : -1;
-    const float inv = (float)(scale / (double)kap[r]);
-    const uint8_t* mr = mask + r * (int64_t)C;
-    float* gr = grad + r * (int64_t)C;
-    if constexpr (V4) {
-      const int nvec = C >> 2;
-      for (int q = lane; q < nvec; q += kWave) {
-        const unsigned mk = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(mr) + q);
-        v4f g;
-        g.x = (mk & 0xFFu) ? inv : 0.0f;
-        g.y = (mk & 0xFF00u) ? inv : 0.0f;
-        g.z = (mk & 0xFF0000u) ? inv : 0.0f;
-        g.w = (mk & 0xFF000000u) ? inv : 0.0f;
-        const int d = yr - 4 * q;
-        if (d == 0) g.x -= scale_f;
-        else if (d == 1) g.y -= scale_f;
-        else if (d == 2) g.z -= scale_f;
-        else if (d == 3) g.w -= scale_f;
-        __builtin_nontemporal_store(g, reinterpret_cast<v4f*>(gr) + q);
-      }
-    } else {
-      for (int j = lane; j < C; j += kWave) {
-        float g = mr[j] ? inv : 0.0f;
-        if (j == yr) g -= scale_f;
-        __builtin_nontemporal_store(g, gr + j);
-      }
-    }
+  const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;
+  const int nrows = w < N ? (int)((N - 1 - w) / stride + 1) : 0;   // <= kRowsPerWave (host grid)
+  const int units = V4 ? C / 4 : C;
+  const int rounds = (units + kWave * kMaskSlots - 1) / (kWave * kMaskSlots);
+  const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
+  const int my_kap = lane < nrows ? kap[w + (int64_t)lane * stride] : 0;
+  auto mask_rsrc = [&](int k) {
+    return k < nrows ? make_rsrc(mask + (w + (int64_t)k * stride) * C, (uint32_t)C) : make_rsrc(mask, 0u);
+  };
+  if (nrows == 0) return;
+  const int items = nrows * rounds;   // (row, round) pairs, row-major
+  uint32_t mk[kMaskSlots];
+  mask_round_load<V4>(mask_rsrc(0), 0, lane, mk);
+  __builtin_amdgcn_sched_barrier(0);   // mirror of the loop's stores (see mirror_row_stores)
+  {
+    uint32_t zero[kMaskSlots] = {};
+    mask_round_store<V4>(make_rsrc(nullptr, 0u), 0, lane, zero, -1, 0u, 0u, 0u);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  int it = 0;
+  do {
+    const int k = it / rounds, rd = it - k * rounds;
+    const int kn = (it + 1) / rounds, rdn = it + 1 - kn * rounds;
+    uint32_t cur[kMaskSlots];
+#pragma unroll
+    for (int u = 0; u < kMaskSlots; ++u) cur[u] = mk[u];
+    mask_round_load<V4>(it + 1 < items ? mask_rsrc(kn) : make_rsrc(mask, 0u), rdn, lane, mk);
+    const int64_t y = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
+                      (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
+    const int yr = (y >= 0 && y < C) ? (int)y : -1;
+    const float inv = (float)(scale / (double)__builtin_amdgcn_readlane(my_kap, k));
+    const rsrc_t g = make_rsrc(grad + (w + (int64_t)k * stride) * C, 4u * (uint32_t)C);
+    mask_round_store<V4>(g, rd, lane, cur, yr, __float_as_uint(inv), __float_as_uint(inv - scale_f),
+                         __float_as_uint(0.0f - scale_f));
+  } while (++it < items);
 }
 
 template <bool V4>
@@ -2304,12 +2347,16 @@ int fwl_backward_small(const int64_t* targets, const uint8_t* selected, const in
   const double scale = 1.0 / (double)N;
   const bool v4 = (C % 4) == 0 && aligned(selected, 4) && aligned(grad, 16);
   const int Ci = (int)C;
-  if (v4)
-    hipLaunchKernelGGL((fwl_mask_to_grad<true>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, targets,
-                       selected, kappa, N, Ci, scale, (float)scale, grad);
-  else
-    hipLaunchKernelGGL((fwl_mask_to_grad<false>), dim3(blocks_wave(N)), dim3(kBlock), 0, stream, targets,
-                       selected, kappa, N, Ci, scale, (float)scale, grad);
+  // at most 64 rows per wavefront (the labels and kappas of its rows are gathered once)
+  if (v4) {
+    const int grid = wave_grid(N, 5 * C, resident_blocks(reinterpret_cast<const void*>(&fwl_mask_to_grad<true>)));
+    hipLaunchKernelGGL((fwl_mask_to_grad<true>), dim3(grid), dim3(kBlock), 0, stream, targets, selected, kappa, N,
+                       Ci, scale, (float)scale, grad);
+  } else {
+    const int grid = wave_grid(N, 5 * C, resident_blocks(reinterpret_cast<const void*>(&fwl_mask_to_grad<false>)));
+    hipLaunchKernelGGL((fwl_mask_to_grad<false>), dim3(grid), dim3(kBlock), 0, stream, targets, selected, kappa, N,
+                       Ci, scale, (float)scale, grad);
+  }
   return launch_status();
 }
 
