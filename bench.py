@@ -175,11 +175,15 @@ def main():
     nbytes = alg_bytes(N, C, ELEM_BYTES[args.dtype])
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
 
-    # the reference's two-op sequence (fw_forward_small + fw_backward_small; fp32 only), for comparison
+    # the reference harness's two-op sequence (fp32 only), for comparison: the small ops below
+    # K = 10000, the candidate-list ops above (benchmarks/cuda_benchmarks/CE_FW_perf.py:76-88)
     def two_op(i):
         zt, yt = sets[i % len(sets)]
-        H, losses, mean, kappa, sel = fwloss.fw_forward_small(zt, yt)
-        return fwloss.fw_backward_small(yt, sel, kappa)
+        if C < 10000:
+            H, losses, mean, kappa, sel = fwloss.fw_forward_small(zt, yt)
+            return fwloss.fw_backward_small(yt, sel, kappa)
+        H, losses, mean, kappa, cb, ci, cc = fwloss.fw_forward(zt, yt)
+        return fwloss.fw_backward(zt, yt, H, kappa, cb, ci, cc)
     two_op_ms = None
     if args.dtype == "f32":
         for i in range(5):

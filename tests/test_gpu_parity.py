@@ -310,6 +310,62 @@ def test_large_batches(ext, dev, N, C):
     torch.cuda.empty_cache()
 
 
+# ---------------------------------------------------------------- graphs and streams
+
+def test_graph_capture_replays(ext, dev):
+    """The fused op allocates nothing on the device path and leaves its workspace zeroed, so it can be
+    captured in a HIP graph: every replay must equal the eager result (the mean's ticket counter
+    resets inside the kernel)."""
+    z, y = data.make("cfg2", N=1000, seed=21)
+    zt, yt = to_dev(dev, z, y)
+    eager = ext.fw_forward_backward(zt, yt)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):   # warm the per-stream workspace outside the capture
+            ext.fw_forward_backward(zt, yt)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ext.fw_forward_backward(zt, yt)
+    print("graph replays", flush=True)
+    for it in range(5):
+        g.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(out, eager):
+            assert torch.equal(a, b), f"replay {it} differs from the eager result"
+        _ = ext.fw_forward_backward(zt, yt)   # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_concurrent_streams(ext, dev):
+    """Two streams run the fused op concurrently, each with its own cached workspace."""
+    z1, y1 = data.make("cfg2", N=4096, seed=31)
+    z2, y2 = data.make("cfg3", N=8192, seed=32)
+    a1, b1 = to_dev(dev, z1, y1)
+    a2, b2 = to_dev(dev, z2, y2)
+    r1 = ext.fw_forward_backward(a1, b1)
+    r2 = ext.fw_forward_backward(a2, b2)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    print("concurrent streams", flush=True)
+    for _ in range(10):
+        with torch.cuda.stream(s1):
+            o1 = ext.fw_forward_backward(a1, b1)
+        with torch.cuda.stream(s2):
+            o2 = ext.fw_forward_backward(a2, b2)
+        outs.append((o1, o2))
+    torch.cuda.synchronize()
+    for o1, o2 in outs:
+        for a, b in zip(o1, r1):
+            assert torch.equal(a, b)
+        for a, b in zip(o2, r2):
+            assert torch.equal(a, b)
+
+
 # ---------------------------------------------------------------- autograd API and the C ABI
 
 @pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
