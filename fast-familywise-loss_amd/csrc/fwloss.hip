@@ -486,17 +486,16 @@ __device__ __forceinline__ void load_row(rsrc_t row, int lane, float* x) {
   for (int k = 0; k < NV; ++k) load_unit<T, VEC>(row, (uint32_t)(lane + kWave * k), x + kUnit<T, VEC> * k);
 }
 
-// set the register slots past the row end to -inf (only the last partial units need it)
+// set the register slots past the row end to -inf (only the last, possibly partial, units need it;
+// fp32 rows of any length use 128-bit units, their last unit partly past the row)
 template <typename T, int NV, bool VEC>
 __device__ __forceinline__ void mask_tail(float* x, int C, int lane) {
   constexpr int U = kUnit<T, VEC>;
-  const int units = C / U;   // C is a multiple of U
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    if (kWave * (k + 1) > units) {
-      const bool ok = lane + kWave * k < units;
+    if (kWave * (k + 1) * U > C) {
 #pragma unroll
-      for (int e = 0; e < U; ++e) x[U * k + e] = ok ? x[U * k + e] : -INFINITY;
+      for (int e = 0; e < U; ++e) x[U * k + e] = U * (lane + kWave * k) + e < C ? x[U * k + e] : -INFINITY;
     }
   }
 }
@@ -2092,12 +2091,18 @@ template <typename T, int MODE>
 void dispatch_wave(const void* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
                    hipStream_t s) {
   if (v4) {
+    // per-lane work grows with NV whatever the row length: tiers at every 64 units up to 6
     constexpr int U = kUnit<T, true>;
     const int units = (C + U - 1) / U;
     if (units <= 64) launch_wave<T, MODE, 1, true>(z, y, N, C, o, s);
     else if (units <= 128) launch_wave<T, MODE, 2, true>(z, y, N, C, o, s);
+    else if (units <= 192) launch_wave<T, MODE, 3, true>(z, y, N, C, o, s);
     else if (units <= 256) launch_wave<T, MODE, 4, true>(z, y, N, C, o, s);
-    else if constexpr (U == 4) launch_wave<T, MODE, 8, true>(z, y, N, C, o, s);
+    else if constexpr (U == 4) {
+      if (units <= 320) launch_wave<T, MODE, 5, true>(z, y, N, C, o, s);
+      else if (units <= 384) launch_wave<T, MODE, 6, true>(z, y, N, C, o, s);
+      else launch_wave<T, MODE, 8, true>(z, y, N, C, o, s);
+    }
   } else {
     if (C <= 64) launch_wave<T, MODE, 1, false>(z, y, N, C, o, s);
     else if (C <= 128) launch_wave<T, MODE, 2, false>(z, y, N, C, o, s);
@@ -2193,14 +2198,19 @@ int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scal
     if (o.mean != nullptr) hipLaunchKernelGGL(fwl_empty_mean, dim3(1), dim3(1), 0, s, o.mean, reduce_div);
     return launch_status();
   }
-  const bool v4 = (C % kUnit<T, true>) == 0 && aligned(z, 16) && out_v4_ok;
+  // 128-bit units: rows of 16-byte multiples from a 16-byte aligned start; fp32 rows of any length
+  // also take them when the outputs are fp32 (the buffer range check is per dword: a last unit that
+  // runs past the row loads zeros there and stores nothing there; unaligned starts are supported)
+  const bool aligned_rows = (C % kUnit<T, true>) == 0 && aligned(z, 16) && out_v4_ok;
+  const bool v4 = aligned_rows || (std::is_same<T, float>::value && MODE != kMask);
   int path = g_path;
   // measured on MI355X: registers win up to 2048 for 128-bit rows, up to 1024 for rows accessed
   // one element at a time; one streaming wavefront per row up to 8192; one block per row beyond
   const int max_wave_c = v4 ? kMaxWaveC : kMaxWaveC1;
+  if (path == 0 && !aligned_rows && C <= 128) path = 6;   // short unaligned rows: 32-bit segments
   if (path == 0) path = C <= max_wave_c ? 6 : (C <= kMaxStreamC ? 4 : 2);
   if ((path == 1 || path == 6) && C > max_wave_c) path = 4;
-  if (path == 6 && dispatch_seg<T, MODE>(z, y, N, C, v4, o, s)) return launch_status();
+  if (path == 6 && dispatch_seg<T, MODE>(z, y, N, C, aligned_rows, o, s)) return launch_status();
   if (path == 1 || path == 6) {
     dispatch_wave<T, MODE>(z, y, N, C, v4, o, s);
   } else if (path == 4 || path == 5) {
