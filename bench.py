@@ -196,7 +196,11 @@ def main():
         two_op_ms = (time.perf_counter() - t1) * 1e3 / args.steps
 
     # the kernel the automatic dispatch runs for this row length (16-byte aligned rows)
-    tag = "fwl_wave_rows" if C <= 2048 else ("fwl_wave_stream_rows" if C <= 8192 else "fwl_block_rows")
+    unit = 16 // ELEM_BYTES[args.dtype]
+    if C % unit == 0 and C // unit <= 64:
+        tag = "fwl_seg_rows"
+    else:
+        tag = "fwl_wave_rows" if C <= 2048 else ("fwl_wave_stream_rows" if C <= 8192 else "fwl_block_rows")
     traffic = traffic_for(tag, args.config if args.dtype == "f32" else f"{args.config}_{args.dtype}")
     result = {
         "metric": METRIC,

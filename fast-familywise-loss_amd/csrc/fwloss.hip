@@ -491,11 +491,24 @@ __device__ __forceinline__ void load_row(rsrc_t row, int lane, float* x) {
 template <typename T, int NV, bool VEC>
 __device__ __forceinline__ void mask_tail(float* x, int C, int lane) {
   constexpr int U = kUnit<T, VEC>;
+  if (C % U == 0) {
+    // whole units: one test per unit
+    const int units = C / U;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    if (kWave * (k + 1) * U > C) {
+    for (int k = 0; k < NV; ++k) {
+      if (kWave * (k + 1) > units) {
+        const bool ok = lane + kWave * k < units;
 #pragma unroll
-      for (int e = 0; e < U; ++e) x[U * k + e] = U * (lane + kWave * k) + e < C ? x[U * k + e] : -INFINITY;
+        for (int e = 0; e < U; ++e) x[U * k + e] = ok ? x[U * k + e] : -INFINITY;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      if (kWave * (k + 1) * U > C) {
+#pragma unroll
+        for (int e = 0; e < U; ++e) x[U * k + e] = U * (lane + kWave * k) + e < C ? x[U * k + e] : -INFINITY;
+      }
     }
   }
 }
