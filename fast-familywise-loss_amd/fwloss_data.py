@@ -54,6 +54,55 @@ def make(cfg, N=None, seed=0):
     return np.ascontiguousarray(z, dtype=np.float32), y
 
 
+FAMILIES = ("gauss", "ties", "constant", "sorted", "two_level", "outlier", "flat", "heavy", "neginf")
+
+
+def families(K, rows=4, seed=0):
+    """Rows of every family for row length K: (z float32 [len(FAMILIES) * rows, K], y int64, names).
+
+    The families are those the reference's CPU test description names (ties, constant, sorted,
+    two-level, outlier; src/cpu/README.md:87), plus flat rows (long supports), heavy tails and
+    rows with -inf entries.
+    """
+    rng = np.random.default_rng(seed)
+    out, names = [], []
+    for fam in FAMILIES:
+        for _ in range(rows):
+            if fam == "gauss":
+                r = rng.standard_normal(K)
+            elif fam == "ties":
+                r = 0.5 * rng.integers(-3, 4, K)
+            elif fam == "constant":
+                r = np.full(K, rng.standard_normal())
+            elif fam == "sorted":
+                r = np.sort(rng.standard_normal(K))
+            elif fam == "two_level":
+                a, gap = rng.standard_normal(), rng.uniform(0.0, 2.0)
+                p = int(rng.integers(1, K + 1))
+                r = np.r_[np.full(p, a), np.full(K - p, a - gap)]
+                rng.shuffle(r)
+            elif fam == "outlier":
+                r = rng.standard_normal(K)
+                r[rng.integers(0, K)] += 10.0
+            elif fam == "flat":
+                r = 1e-3 * rng.standard_normal(K)
+            elif fam == "heavy":
+                r = np.clip(rng.standard_cauchy(K), -1e6, 1e6)
+            else:
+                r = rng.standard_normal(K)
+                r[rng.random(K) < 0.3] = -np.inf
+                r[rng.integers(0, K)] = rng.standard_normal()
+            out.append(r)
+            names.append(fam)
+    z = np.ascontiguousarray(np.stack(out).astype(np.float32))
+    y = rng.integers(0, K, size=z.shape[0], dtype=np.int64)
+    # keep labels off -inf entries, so every loss is finite
+    for i in range(z.shape[0]):
+        if not np.isfinite(z[i, y[i]]):
+            y[i] = int(np.flatnonzero(np.isfinite(z[i]))[0])
+    return z, y, names
+
+
 def edge_rows():
     """Hand-made rows exercising the special cases of the definition: (z [R, C], y [R]) per C."""
     C = 16

@@ -71,6 +71,17 @@ def test_dtype_forced_paths(ext, dev, reset_params16, name, path, cap):
 
 
 @pytest.mark.parametrize("name", sorted(DTYPES))
+@pytest.mark.parametrize("K", [3, 100, 1000, 40000])
+def test_dtype_row_families(ext, dev, name, K):
+    # every row family, rounded to the 16-bit dtype (which adds many exact ties)
+    import fwloss_data as data
+    z, y, _ = data.families(K, rows=3, seed=K + 7)
+    z16 = torch.from_numpy(z).to(DTYPES[name])
+    print(f"{name} families K={K}", flush=True)
+    check(ext, dev, z16, y)
+
+
+@pytest.mark.parametrize("name", sorted(DTYPES))
 def test_dtype_subnormal_gradients(ext, dev, name):
     # scale 1e-6: scale/kappa is subnormal in float16 and tests the rounding there
     z16, y = case(512, 64, 3, DTYPES[name])

@@ -187,6 +187,25 @@ def test_short_rows_groups(ext, dev, N, C):
     np.testing.assert_array_equal(sel.cpu().numpy(), z > ref["tau"][:, None])
 
 
+@pytest.mark.parametrize("K", [1, 2, 3, 7, 10, 100, 257, 1000, 4097, 40000])
+def test_row_families(ext, dev, K):
+    """Every row family (ties, constant, sorted, two-level, outlier, flat, heavy tails, -inf) at K
+    from 1 to 40000: bit-exact against the oracle, and within the reference harness's tolerances
+    against its fp64 sort recipe (CE_FW_perf.py:137-177)."""
+    from test_oracle import fp64_sort_recipe
+    z, y, _ = data.families(K, rows=4, seed=K + 1)
+    print(f"families K={K} rows={z.shape[0]}", flush=True)
+    ref = oracle.definition(z, y)
+    out = fused(ext, *to_dev(dev, z, y))
+    assert_parity(out, ref, z)
+    H, kappa, grad, loss = fp64_sort_recipe(z, y, 1.0 / z.shape[0])
+    ok = (ref["flags"] & 1) == 0
+    np.testing.assert_array_equal(out["kappa"][ok], kappa[ok])
+    np.testing.assert_allclose(out["H"], H, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(out["loss"], loss, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(out["grad"][ok], grad[ok], rtol=1e-5, atol=1e-6)
+
+
 def test_edge_rows(ext, dev):
     z, y = data.edge_rows()
     print("edge rows", flush=True)

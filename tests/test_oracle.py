@@ -179,3 +179,37 @@ def test_oracle_matches_compiled_reference():
         np.testing.assert_array_equal(out["kappa"], k.numpy())
         np.testing.assert_allclose(out["loss64"], L.numpy(), rtol=1e-12, atol=1e-12)
         np.testing.assert_array_equal(out["grad"], G.numpy())
+
+
+def fp64_sort_recipe(z, y, scale):
+    """The reference GPU harness's check recipe (benchmarks/cuda_benchmarks/CE_FW_perf.py:137-168),
+    restated with torch fp64 CPU ops: sort descending, prefix sums, H_k = (S_k - 1)/k, H = max_k,
+    kappa = first argmax + 1, grad = [z > H]/kappa - [j = y], times scale."""
+    import torch
+    z64 = torch.from_numpy(z).double()
+    srt = torch.sort(z64, dim=1, descending=True).values
+    S = srt.cumsum(dim=1)
+    k = torch.arange(1, z.shape[1] + 1, dtype=torch.float64)
+    H, idx = ((S - 1.0) / k).max(dim=1)
+    kappa = idx + 1
+    grad = (z64 > H[:, None]).double() / kappa[:, None].double()
+    grad[torch.arange(z.shape[0]), torch.from_numpy(y)] -= 1.0
+    loss = 1.0 - z64[torch.arange(z.shape[0]), torch.from_numpy(y)] + H
+    return H.numpy(), kappa.numpy(), (grad * scale).numpy(), loss.numpy()
+
+
+@pytest.mark.parametrize("K", [1, 2, 3, 7, 10, 100, 1000, 40000])
+def test_oracle_matches_fp64_sort_recipe(K):
+    """The oracle against the reference harness's own fp64 recipe on every row family, with the
+    harness's tolerances (CE_FW_perf.py:170-177: kappa equal, the rest rtol 1e-5 / atol 1e-6).
+    Rows where the fp64 argmax and the strict support count part ways (flag bit 1; only possible
+    through fp64 rounding at an exact tie) are excluded from the kappa comparison."""
+    z, y, _ = data.families(K, rows=3, seed=K)
+    scale = 1.0 / z.shape[0]
+    out = oracle.definition(z, y, scale=scale)
+    H, kappa, grad, loss = fp64_sort_recipe(z, y, scale)
+    ok = (out["flags"] & 1) == 0
+    np.testing.assert_array_equal(out["kappa"][ok], kappa[ok])
+    np.testing.assert_allclose(out["H"], H, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(out["loss64"], loss, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(out["grad"][ok], grad[ok], rtol=1e-5, atol=1e-6)
