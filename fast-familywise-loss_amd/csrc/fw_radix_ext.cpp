@@ -248,7 +248,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("logits"), py::arg("targets"), py::arg("scale") = -1.0, py::arg("reduce_div") = -1.0);
   m.def("fw_scale_grad", &fw_scale_grad, "In-place grad *= grad_output (device-side skip when 1)");
   m.def("set_params", &set_params, "Dispatch switches: path (0 auto, 1 wave registers, 2 block stream, 3 block generic, "
-        "4 wave stream, 5 wave generic, 6 short-row segments), cand_cap",
+        "4 wave stream, 5 wave generic, 6 short-row segments, 7 split rows), cand_cap",
         py::arg("path"), py::arg("cand_cap") = 512);
   m.def("get_params", &get_params);
 }

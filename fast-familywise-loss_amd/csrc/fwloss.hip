@@ -1364,17 +1364,18 @@ __device__ __forceinline__ bool scan_round(Round<T, VEC>& a, int round, int C, i
 
 // Stream this wavefront's share of row r once: loads run one round ahead of the candidate scan,
 // and every output element gets its zero placeholder.  Returns false if the list overflowed.
+// (`out_row`: the row's dense output -- gradient or mask -- or null in candidate-list mode; a
+// stretch of a row streams the same way, with `row`, `out_row` and C narrowed to it)
 template <int W, typename T, int MODE, bool VEC>
-__device__ bool stream_row(const void* __restrict__ row, int64_t r, int C, int lane, int wid, float* bv,
-                           int* bi, const Outs& o, int& n, float& m, float& t) {
+__device__ __forceinline__ bool stream_span(const void* __restrict__ row, void* out_row, int C, int lane, int wid, float* bv,
+                            int* bi, int cap, int& n, float& m, float& t) {
   constexpr int per_round = kWave * W * Round<T, VEC>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
   const rsrc_t in = make_rsrc(row, row_bytes);
   rsrc_t out = make_rsrc(nullptr, 0u);
-  if constexpr (MODE == kGrad) out = make_rsrc(static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>, row_bytes);
-  else if constexpr (MODE == kMask) out = make_rsrc(o.mask + r * (int64_t)C, (uint32_t)C);
-  const int cap = o.cap;
+  if constexpr (MODE == kGrad) out = make_rsrc(out_row, row_bytes);
+  else if constexpr (MODE == kMask) out = make_rsrc(out_row, (uint32_t)C);
   Round<T, VEC> a, b;
   load_round<W, T, VEC>(in, 0, wid, lane, a);
   // stores to a zero-size resource (no traffic) so that the wait counts on entry match those of
@@ -1396,7 +1397,104 @@ __device__ bool stream_row(const void* __restrict__ row, int64_t r, int C, int l
   return true;
 }
 
+template <int W, typename T, int MODE, bool VEC>
+__device__ bool stream_row(const void* __restrict__ row, int64_t r, int C, int lane, int wid, float* bv,
+                           int* bi, const Outs& o, int& n, float& m, float& t) {
+  void* out_row = nullptr;
+  if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
+  else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
+  return stream_span<W, T, MODE, VEC>(row, out_row, C, lane, wid, bv, bi, o.cap, n, m, t);
+}
+
 // block-wide fp64 sum and count of the row entries > thr (fixed order)
+// The wavefronts' candidate lists of a row (or of a stretch of one) in `sh` hold every entry above
+// each wavefront's final bound; cut them at the block maximum and resolve tau and kappa into
+// sh.tau / sh.kappa (valid after the caller's next barrier).
+__device__ __forceinline__ void block_merge_resolve(BlockShared& sh, int n, int wid, int lane) {
+  const float* bv = sh.bval[wid];
+  const float M = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
+  const float tb = bound_below_max(M);
+  int nb = 0;
+  for (int p0 = 0; p0 < n; p0 += kWave) {
+    const int p = p0 + lane;
+    nb += __popcll(ballot(p < n && bv[p] > tb));
+  }
+  if (lane == 0) sh.wsel[wid] = nb;
+  __syncthreads();
+  const int ntot = (sh.wsel[0] + sh.wsel[1]) + (sh.wsel[2] + sh.wsel[3]);
+  if (ntot > 0 && ntot <= kWave) {
+    int off = 0;
+    for (int w = 0; w < wid; ++w) off += sh.wsel[w];
+    for (int p0 = 0; p0 < n; p0 += kWave) {
+      const int p = p0 + lane;
+      const float v = p < n ? bv[p] : -INFINITY;
+      const bool k = v > tb;
+      const uint64_t b = ballot(k);
+      if (k) sh.sel[off + rank_in(b)] = v;
+      off += __popcll(b);
+    }
+    __syncthreads();
+    if (wid == 0) {
+      const float c = lane < ntot ? sh.sel[lane] : -INFINITY;
+      const double tt = clamp_below_max(select_small(c, ntot, lane), M);
+      const int kk = __popcll(ballot(lane < ntot && c > rd32(tt)));
+      if (lane == 0) {
+        sh.tau = tt;
+        sh.kappa = kk;
+      }
+    }
+  } else if (ntot > kWave) {
+    if (wid == 0) {
+      // fixed-point iterations over the four lists (wavefront 0)
+      auto all_sum_count = [&](float thr, double& s, int& c) {
+        double st = 0.0;
+        int ct = 0;
+        for (int w = 0; w < kWavesPerBlock; ++w) {
+          double sw;
+          int cw;
+          list_sum_count(sh.bval[w], sh.wn[w], thr, lane, sw, cw);
+          st += sw;
+          ct += cw;
+        }
+        s = st;
+        c = ct;
+      };
+      double tt = (double)tb, s;
+      int c;
+      all_sum_count(tb, s, c);
+      double res_t = NAN;
+      int res_k = 0;
+      for (int it = 0; it <= ntot + 1; ++it) {
+        const double tn = (s - 1.0) / (double)c;
+        double s2;
+        int c2;
+        all_sum_count(rd32(tn), s2, c2);
+        if (c2 == c || !(tn > tt)) {
+          res_t = tn;
+          res_k = c2;
+          break;
+        }
+        tt = tn;
+        s = s2;
+        c = c2;
+      }
+      const double tc = clamp_below_max(res_t, M);
+      if (tc != res_t) {
+        double s3;
+        res_t = tc;
+        all_sum_count(rd32(res_t), s3, res_k);
+      }
+      if (lane == 0) {
+        sh.tau = res_t;
+        sh.kappa = res_k;
+      }
+    }
+  } else if (threadIdx.x == 0) {
+    sh.tau = NAN;
+    sh.kappa = 0;
+  }
+}
+
 template <typename T>
 __device__ void block_sum_count(const void* __restrict__ row, int C, float thr, BlockShared& sh,
                                 int lane, int wid, double& s, int& c) {
@@ -1530,87 +1628,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
     double tau = NAN;
     int kappa = 0;
     if (!overflow) {
-      const float M = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
-      const float tb = bound_below_max(M);
-      int nb = 0;
-      for (int p0 = 0; p0 < n; p0 += kWave) {
-        const int p = p0 + lane;
-        nb += __popcll(ballot(p < n && bv[p] > tb));
-      }
-      if (lane == 0) sh.wsel[wid] = nb;
-      __syncthreads();
-      const int ntot = (sh.wsel[0] + sh.wsel[1]) + (sh.wsel[2] + sh.wsel[3]);
-      if (ntot > 0 && ntot <= kWave) {
-        int off = 0;
-        for (int w = 0; w < wid; ++w) off += sh.wsel[w];
-        for (int p0 = 0; p0 < n; p0 += kWave) {
-          const int p = p0 + lane;
-          const float v = p < n ? bv[p] : -INFINITY;
-          const bool k = v > tb;
-          const uint64_t b = ballot(k);
-          if (k) sh.sel[off + rank_in(b)] = v;
-          off += __popcll(b);
-        }
-        __syncthreads();
-        if (wid == 0) {
-          const float c = lane < ntot ? sh.sel[lane] : -INFINITY;
-          const double tt = clamp_below_max(select_small(c, ntot, lane), M);
-          const int kk = __popcll(ballot(lane < ntot && c > rd32(tt)));
-          if (lane == 0) {
-            sh.tau = tt;
-            sh.kappa = kk;
-          }
-        }
-      } else if (ntot > kWave) {
-        if (wid == 0) {
-          // fixed-point iterations over the four lists (wavefront 0)
-          auto all_sum_count = [&](float thr, double& s, int& c) {
-            double st = 0.0;
-            int ct = 0;
-            for (int w = 0; w < kWavesPerBlock; ++w) {
-              double sw;
-              int cw;
-              list_sum_count(sh.bval[w], sh.wn[w], thr, lane, sw, cw);
-              st += sw;
-              ct += cw;
-            }
-            s = st;
-            c = ct;
-          };
-          double tt = (double)tb, s;
-          int c;
-          all_sum_count(tb, s, c);
-          double res_t = NAN;
-          int res_k = 0;
-          for (int it = 0; it <= C + 1; ++it) {
-            const double tn = (s - 1.0) / (double)c;
-            double s2;
-            int c2;
-            all_sum_count(rd32(tn), s2, c2);
-            if (c2 == c || !(tn > tt)) {
-              res_t = tn;
-              res_k = c2;
-              break;
-            }
-            tt = tn;
-            s = s2;
-            c = c2;
-          }
-          const double tc = clamp_below_max(res_t, M);
-          if (tc != res_t) {
-            double s3;
-            res_t = tc;
-            all_sum_count(rd32(res_t), s3, res_k);
-          }
-          if (lane == 0) {
-            sh.tau = res_t;
-            sh.kappa = res_k;
-          }
-        }
-      } else if (threadIdx.x == 0) {
-        sh.tau = NAN;
-        sh.kappa = 0;
-      }
+      block_merge_resolve(sh, n, wid, lane);
       __syncthreads();
       tau = sh.tau;
       kappa = sh.kappa;
@@ -1861,6 +1879,271 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
   __syncthreads();
   const double bsum = (s_wsum[0] + s_wsum[1]) + (s_wsum[2] + s_wsum[3]);
   mean_epilogue(bsum, o);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Split rows: few rows, each very long.  fwl_split_chunks runs one block per (row, chunk): it
+// streams the chunk (zero placeholders, candidate lists), resolves the chunk's own threshold
+// tau_c and keeps the chunk's own support, {z > tau_c} -- tau_c = H(top kappa_c of the chunk) <=
+// tau, so the row's support lies in the union of the chunk supports.  fwl_split_finish runs one
+// block per row on that union: every entry above max_c tau_c, resolved like a candidate list.
+// A chunk whose support exceeds kSplitCap entries (or whose lists overflow) marks its row for the
+// generic solve, which the finishing kernel runs on the row in memory.
+
+constexpr int kSplitCap = 64;           // support entries kept per chunk
+// measured on MI355X (fp32, 1..256 rows of 16384..128256): splitting wins up to 128 rows of at
+// least ~96 KiB (1.3-2.9x at 1..64 rows of 128256); one block per row wins beyond
+constexpr int kSplitMaxRows = 128;      // rows up to which long rows are split
+constexpr int64_t kSplitMinBytes = 96 * 1024;   // shortest row (in bytes) that is split
+constexpr int kSplitTargetItems = 1024; // (row, chunk) items to aim for
+constexpr int kSplitMinChunk = 4096;    // elements: one streaming round of a block (fp32)
+constexpr int kSplitMaxChunks = 256;
+constexpr int kSplitListCap = 2048;     // entries of a row's list in the finishing kernel
+
+struct SplitScratch {
+  int* count;     // [N * nch]: support size of the chunk, -1 = the row needs the generic solve
+  double* tau;    // [N * nch]: tau_c
+  float* val;     // [N * nch * kSplitCap]
+  int* idx;       // [N * nch * kSplitCap] (index within the row)
+};
+
+template <typename T, int MODE, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_split_chunks(const void* __restrict__ z, int64_t N, int C, int CH,
+                                                           int nch, Outs o, SplitScratch sc) {
+  __shared__ BlockShared sh;
+  __shared__ int s_base[kWavesPerBlock];
+  const int lane = lane_id();
+  const int wid = uniform((int)(threadIdx.x >> 6));
+  const int64_t items = N * (int64_t)nch;
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const int64_t r = it / nch;
+    const int c = (int)(it - r * nch);
+    const int c0 = c * CH;
+    const int len = C - c0 < CH ? C - c0 : CH;
+    const void* span = static_cast<const char*>(z) + (r * (int64_t)C + c0) * kElemBytes<T>;
+    void* out_span = nullptr;
+    if constexpr (MODE == kGrad) out_span = static_cast<char*>(o.grad) + (r * (int64_t)C + c0) * kElemBytes<T>;
+    else if constexpr (MODE == kMask) out_span = o.mask + r * (int64_t)C + c0;
+    float* bv = sh.bval[wid];
+    int* bi = sh.bidx[wid];
+    int n = 0;
+    float m = -INFINITY, t = -INFINITY;
+    const bool ok = !o.force_generic &&
+                    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, n, m, t);
+    if (lane == 0) {
+      sh.wmax[wid] = m;
+      sh.wn[wid] = n;
+      sh.ovf[wid] = !ok;
+    }
+    __syncthreads();
+    const bool overflow = sh.ovf[0] | sh.ovf[1] | sh.ovf[2] | sh.ovf[3];
+    if (!overflow) {
+      block_merge_resolve(sh, n, wid, lane);
+      __syncthreads();
+    }
+    // the chunk's support, {list entries > rd32(tau_c)}, or -1: the row needs the generic solve
+    // (lists overflowed; a support too large to keep; a +inf maximum, whose row has no finite tau)
+    const float Mc = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
+    int status = -1;
+    if (!overflow) {
+      if (sh.kappa == 0) {
+        status = Mc == -INFINITY ? 0 : -1;   // 0: no finite entry in the chunk
+      } else if (isfinite(sh.tau)) {
+        const float Hc = rd32(sh.tau);
+        int cnt = 0;
+        for (int p0 = 0; p0 < n; p0 += kWave) cnt += __popcll(ballot(p0 + lane < n && bv[p0 + lane] > Hc));
+        if (lane == 0) s_base[wid] = cnt;
+        __syncthreads();
+        const int total = (s_base[0] + s_base[1]) + (s_base[2] + s_base[3]);
+        if (total <= kSplitCap) {
+          status = total;
+          int off = 0;
+          for (int w = 0; w < wid; ++w) off += s_base[w];
+          const int64_t slot = it * kSplitCap;
+          for (int p0 = 0; p0 < n; p0 += kWave) {
+            const int p = p0 + lane;
+            const bool sel = p < n && bv[p] > Hc;
+            const uint64_t b = ballot(sel);
+            if (sel) {
+              sc.val[slot + off + rank_in(b)] = bv[p];
+              sc.idx[slot + off + rank_in(b)] = c0 + bi[p];
+            }
+            off += __popcll(b);
+          }
+        }
+      }
+    }
+    if (threadIdx.x == 0) {
+      sc.count[it] = status;
+      sc.tau[it] = status > 0 ? sh.tau : -INFINITY;
+    }
+    __syncthreads();
+  }
+}
+
+// One block per row.  Thread t reads chunk t's bound and support; the entries above the largest
+// chunk bound form the row's list in LDS (chunk order), which wavefront 0 resolves.
+template <typename T, int MODE, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_split_finish(const void* __restrict__ z, const int64_t* __restrict__ tgt,
+                                                           int64_t N, int C, int nch, Outs o, SplitScratch sc) {
+  static_assert(kSplitMaxChunks <= kBlock, "one thread per chunk");
+  static_assert(kSplitListCap <= kWavesPerBlock * kCapMax, "the row's list lives in the block's candidate lists");
+  constexpr int B = 8;   // support entries loaded per batch
+  __shared__ BlockShared sh;
+  __shared__ double s_lo[kWavesPerBlock];
+  __shared__ int s_w[kWavesPerBlock];
+  const int lane = lane_id();
+  const int wid = uniform((int)(threadIdx.x >> 6));
+  const int t = (int)threadIdx.x;
+  float* cl = &sh.bval[0][0];
+  int* cx = &sh.bidx[0][0];
+  double lsum = 0.0;
+  for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
+    const void* row = static_cast<const char*>(z) + r * (int64_t)C * kElemBytes<T>;
+    const int64_t y64 = tgt[r];
+    // the chunks' lower bounds, and whether any chunk gave up
+    const int64_t item = r * nch + t;
+    const int cnt = t < nch ? sc.count[item] : 0;
+    const double tc = t < nch ? sc.tau[item] : -INFINITY;
+    const bool yok = y64 >= 0 && y64 < C;
+    const int yr = yok ? (int)y64 : -1;
+    const float zy = t == 0 && yok ? load_elem<T>(row, yr) : NAN;   // used by thread 0
+    const double wlo = wave_max_f64(tc);
+    const int wbad = ballot(cnt < 0) != 0;
+    if (lane == 0) {
+      s_lo[wid] = wlo;
+      s_w[wid] = wbad;
+    }
+    __syncthreads();
+    const double lo = fmax(fmax(s_lo[0], s_lo[1]), fmax(s_lo[2], s_lo[3]));
+    bool generic = ((s_w[0] | s_w[1]) | (s_w[2] | s_w[3])) != 0 || o.force_generic;
+    __syncthreads();
+    // chunk t's entries above lo: count them, then write them at their place in the row's list
+    // (the first B entries stay in registers; longer chunk supports are read again)
+    const float lof = rd32(lo);
+    const int64_t slot = item * kSplitCap;
+    int mine = 0;
+    float v0[B];
+    int id0[B];
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+      const bool in = !generic && k < cnt;
+      v0[k] = in ? sc.val[slot + k] : -INFINITY;
+      id0[k] = in ? sc.idx[slot + k] : 0;
+      mine += v0[k] > lof;
+    }
+    if (!generic) {
+      for (int e0 = B; e0 < cnt; e0 += B) {
+        float v[B];
+#pragma unroll
+        for (int k = 0; k < B; ++k) v[k] = e0 + k < cnt ? sc.val[slot + e0 + k] : -INFINITY;
+#pragma unroll
+        for (int k = 0; k < B; ++k) mine += v[k] > lof;
+      }
+    }
+    int wtot;
+    int off = wave_excl_scan_i32(mine, wtot);
+    if (lane == 0) s_w[wid] = wtot;
+    __syncthreads();
+    for (int w = 0; w < wid; ++w) off += s_w[w];
+    const int n = (s_w[0] + s_w[1]) + (s_w[2] + s_w[3]);
+    generic = generic || n > kSplitListCap;
+    if (!generic && mine > 0) {
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        if (v0[k] > lof) {
+          cl[off] = v0[k];
+          cx[off] = id0[k];
+          ++off;
+        }
+      }
+      for (int e0 = B; e0 < cnt; e0 += B) {
+        float v[B];
+        int id[B];
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+          const bool in = e0 + k < cnt;
+          v[k] = in ? sc.val[slot + e0 + k] : -INFINITY;
+          id[k] = in ? sc.idx[slot + e0 + k] : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+          if (v[k] > lof) {
+            cl[off] = v[k];
+            cx[off] = id[k];
+            ++off;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    double tau;
+    int kappa;
+    if (!generic) {
+      if (wid == 0) {
+        float lm = -INFINITY;
+        for (int p = lane; p < n; p += kWave) lm = fmaxf(lm, cl[p]);
+        double tt;
+        int kk;
+        uint64_t sup;
+        resolve_list(cl, n, lof, wave_max_f32(lm), lane, tt, kk, sup);
+        if (lane == 0) {
+          sh.tau = tt;
+          sh.kappa = kk;
+        }
+      }
+      __syncthreads();
+      tau = sh.tau;
+      kappa = sh.kappa;
+      const float Hf = rd32(tau);
+      const float inv = (float)(o.scale / (double)kappa);
+      // the support (every other output element holds the zero placeholder already)
+      if constexpr (MODE == kGrad || MODE == kMask) {
+        for (int p = t; p < n; p += kBlock) {
+          const int id = cx[p];
+          if (id == yr || !(cl[p] > Hf)) continue;
+          if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + id, inv);
+          else o.mask[r * (int64_t)C + id] = 1;
+        }
+      } else {
+        int base = 0;
+        for (int p0 = 0; p0 < n; p0 += kBlock) {
+          const int p = p0 + t;
+          const float v = p < n ? cl[p] : -INFINITY;
+          const bool sel = v > Hf;
+          const uint64_t b = ballot(sel);
+          if (lane == 0) sh.wsel[wid] = __popcll(b);
+          __syncthreads();
+          int q = base;
+          for (int w = 0; w < wid; ++w) q += sh.wsel[w];
+          if (sel) {
+            o.cval[r * (int64_t)C + q + rank_in(b)] = v;
+            o.cidx[r * (int64_t)C + q + rank_in(b)] = cx[p];
+          }
+          base += (sh.wsel[0] + sh.wsel[1]) + (sh.wsel[2] + sh.wsel[3]);
+          __syncthreads();
+        }
+      }
+    } else {
+      generic_row<T, MODE>(row, r, C, yr, lane, wid, sh, o, tau, kappa);
+    }
+    if (t == 0) {
+      const float Hf = rd32(tau);
+      const float inv = (float)(o.scale / (double)kappa);
+      if (yok) {
+        if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + yr, (zy > Hf ? inv : 0.0f) - o.scale_f);
+        else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
+      }
+      const float loss = (float)((1.0 - (double)zy) + tau);
+      if (o.H) o.H[r] = Hf;
+      if (o.loss) o.loss[r] = loss;
+      if (o.kappa) o.kappa[r] = kappa;
+      if constexpr (MODE == kCand) o.ccnt[r] = kappa;
+      lsum += (double)loss;
+    }
+    __syncthreads();
+  }
+  mean_epilogue(lsum, o);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -2185,6 +2468,67 @@ void launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const
   hipLaunchKernelGGL((fwl_wave_stream_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
 }
 
+// Split rows: chunks of whole streaming rounds (`round` elements; 16-byte aligned whenever the
+// row is), about kSplitTargetItems (row, chunk) items in all, at most kSplitMaxChunks per row.
+struct SplitPlan {
+  int nch;   // chunks per row
+  int CH;    // elements per chunk (the last one may be shorter)
+};
+
+// chunks per row before rounding the chunk length up to whole rounds: an upper bound of
+// split_plan(N, C, round).nch for every round >= kSplitMinChunk (sizes the workspace)
+int64_t split_chunks_bound(int64_t N, int64_t C, int64_t round) {
+  int64_t nch = (kSplitTargetItems + N - 1) / (N > 0 ? N : 1);
+  const int64_t by_c = (C + round - 1) / round;
+  if (nch > kSplitMaxChunks) nch = kSplitMaxChunks;
+  if (nch > by_c) nch = by_c;
+  return nch < 1 ? 1 : nch;
+}
+
+SplitPlan split_plan(int64_t N, int64_t C, int64_t round) {
+  const int64_t nch = split_chunks_bound(N, C, round);
+  int64_t CH = (C + nch - 1) / nch;
+  CH = (CH + round - 1) / round * round;
+  return {(int)((C + CH - 1) / CH), (int)CH};
+}
+
+// whether rows of this shape (elements of `elem` bytes) take the split kernels under dispatch
+// switch `path`; elem = 4 answers for every element type (the workspace size)
+bool split_rows(int64_t N, int64_t C, int64_t elem, int path) {
+  return N >= 1 && N <= kSplitMaxRows && C >= 1 && (path == 7 || (path == 0 && C * elem >= kSplitMinBytes));
+}
+
+// fp64 partial sums of the mean: one per block of the largest grid any forward launches for N rows
+int64_t partial_slots(int64_t N) {
+  const int64_t wave_max = (N + (int64_t)kWavesPerBlock * kRowsPerWave - 1) / ((int64_t)kWavesPerBlock * kRowsPerWave);
+  int64_t b = kMaxBlocksRow > kMaxBlocksWave ? kMaxBlocksRow : kMaxBlocksWave;
+  return wave_max > b ? wave_max : b;
+}
+
+size_t split_scratch_bytes(int64_t N, int64_t C) {
+  const int64_t items = N * split_chunks_bound(N, C, kSplitMinChunk);
+  return (size_t)items * (sizeof(double) + sizeof(int) + (size_t)kSplitCap * (sizeof(float) + sizeof(int)));
+}
+
+template <typename T, int MODE, bool V4>
+void launch_split(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, void* ws, hipStream_t s) {
+  constexpr int kRound = kWave * kWavesPerBlock * Round<T, V4>::kSlots;
+  static_assert(kRound >= kSplitMinChunk, "the workspace bound assumes rounds of >= kSplitMinChunk elements");
+  const SplitPlan pl = split_plan(N, C, kRound);
+  const int64_t items = N * split_chunks_bound(N, C, kSplitMinChunk);   // the workspace layout
+  char* base = static_cast<char*>(ws) + kWsHeader + sizeof(double) * (size_t)partial_slots(N);
+  SplitScratch sc;
+  sc.tau = reinterpret_cast<double*>(base);
+  sc.count = reinterpret_cast<int*>(base + sizeof(double) * items);
+  sc.val = reinterpret_cast<float*>(base + (sizeof(double) + sizeof(int)) * items);
+  sc.idx = reinterpret_cast<int*>(base + (sizeof(double) + sizeof(int) + sizeof(float) * kSplitCap) * items);
+  const void* ka = reinterpret_cast<const void*>(&fwl_split_chunks<T, MODE, V4>);
+  const int ga = persistent_grid(N * (int64_t)pl.nch, 1, resident_blocks(ka), kMaxBlocksRow);
+  hipLaunchKernelGGL((fwl_split_chunks<T, MODE, V4>), dim3(ga), dim3(kBlock), 0, s, z, N, C, pl.CH, pl.nch, o, sc);
+  const int gb = (int)N;   // N <= kSplitMaxRows
+  hipLaunchKernelGGL((fwl_split_finish<T, MODE, V4>), dim3(gb), dim3(kBlock), 0, s, z, y, N, C, pl.nch, o, sc);
+}
+
 // rows are addressed through buffer resources with 32-bit byte ranges and offsets (one round
 // past the row end included), hence the bound on C
 constexpr int64_t kMaxC = (int64_t)1 << 29;
@@ -2220,6 +2564,16 @@ int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scal
   // measured on MI355X: registers win up to 2048 for 128-bit rows, up to 1024 for rows accessed
   // one element at a time; one streaming wavefront per row up to 8192; one block per row beyond
   const int max_wave_c = v4 ? kMaxWaveC : kMaxWaveC1;
+  // few long rows: chunks of every row on their own blocks (needs the scratch of the workspace)
+  if (path == 0 && split_rows(N, C, kElemBytes<T>, 0)) path = 7;
+  if (path == 7) {
+    if (split_rows(N, C, kElemBytes<T>, 7) && ws != nullptr && ws_bytes >= fwl_workspace_bytes(N, C64) && aligned(ws, 8)) {
+      if (v4) launch_split<T, MODE, true>(z, y, N, C, o, ws, s);
+      else launch_split<T, MODE, false>(z, y, N, C, o, ws, s);
+      return launch_status();
+    }
+    path = 2;
+  }
   if (path == 0 && !aligned_rows && C <= 128) path = 6;   // short unaligned rows: 32-bit segments
   if (path == 0) path = C <= max_wave_c ? 6 : (C <= kMaxStreamC ? 4 : 2);
   if ((path == 1 || path == 6) && C > max_wave_c) path = 4;
@@ -2272,12 +2626,11 @@ const char* fwl_status_string(int status) {
 }
 
 size_t fwl_workspace_bytes(int64_t N, int64_t C) {
-  (void)C;
-  // one fp64 partial per block of the largest grid any forward launches for N rows
-  const int64_t wave_max = (N + (int64_t)kWavesPerBlock * kRowsPerWave - 1) / ((int64_t)kWavesPerBlock * kRowsPerWave);
-  int64_t b = kMaxBlocksRow > kMaxBlocksWave ? kMaxBlocksRow : kMaxBlocksWave;
-  if (wave_max > b) b = wave_max;
-  return kWsHeader + sizeof(double) * (size_t)b;
+  if (N < 0) N = 0;
+  // the completion counter, the fp64 partials of the mean, then the split rows' scratch
+  size_t b = kWsHeader + sizeof(double) * (size_t)partial_slots(N);
+  if (split_rows(N, C, 4, g_path)) b += split_scratch_bytes(N, C);
+  return b;
 }
 
 int fwl_forward_backward(const float* logits, const int64_t* targets, int64_t N, int64_t C,
@@ -2423,7 +2776,7 @@ int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_
 }
 
 int fwl_set_params(int path, int cand_cap) {
-  if (path < 0 || path > 6 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
+  if (path < 0 || path > 7 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
   g_path = path;
   g_cap = cand_cap;
   return FWL_OK;

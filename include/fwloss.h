@@ -22,8 +22,10 @@
  *   - all pointers are device pointers; logits and grad are row-major [N, C], contiguous;
  *   - every call is asynchronous on `stream` and allocates nothing;
  *   - `workspace` is caller-provided device memory of at least fwl_workspace_bytes(N, C) bytes,
- *     zero-filled before its first use; every call leaves it zero-filled again.  Calls that run
- *     concurrently (different streams) must not share one workspace;
+ *     8-byte aligned and zero-filled before its first use.  Its first 256 bytes hold a completion
+ *     counter that every call returns to zero; the rest is scratch (per-block partial sums, and
+ *     for few long rows the chunk thresholds and supports), written before it is read.  Calls
+ *     that run concurrently (different streams) must not share one workspace;
  *   - targets outside [0, C) do not fault: that row gets loss = NaN and no label term in grad;
  *   - NaN logits are never selected; rows without a finite maximum give kappa = 0, H = NaN;
  *   - the return value is FWL_OK or an fwl_status (argument errors are detected before launch).
@@ -59,7 +61,10 @@ enum fwl_dtype {
 /* Human-readable text of a status code (static storage). */
 const char* fwl_status_string(int status);
 
-/* Bytes of device workspace the forward entry points need for an [N, C] problem. */
+/* Bytes of device workspace the forward entry points need for an [N, C] problem: 256 bytes, one
+ * fp64 per block of the largest grid (>= 4096), and for at most 128 rows of >= 24576 elements
+ * 524 bytes per (row, chunk).  The answer follows the current fwl_set_params switches (forcing
+ * path 7 needs the chunk scratch for rows of any length). */
 size_t fwl_workspace_bytes(int64_t N, int64_t C);
 
 /* Fused forward + backward: the whole hot path in one launch, reading logits once and writing the
@@ -135,8 +140,8 @@ int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_
 /* Process-wide dispatch switches, the GPU counterpart of the reference CPU path's set_params
  * (src/cpu/fw_cpu.cpp:758-763, used by its tests to force each branch).  Not thread-safe; meant
  * for tests and tuning.
- *   path:      0 = automatic (6 for short rows, 1 for C <= 2048 or C <= 1024 when rows are not
- *              16-byte aligned, 4 for C <= 8192, else 2),
+ *   path:      0 = automatic (7 for at most 128 rows of at least 96 KiB, 6 for short rows, 1 for
+ *              C <= 2048 or C <= 1024 when rows are not 16-byte aligned, 4 for C <= 8192, else 2),
  *              1 = one wavefront per row with the row in registers (C <= 2048, or 1024 for rows
  *              that are not 16-byte aligned; larger C runs path 4),
  *              2 = one block per row, streamed, with LDS candidate lists,
@@ -144,7 +149,11 @@ int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_
  *              4 = one wavefront per row, streamed, with an LDS candidate list,
  *              5 = path 4 with the generic multi-pass solve forced,
  *              6 = short rows: 16- or 32-lane segments of a wavefront, 4 or 2 rows per
- *              iteration (rows of up to 64 units; longer rows and candidate lists run path 1).
+ *              iteration (rows of up to 64 units; longer rows and candidate lists run path 1),
+ *              7 = split rows: one block per (row, chunk of >= 4096 elements) streams the chunk
+ *              and keeps its own support, then one block per row resolves their union (at most
+ *              128 rows, and a workspace of fwl_workspace_bytes(N, C) taken with path 7 set;
+ *              otherwise path 2 runs).
  *   cand_cap:  LDS candidate capacity per wavefront of paths 2 and 4, in [64, 512] (512 =
  *              default); smaller values make rows overflow into the generic solve sooner.
  * Returns FWL_ERR_INVALID_ARG for values out of range. */

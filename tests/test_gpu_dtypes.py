@@ -71,6 +71,17 @@ def test_dtype_forced_paths(ext, dev, reset_params16, name, path, cap):
 
 
 @pytest.mark.parametrize("name", sorted(DTYPES))
+@pytest.mark.parametrize("N,C,path", [(40, 20000, 7), (16, 50000, 0), (3, 131072, 0), (16, 40000, 0)])
+def test_dtype_split_rows(ext, dev, reset_params16, name, N, C, path):
+    # few long rows: forced split, and the automatic rule (rows of >= 96 KiB: 49152 16-bit elements;
+    # 40000 elements run one block per row)
+    z16, y = case(C, N, C + N, DTYPES[name])
+    print(f"{name} split rows N={N} C={C} path={path}", flush=True)
+    ext.set_params(path, 512)
+    check(ext, dev, z16, y)
+
+
+@pytest.mark.parametrize("name", sorted(DTYPES))
 @pytest.mark.parametrize("K", [3, 100, 1000, 40000])
 def test_dtype_row_families(ext, dev, name, K):
     # every row family, rounded to the 16-bit dtype (which adds many exact ties)

@@ -155,6 +155,119 @@ def test_streamed_overflow_and_tighten(ext, dev, reset_params, path, cap):
     assert_parity(fused(ext, *to_dev(dev, z, y)), ref, z)
 
 
+# ---------------------------------------------------------------- split rows: few long rows
+
+def _split_case(N, C, seed):
+    rng = np.random.default_rng(seed)
+    z = (rng.standard_normal((N, C)) * rng.choice([0.05, 1.0, 4.0], size=(N, 1))).astype(np.float32)
+    z[::7] *= np.float32(0.01)                   # flat rows: long chunk supports (generic solve)
+    z[3::11] = np.round(z[3::11] * 2) / 2        # dyadic ties
+    z[5::13, -1] = z[5::13].max(axis=1) + 3      # the maximum in the last (possibly short) chunk
+    y = rng.integers(0, C, N)
+    return z, y
+
+
+@pytest.mark.parametrize("N,C", [(1, 1), (3, 10), (5, 1000), (16, 1024), (7, 2999), (128, 3000), (33, 20000),
+                                 (2, 70001), (128, 4097), (300, 3000)])
+def test_split_rows_forced(ext, dev, reset_params, N, C):
+    # path 7 at any length: one chunk, a short last chunk, up to 256 chunks per row (300 rows:
+    # beyond path 7's 128, so one block per row runs)
+    z, y = _split_case(N, C, N * 7 + C)
+    print(f"split forced N={N} C={C}", flush=True)
+    ext.set_params(7, 512)
+    assert_parity(fused(ext, *to_dev(dev, z, y)), oracle.definition(z, y), z)
+
+
+@pytest.mark.parametrize("N,C", [(1, 24575), (1, 24576), (16, 50000), (3, 131072), (128, 32000), (129, 24576)])
+def test_split_rows_auto(ext, dev, N, C):
+    # the automatic rule: rows of >= 96 KiB (24576 fp32 elements), at most 128 of them; the
+    # shapes just outside it (24575 elements, 129 rows) run one block per row
+    z, y = _split_case(N, C, N + C)
+    print(f"split auto N={N} C={C}", flush=True)
+    assert_parity(fused(ext, *to_dev(dev, z, y)), oracle.definition(z, y), z)
+
+
+def test_split_rows_union_sizes(ext, dev, reset_params):
+    # 40 chunks of 1024 per row, a plateau of near-equal values in every chunk: per chunk 20, 40 or
+    # 60 support entries (kept), or 70 (too many to keep: generic solve); the union of the kept
+    # entries has 800 (a long list for the finishing wavefront), 1600 or 2400 (generic) entries
+    rng = np.random.default_rng(3)
+    C = 40960
+    per = [20, 40, 60, 70, 20, 5]
+    z = np.full((len(per), C), -5.0, np.float32)
+    z += np.float32(1e-3) * rng.standard_normal(z.shape).astype(np.float32)
+    for r, k in enumerate(per):
+        for c in range(40):
+            pos = c * 1024 + rng.choice(1024, k, replace=False)
+            z[r, pos] = np.float32(1.0) + np.float32(1e-3) * rng.standard_normal(k).astype(np.float32)
+    z[4, 1024:2048] = -np.inf                    # a chunk with no finite entry
+    z[5, 3 * 1024:] = -np.inf                    # only 3 chunks with finite entries
+    y = rng.integers(0, C, len(per))
+    y[5] = C - 1                                 # label at -inf
+    ref = oracle.definition(z, y)
+    for path in (7, 0):
+        print(f"split union sizes path={path}", flush=True)
+        ext.set_params(path, 512)
+        assert_parity(fused(ext, *to_dev(dev, z, y)), ref, z)
+
+
+@pytest.mark.parametrize("C", [5000, 40000])
+def test_split_rows_drop_in_ops(ext, dev, reset_params, C):
+    # support mask and candidate-list outputs of the split kernels (forced at 5000, automatic at
+    # 40000)
+    z, y = _split_case(40, C, C + 1)
+    ext.set_params(7 if C < 24576 else 0, 512)
+    print(f"split drop-in ops C={C}", flush=True)
+    zt, yt = to_dev(dev, z, y)
+    ref = oracle.definition(z, y)
+    H, losses, mean, kappa, sel = ext.fw_forward_small(zt, yt)
+    grad = ext.fw_backward_small(yt, sel, kappa)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(sel.cpu().numpy(), z > ref["tau"][:, None])
+    assert_parity(dict(H=H.cpu().numpy(), loss=losses.cpu().numpy(), mean=float(mean.cpu()),
+                       kappa=kappa.cpu().numpy(), grad=grad.cpu().numpy()), ref, z)
+    H, losses, mean, kappa, cbuf, cidx, ccnt = ext.fw_forward(zt, yt)
+    grad = ext.fw_backward(zt, yt, H, kappa, cbuf, cidx, ccnt)
+    torch.cuda.synchronize()
+    cnt, cb, ci = ccnt.cpu().numpy(), cbuf.cpu().numpy(), cidx.cpu().numpy()
+    np.testing.assert_array_equal(cnt, ref["kappa"])
+    for r in range(z.shape[0]):
+        idx = ci[r, :cnt[r]]
+        assert np.array_equal(np.sort(idx), np.nonzero(z[r] > ref["tau"][r])[0]), f"row {r} support"
+        assert bits_equal(cb[r, :cnt[r]], z[r, idx])
+    assert_parity(dict(H=H.cpu().numpy(), loss=losses.cpu().numpy(), mean=float(mean.cpu()),
+                       kappa=kappa.cpu().numpy(), grad=grad.cpu().numpy()), ref, z)
+
+
+def test_split_rows_non_finite_like_block_rows(ext, dev, reset_params):
+    # rows with +inf, NaN or no finite entry: the split kernels give what one block per row gives
+    rng = np.random.default_rng(11)
+    C = 20000
+    z = rng.standard_normal((8, C)).astype(np.float32)
+    z[0, 17000] = np.inf
+    z[1, ::3] = np.nan
+    z[2, 1024:2048] = -np.inf
+    z[3] = -np.inf
+    z[4] = np.nan
+    z[5, :16384] = -np.inf
+    z[6, 5] = np.inf
+    z[6, 19999] = np.nan
+    y = np.array([17000, 1, 1500, 3, 4, 19999, 5, 0])
+    zt, yt = to_dev(dev, z, y)
+    outs = []
+    for path in (7, 2):
+        ext.set_params(path, 512)
+        print(f"non-finite rows path={path}", flush=True)
+        outs.append(fused(ext, zt, yt))
+    for k in ("H", "loss", "kappa", "grad"):
+        a, b = outs[0][k], outs[1][k]
+        assert (bits_equal(a, b) if a.dtype == np.float32 else np.array_equal(a, b)), k
+    # finite rows against the oracle
+    fin = [2, 5, 7]
+    assert_parity({k: outs[0][k][fin] for k in ("H", "loss", "kappa", "grad")}, oracle.definition(z[fin], y[fin],
+                  scale=1.0 / 8), z[fin])
+
+
 # ---------------------------------------------------------------- shapes, layouts, special values
 
 @pytest.mark.parametrize("C", [1, 2, 3, 5, 10, 37, 63, 64, 65, 255, 257, 999, 1001, 1023, 1025, 2049, 5000, 10001,

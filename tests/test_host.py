@@ -136,13 +136,47 @@ def test_set_params_validation_and_round_trip():
     assert L.fwl_get_params(ctypes.byref(p), ctypes.byref(c)) == 0
     saved = (p.value, c.value)
     try:
-        assert L.fwl_set_params(7, 512) == 1
+        assert L.fwl_set_params(8, 512) == 1
+        assert L.fwl_set_params(7, 512) == 0
         assert L.fwl_set_params(-1, 512) == 1
         assert L.fwl_set_params(2, 63) == 1
         assert L.fwl_set_params(2, 513) == 1
         assert L.fwl_set_params(2, 64) == 0
         L.fwl_get_params(ctypes.byref(p), ctypes.byref(c))
         assert (p.value, c.value) == (2, 64)
+    finally:
+        L.fwl_set_params(*saved)
+
+
+def test_workspace_sizes():
+    """The split-row scratch is counted exactly where the split kernels may run: few rows (<= 128)
+    of at least 96 KiB (24576 fp32 elements; the size covers every element type), or rows of any
+    length when path 7 is forced."""
+    L = capi.lib()
+    p, c = ctypes.c_int(-1), ctypes.c_int(-1)
+    L.fwl_get_params(ctypes.byref(p), ctypes.byref(c))
+    saved = (p.value, c.value)
+    try:
+        L.fwl_set_params(0, 512)
+        base = L.fwl_workspace_bytes(4096, 1000)
+        assert base >= 256 + 8 * 4096
+        assert L.fwl_workspace_bytes(16, 1000) == base           # short rows: no scratch
+        assert L.fwl_workspace_bytes(2048, 131072) == base       # many rows: no scratch
+        assert L.fwl_workspace_bytes(0, 131072) == base
+        assert L.fwl_workspace_bytes(129, 24576) == base
+        assert L.fwl_workspace_bytes(128, 24575) == base
+        # (row, chunk) items: about 1024 in all, chunks of at least 4096 elements, <= 256 per row;
+        # 8 + 4 + 64 * 8 bytes per item
+        item = 8 + 4 + 64 * 8
+        assert L.fwl_workspace_bytes(16, 131072) - base == 16 * 32 * item
+        assert L.fwl_workspace_bytes(3, 131072) - base == 3 * 32 * item
+        assert L.fwl_workspace_bytes(1, 2 ** 29) - base == 1 * 256 * item
+        assert L.fwl_workspace_bytes(128, 24576) - base == 128 * 6 * item
+        assert L.fwl_workspace_bytes(100, 40000) - base == 100 * 10 * item
+        L.fwl_set_params(7, 512)
+        assert L.fwl_workspace_bytes(16, 1000) - base == 16 * 1 * item
+        assert L.fwl_workspace_bytes(4, 30000) - base == 4 * 8 * item
+        assert L.fwl_workspace_bytes(129, 30000) == base          # more rows than path 7 takes
     finally:
         L.fwl_set_params(*saved)
 
@@ -161,7 +195,7 @@ def test_extension_rejects_cpu_and_bad_inputs():
     with pytest.raises(KeyError):   # what the reference's dict lookup raises (src/cpu/fwcpp.py:19)
         fwloss.familywise_loss(z, y, reduction="max")
     with pytest.raises(RuntimeError):
-        fwloss.set_params(7, 512)
+        fwloss.set_params(8, 512)
     assert tuple(fwloss.get_params()) == (0, 512)
     libs = fwloss.native_libraries()
     assert any(p.endswith("libfwloss.so") for p in libs) and any("fw_radix_cuda" in p for p in libs)
