@@ -355,25 +355,79 @@ __device__ __forceinline__ float bitonic_merge(float v, int lane) {
   return bitonic_step<K, 1>(v, lane);
 }
 
-// sort lanes [0, T) descending (T = 16, 32 or 64)
+// Order-preserving integer key of a float that is not NaN: signed comparison of keys orders the
+// values (-0.0 just below +0.0).  The map is its own inverse.  Integer max/min need no NaN
+// quieting, so a compare-exchange is a DPP max, a DPP min and one select.
+__device__ __forceinline__ int fkey(float v) {
+  const int b = __float_as_int(v);
+  return b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float fkey_inv(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7FFFFFFF)); }
+
+// partner of lane ^ M for integer values; lane ^ 4 takes two bank-masked DPP moves (banks 0 and 2
+// of each row, lanes with bit 2 clear, read lane + 4 = row_ror:12; banks 1 and 3 read lane - 4 =
+// row_ror:4)
+template <int M>
+__device__ __forceinline__ int xor_lane_i(int x, int lane) {
+  if constexpr (M == 1) return dpp_mov<kQuadXor1>(x);
+  else if constexpr (M == 2) return dpp_mov<kQuadXor2>(x);
+  else if constexpr (M == 4) {
+    const int a = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0x5, false);
+    return __builtin_amdgcn_update_dpp(a, x, 0x124, 0xF, 0xA, false);
+  } else if constexpr (M == 8) return dpp_mov<kRowRor8>(x);
+  else return __float_as_int(xor_lane<M>(__int_as_float(x), lane));
+}
+
+__device__ __forceinline__ int select_lanes_i(uint64_t mask, int if_set, int if_clear) {
+  int r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(if_clear), "v"(if_set), "s"(mask));
+  return r;
+}
+
+template <int K, int J>
+__device__ __forceinline__ int bitonic_step_i(int v, int lane) {
+  const int p = xor_lane_i<J>(v, lane);
+  return select_lanes_i(keep_max_mask(K, J), max(v, p), min(v, p));
+}
+
+template <int K>
+__device__ __forceinline__ int bitonic_merge_i(int v, int lane) {
+  if constexpr (K >= 64) v = bitonic_step_i<K, 32>(v, lane);
+  if constexpr (K >= 32) v = bitonic_step_i<K, 16>(v, lane);
+  if constexpr (K >= 16) v = bitonic_step_i<K, 8>(v, lane);
+  if constexpr (K >= 8) v = bitonic_step_i<K, 4>(v, lane);
+  if constexpr (K >= 4) v = bitonic_step_i<K, 2>(v, lane);
+  return bitonic_step_i<K, 1>(v, lane);
+}
+
+// sort the keys of lanes [0, T) descending (T = 16, 32 or 64)
 template <int T>
-__device__ __forceinline__ float sort_desc(float v, int lane) {
-  v = bitonic_merge<2>(v, lane);
-  v = bitonic_merge<4>(v, lane);
-  v = bitonic_merge<8>(v, lane);
-  v = bitonic_merge<16>(v, lane);
-  if constexpr (T >= 32) v = bitonic_merge<32>(v, lane);
-  if constexpr (T >= 64) v = bitonic_merge<64>(v, lane);
+__device__ __forceinline__ int sort_desc_i(int v, int lane) {
+  v = bitonic_merge_i<2>(v, lane);
+  v = bitonic_merge_i<4>(v, lane);
+  v = bitonic_merge_i<8>(v, lane);
+  v = bitonic_merge_i<16>(v, lane);
+  if constexpr (T >= 32) v = bitonic_merge_i<32>(v, lane);
+  if constexpr (T >= 64) v = bitonic_merge_i<64>(v, lane);
   return v;
+}
+
+// DPP move whose lanes without a source (shifted in past the row edge) read 0
+template <int CTRL>
+__device__ __forceinline__ double dpp_zero_f64(double v) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_mov_dpp((int)b, CTRL, 0xF, 0xF, true);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), CTRL, 0xF, 0xF, true);
+  return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
 }
 
 // inclusive prefix sum over lanes [0, T)
 template <int T>
 __device__ __forceinline__ double scan_f64(double v) {
-  v += dpp_or0_f64<0x111, 0xF>(v);          // row_shr:1
-  v += dpp_or0_f64<0x112, 0xF>(v);          // row_shr:2
-  v += dpp_or0_f64<0x114, 0xF>(v);          // row_shr:4
-  v += dpp_or0_f64<0x118, 0xF>(v);          // row_shr:8
+  v += dpp_zero_f64<0x111>(v);          // row_shr:1
+  v += dpp_zero_f64<0x112>(v);          // row_shr:2
+  v += dpp_zero_f64<0x114>(v);          // row_shr:4
+  v += dpp_zero_f64<0x118>(v);          // row_shr:8
   if constexpr (T >= 32) v += dpp_or0_f64<kRowBcast15, 0xA>(v);   // rows 1, 3 += last lane of 0, 2
   if constexpr (T >= 64) v += dpp_or0_f64<kRowBcast31, 0xC>(v);   // rows 2, 3 += lane 31
   return v;
@@ -420,15 +474,22 @@ __device__ __forceinline__ double clamp_below_max(double tau, float m) {
   return (tau >= (double)m && isfinite(m)) ? prev_f64((double)m) : tau;
 }
 
-// tau of a candidate set held one value per lane in lanes [0, n), 1 <= n <= T <= 64:
-// sort descending, S_k = fp64 prefix sums, tau = max_k (S_k - 1)/k (reference_impl.py:17-21)
+// tau of a candidate set held one value per lane in lanes [0, n), 1 <= n <= T <= 64: sort
+// descending, S_k = fp64 prefix sums; tau = max_k (S_k - 1)/k (reference_impl.py:17-21).  The
+// maximising k is the support size: k z_(k) > S_k - 1 holds exactly for k = 1 .. kappa (the
+// sparsemax support condition; both sides are exact in fp64 whenever S_k is), so one division
+// gives tau = (S_kappa - 1)/kappa.  Rounding is monotone, so this is the largest of the rounded
+// (S_k - 1)/k.
 template <int T>
 __device__ __forceinline__ double select_tier(float c, int n, int lane) {
-  float v = lane < n ? c + 0.0f : -INFINITY;   // + 0.0f: -0.0 -> +0.0 before min/max
-  v = sort_desc<T>(v, lane);
+  int key = fkey(lane < n ? c + 0.0f : -INFINITY);   // + 0.0f: -0.0 -> +0.0
+  key = sort_desc_i<T>(key, lane);
+  const float v = fkey_inv(key);
   const double S = scan_f64<T>(lane < n ? (double)v : 0.0);
-  const double f = (S - 1.0) / (double)(lane + 1);
-  return wave_max_f64(lane < n ? f : -INFINITY);
+  const uint64_t in = ballot(lane < n && (double)v * (double)(lane + 1) > S - 1.0);
+  int kap = 64 - (int)__builtin_clzll(in | 1ull);   // the highest k that satisfies it (>= 1)
+  kap = uniform(kap);
+  return (readlane_f64(S, kap - 1) - 1.0) / (double)kap;
 }
 
 __device__ __forceinline__ double select_small(float c, int n, int lane) {
@@ -486,32 +547,6 @@ __device__ __forceinline__ void load_row(rsrc_t row, int lane, float* x) {
   for (int k = 0; k < NV; ++k) load_unit<T, VEC>(row, (uint32_t)(lane + kWave * k), x + kUnit<T, VEC> * k);
 }
 
-// set the register slots past the row end to -inf (only the last, possibly partial, units need it;
-// fp32 rows of any length use 128-bit units, their last unit partly past the row)
-template <typename T, int NV, bool VEC>
-__device__ __forceinline__ void mask_tail(float* x, int C, int lane) {
-  constexpr int U = kUnit<T, VEC>;
-  if (C % U == 0) {
-    // whole units: one test per unit
-    const int units = C / U;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      if (kWave * (k + 1) > units) {
-        const bool ok = lane + kWave * k < units;
-#pragma unroll
-        for (int e = 0; e < U; ++e) x[U * k + e] = ok ? x[U * k + e] : -INFINITY;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      if (kWave * (k + 1) * U > C) {
-#pragma unroll
-        for (int e = 0; e < U; ++e) x[U * k + e] = U * (lane + kWave * k) + e < C ? x[U * k + e] : -INFINITY;
-      }
-    }
-  }
-}
 
 // element index of register slot i of this lane
 template <typename T, bool VEC>
@@ -607,24 +642,35 @@ struct RowResult {
   int kappa;
 };
 
-// The LDS candidate list of a wavefront holds up to a whole register row (E values per lane),
-// then one spare slot per lane: the target of the branch-free writes of non-candidates.  The
+// The LDS candidate list of a wavefront holds up to a whole register row (E values per lane); the
 // candidate-list mode keeps the element indices alongside.
 constexpr int kRowsPerWave = kWave;   // rows of one wavefront per launch (labels/results: one lane each)
 
+// Per-slot bias of a register row: -0.0 for slots inside the row, -inf past its end.  Slots past
+// the end load 0, and x + bias sets them to -inf; for every other value x + (-0.0) == x (signed
+// zeros included) except that a signaling NaN is quieted, so the result needs no further NaN
+// quieting before max/min.
+template <typename T, int NV, bool VEC>
+__device__ __forceinline__ void row_bias(int C, int lane, float* bias) {
+  constexpr int E = kUnit<T, VEC> * NV;
+#pragma unroll
+  for (int i = 0; i < E; ++i) bias[i] = slot_index<T, VEC>(i, lane) < C ? -0.0f : -INFINITY;
+}
+
 // One row: x holds it (E values per lane).  Once its candidates are in the LDS list, the loads of
-// the next row (resource `next`, zero-size if there is none) are issued into x, so they are in
-// flight during the selection and the stores of this row; no second row buffer is needed.
+// the next row (resource `next`, zero-size if there is none) are issued into xn, so they are in
+// flight during the selection and the stores of this row; x stays for the outputs.
 template <typename T, int MODE, int NV, bool V4>
 __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t y64, int C, int lane,
-                                                 float* x, float* cl, int* ci_lds, const Outs& o) {
+                                                 float* x, float* xn, const float* bias, float* cl, int* ci_lds,
+                                                 const Outs& o) {
   constexpr int U = kUnit<T, V4>;
   constexpr int E = U * NV;
-  static_assert(E <= 32, "one mask bit per register slot");
   static_assert(std::is_same<T, float>::value || MODE == kGrad, "16-bit logits: fused op only");
   const bool yok = y64 >= 0 && y64 < C;
   const int yr = yok ? (int)y64 : -1;
-  mask_tail<T, NV, V4>(x, C, lane);
+#pragma unroll
+  for (int i = 0; i < E; ++i) x[i] += bias[i];
 
   // row maximum and the first lower bound max - 1 (rounded down: every support entry passes)
   float lm = x[0];
@@ -633,53 +679,31 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
   const float m = wave_max_f32(lm);
   const float t0 = bound_below_max(m);
 
-  // candidates z > t0: one bit per register slot, then lane-major positions in the LDS list
-  unsigned cm = 0;
+  // candidates z > t0, slot-major: the candidates of slot i follow those of the slots before it,
+  // in lane order (slots without any candidate cost one compare)
+  int n = 0;
 #pragma unroll
-  for (int i = 0; i < E; ++i) cm |= (unsigned)(x[i] > t0) << i;
-  int n;
-  const int base = wave_excl_scan_i32(__popc(cm), n);
-  {
-    int pos = base;
-#pragma unroll
-    for (int i = 0; i < E; ++i) {
-      const int bit = (cm >> i) & 1;
-      const int at = bit ? pos : E * kWave + lane;
-      cl[at] = x[i];
-      if constexpr (MODE == kCand) ci_lds[at] = slot_index<T, V4>(i, lane);
-      pos += bit;
+  for (int i = 0; i < E; ++i) {
+    const bool c = x[i] > t0;
+    const uint64_t b = ballot(c);
+    if (b != 0) {
+      if (c) {
+        const int at = n + rank_in(b);
+        cl[at] = x[i];
+        if constexpr (MODE == kCand) ci_lds[at] = slot_index<T, V4>(i, lane);
+      }
+      n += __popcll(b);
     }
   }
   const float zy = yok ? element_at<T, NV, V4>(x, yr) : NAN;
   __builtin_amdgcn_wave_barrier();
-  load_row<T, NV, V4>(next, lane, x);
+  load_row<T, NV, V4>(next, lane, xn);
 
   double tau;
   int kappa;
-  uint64_t support;   // n <= 64: bit p set <=> list entry p is in the support
+  uint64_t support;
   resolve_list(cl, n, t0, m, lane, tau, kappa, support);
   const float Hf = rd32(tau);
-
-  // support bit of every register slot of this lane (supports are subsets of the candidates)
-  unsigned sm = 0;
-  if (n <= kWave) {
-    unsigned sb = base < kWave ? (unsigned)(support >> base) : 0u;
-#pragma unroll
-    for (int i = 0; i < E; ++i) {
-      const unsigned bit = (cm >> i) & 1u;
-      sm |= (bit & sb) << i;
-      sb >>= bit;
-    }
-  } else {
-    int pos = base;
-#pragma unroll
-    for (int i = 0; i < E; ++i) {
-      if ((cm >> i) & 1u) {
-        sm |= (unsigned)(cl[pos] > Hf) << i;
-        ++pos;
-      }
-    }
-  }
   __builtin_amdgcn_wave_barrier();
 
   const float inv = (float)(o.scale / (double)kappa);
@@ -694,10 +718,10 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
     for (int k = 0; k < NV; ++k) {
       uint32_t g[U];
 #pragma unroll
-      for (int e = 0; e < U; ++e) g[e] = ((sm >> (U * k + e)) & 1u) ? b_inv : 0u;
+      for (int e = 0; e < U; ++e) g[e] = x[U * k + e] > Hf ? b_inv : 0u;
       if (k == ky && lane == ly) {
 #pragma unroll
-        for (int e = 0; e < U; ++e) g[e] = e == ey ? (((sm >> (U * k + e)) & 1u) ? b_lab_in : b_lab_out) : g[e];
+        for (int e = 0; e < U; ++e) g[e] = e == ey ? (x[U * k + e] > Hf ? b_lab_in : b_lab_out) : g[e];
       }
       store_unit_bits<T, V4>(out, (uint32_t)(lane + kWave * k), g);
     }
@@ -706,15 +730,14 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
     if constexpr (V4) {
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
-        const unsigned b4 = (sm >> (4 * k)) & 0xFu;
-        const unsigned mk = (b4 & 1u) | ((b4 & 2u) << 7) | ((b4 & 4u) << 14) | ((b4 & 8u) << 21);
+        const unsigned mk = (unsigned)(x[4 * k] > Hf) | ((unsigned)(x[4 * k + 1] > Hf) << 8) |
+                            ((unsigned)(x[4 * k + 2] > Hf) << 16) | ((unsigned)(x[4 * k + 3] > Hf) << 24);
         __builtin_amdgcn_raw_buffer_store_b32(mk, out, 4 * (lane + kWave * k), 0, kNonTemporal);
       }
     } else {
 #pragma unroll
       for (int k = 0; k < NV; ++k)
-        __builtin_amdgcn_raw_buffer_store_b8((unsigned char)((sm >> k) & 1u), out, lane + kWave * k, 0,
-                                             kNonTemporal);
+        __builtin_amdgcn_raw_buffer_store_b8((unsigned char)(x[k] > Hf), out, lane + kWave * k, 0, kNonTemporal);
     }
   } else {
     // the support list, in the (deterministic) order of the candidate list; lanes without an
@@ -769,7 +792,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
                                                         const int64_t* __restrict__ tgt, int64_t N,
                                                         int C, Outs o) {
   constexpr int E = kUnit<T, V4> * NV;
-  constexpr int kListFloats = (E + 1) * kWave;   // a whole register row, then one spare slot per lane
+  constexpr int kListFloats = E * kWave;   // a whole register row
   constexpr int kIdx = MODE == kCand ? kListFloats : 1;
   __shared__ float s_list[kWavesPerBlock][kListFloats];
   __shared__ int s_idx[kWavesPerBlock][kIdx];
@@ -788,25 +811,33 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
   float my_H = 0.0f, my_loss = 0.0f;
   int my_kappa = 0;
   double lsum = 0.0;
-  float x[E];
+  float xa[E], xb[E], bias[E];
+  row_bias<T, NV, V4>(C, lane, bias);
+  auto row = [&](int k, float* x, float* xn) {
+    const int64_t y = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
+                      (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
+    const RowResult res = process_row<T, MODE, NV, V4>(w + (int64_t)k * stride, row_rsrc(k + 1), y, C, lane, x, xn,
+                                                    bias, s_list[wid], s_idx[wid], o);
+    lsum += (double)res.loss;
+    if (lane == k) {
+      my_H = res.H;
+      my_loss = res.loss;
+      my_kappa = res.kappa;
+    }
+  };
   if (nrows > 0) {
-    load_row<T, NV, V4>(row_rsrc(0), lane, x);
+    load_row<T, NV, V4>(row_rsrc(0), lane, xa);
     __builtin_amdgcn_sched_barrier(0);   // keep the mirror stores after the loads
     mirror_row_stores<T, MODE, NV, V4>(lane);
     __builtin_amdgcn_sched_barrier(0);
+    // two row buffers whose roles alternate: the loop is unrolled by two so that no buffer is copied
     int k = 0;
-    do {
-      const int64_t y = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
-                        (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
-      const RowResult res = process_row<T, MODE, NV, V4>(w + (int64_t)k * stride, row_rsrc(k + 1), y, C, lane, x,
-                                                      s_list[wid], s_idx[wid], o);
-      lsum += (double)res.loss;
-      if (lane == k) {
-        my_H = res.H;
-        my_loss = res.loss;
-        my_kappa = res.kappa;
-      }
-    } while (++k < nrows);
+    while (true) {
+      row(k, xa, xb);
+      if (++k >= nrows) break;
+      row(k, xb, xa);
+      if (++k >= nrows) break;
+    }
   }
   if (lane < nrows) {
     const int64_t r = w + (int64_t)lane * stride;
