@@ -960,6 +960,40 @@ __device__ __forceinline__ float seg_sort_desc(float v, int lane) {
   return v;
 }
 
+template <int K, int J, int L>
+__device__ __forceinline__ int seg_bitonic_step_i(int v, int lane) {
+  const int p = xor_lane_i<J>(v, lane);
+  return select_lanes_i(seg_keep_max_mask(K, J, L), max(v, p), min(v, p));
+}
+
+template <int K, int L>
+__device__ __forceinline__ int seg_bitonic_merge_i(int v, int lane) {
+  if constexpr (K >= 32) v = seg_bitonic_step_i<K, 16, L>(v, lane);
+  if constexpr (K >= 16) v = seg_bitonic_step_i<K, 8, L>(v, lane);
+  if constexpr (K >= 8) v = seg_bitonic_step_i<K, 4, L>(v, lane);
+  if constexpr (K >= 4) v = seg_bitonic_step_i<K, 2, L>(v, lane);
+  return seg_bitonic_step_i<K, 1, L>(v, lane);
+}
+
+// integer keys (fkey) of every segment sorted descending
+template <int L>
+__device__ __forceinline__ int seg_sort_desc_i(int v, int lane) {
+  v = seg_bitonic_merge_i<2, L>(v, lane);
+  v = seg_bitonic_merge_i<4, L>(v, lane);
+  v = seg_bitonic_merge_i<8, L>(v, lane);
+  v = seg_bitonic_merge_i<16, L>(v, lane);
+  if constexpr (L == 32) v = seg_bitonic_merge_i<32, L>(v, lane);
+  return v;
+}
+
+// value of lane src (per-lane source) through the LDS crossbar
+__device__ __forceinline__ double bpermute_f64(int src, double v) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_ds_bpermute(4 * src, (int)b);
+  const int hi = __builtin_amdgcn_ds_bpermute(4 * src, (int)(b >> 32));
+  return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
+}
+
 // sum/count of the entries > thr among the first n of one segment's list (li = lane in segment;
 // nmax = the largest n of the wavefront's segments)
 template <int L>
@@ -990,8 +1024,10 @@ __device__ __forceinline__ float load_one(rsrc_t r, uint32_t byte_off) {
 constexpr uint32_t kOffNone = 0x7FFFFFF0u;   // a buffer offset past every resource: access dropped
 
 // A wavefront handles groups g = w + k*stride of R consecutive rows (rows g*R + s, s < R); lane j
-// collects the results of the wavefront's row j = k*R + s.  The group's rows share one buffer
-// resource; units past a row's end are masked on load and dropped on store.
+// holds the label of the wavefront's row j = k*R + s.  The group's rows share one buffer resource;
+// units past a row's end are masked on load and dropped on store.  Two register buffers alternate
+// (the loop is unrolled by two): the next group loads into one while the other is resolved and
+// its outputs are computed from the values.
 template <typename T, int MODE, int L, int NV, bool V4>
 __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ z,
                                                        const int64_t* __restrict__ tgt, int64_t N, int C,
@@ -999,10 +1035,11 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
   constexpr int R = kWave / L;
   constexpr int U = kUnit<T, V4>;
   constexpr int E = U * NV;
+  constexpr unsigned kSegMask = L == 32 ? 0xFFFFFFFFu : 0xFFFFu;
   static_assert(E <= 32, "one mask bit per register slot");
   static_assert(MODE != kCand, "candidate lists: fwl_wave_rows");
   static_assert(std::is_same<T, float>::value || MODE == kGrad, "16-bit logits: fused op only");
-  __shared__ float s_list[kWavesPerBlock][(E + 1) * kWave];
+  __shared__ float s_list[kWavesPerBlock][E * kWave];
   __shared__ double s_wsum[kWavesPerBlock];
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
@@ -1012,7 +1049,7 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
   const int64_t G = (N + R - 1) / R;                        // row groups
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
   const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  const int ngroups = w < G ? (int)((G - 1 - w) / stride + 1) : 0;   // <= kGroupsPerWave (host grid)
+  const int ngroups = w < G ? (int)((G - 1 - w) / stride + 1) : 0;   // <= kWave / R (host grid)
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
   const int units_row = C / U;                               // V4 rows: C is a multiple of U
   auto group_rows = [&](int k) -> int {
@@ -1024,7 +1061,6 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
     const char* base = static_cast<const char*>(z) + (w + (int64_t)(k < ngroups ? k : 0) * stride) * R * (int64_t)row_bytes;
     return make_rsrc(base, (uint32_t)rows * row_bytes);
   };
-  // labels: lane j holds the label of the wavefront's row j (group j / R, segment j % R)
   int64_t my_y = 0;
   {
     const int kk = lane / R, ss = lane % R;
@@ -1032,23 +1068,19 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
     if (kk < ngroups && r < N) my_y = tgt[r];
   }
   auto seg_label = [&](int k) -> int64_t {   // label of this lane's segment row in group k
-    int64_t y = 0;
-#pragma unroll
-    for (int s = 0; s < R; ++s) {
-      const int src = (k * R + s) & 63;
-      const int64_t v = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), src) << 32) |
-                        (uint32_t)__builtin_amdgcn_readlane((int)my_y, src);
-      y = s == seg ? v : y;
-    }
-    return y;
+    const int src = (k * R + seg) & 63;
+    const int lo = __builtin_amdgcn_ds_bpermute(4 * src, (int)my_y);
+    const int hi = __builtin_amdgcn_ds_bpermute(4 * src, (int)(my_y >> 32));
+    return (int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo);
   };
   auto label_off = [&](int64_t y) -> uint32_t {
     return (y >= 0 && y < C) ? (uint32_t)seg * row_bytes + (uint32_t)(y * kElemBytes<T>) : kOffNone;
   };
-  float my_H = 0.0f, my_loss = 0.0f;
-  int my_kappa = 0;
-  double lsum = 0.0;
-  float x[E];
+  double lsum = 0.0;   // losses of the rows whose results this lane (a segment's lane 0) wrote
+  float xa[E], xb[E], bias[E];
+  // -0.0 inside the row, -inf past its end (see row_bias)
+#pragma unroll
+  for (int i = 0; i < E; ++i) bias[i] = li + L * (i / U) < units_row ? -0.0f : -INFINITY;
   auto load_group = [&](rsrc_t rs, float* xx) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -1057,10 +1089,153 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
                        xx + U * k);
     }
   };
+  float zy_next = 0.0f;
+  auto group = [&](int k, float* x, float* xn) {
+    const int rows = group_rows(k);
+    const int64_t y64 = seg_label(k);
+    const bool yok = y64 >= 0 && y64 < C;
+    const int yr = yok ? (int)y64 : -1;
+    const float zy = zy_next;
+#pragma unroll
+    for (int i = 0; i < E; ++i) x[i] += bias[i];
+    if (rows < R) {   // phantom segments of a short last group
+      const bool valid = seg < rows;
+#pragma unroll
+      for (int i = 0; i < E; ++i) x[i] = valid ? x[i] : -INFINITY;
+    }
+    float lm = x[0];
+#pragma unroll
+    for (int i = 1; i < E; ++i) lm = fmaxf(lm, x[i]);
+    const float m = seg_max_f32<L>(lm, lane);
+    const float t0 = bound_below_max(m);
+    // candidates z > t0, lane-major inside the segment's list
+    unsigned cm = 0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) cm |= (unsigned)(x[i] > t0) << i;
+    const int cnt = __popc(cm);
+    const int base = seg_excl_scan_i32<L>(cnt);
+    const int n = seg_sum_i32<L>(cnt, lane);
+    float* cls = cl + seg * (L * E);   // this segment's list
+    {
+      int pos = base;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        if ((cm >> i) & 1u) {
+          cls[pos] = x[i];
+          ++pos;
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // next group's loads into the other buffer
+    const bool has_next = k + 1 < ngroups;
+    const rsrc_t rs_next = has_next ? group_rsrc(k + 1) : make_rsrc(z, 0u);
+    load_group(rs_next, xn);
+    zy_next = load_one<T>(rs_next, label_off(seg_label(has_next ? k + 1 : k)));
+
+    double tau = NAN;
+    int kappa = 0;
+    const bool big = ballot(n > L) != 0;
+    if (!big) {
+      // sort, fp64 prefix sums, the support size by k z_(k) > S_k - 1 (see select_tier)
+      const float c = li < n ? cls[li] : -INFINITY;
+      int key = fkey(li < n ? c + 0.0f : -INFINITY);
+      key = seg_sort_desc_i<L>(key, lane);
+      const float v = fkey_inv(key);
+      const double S = scan_f64<L>(li < n ? (double)v : 0.0);
+      const uint64_t in = ballot(li < n && (double)v * (double)(li + 1) > S - 1.0);
+      const unsigned sb = ((unsigned)(in >> (seg * L)) & kSegMask) | 1u;
+      const int kap = 32 - __clz(sb);
+      const double Sk = bpermute_f64(seg * L + kap - 1, S);
+      tau = n > 0 ? clamp_below_max((Sk - 1.0) / (double)kap, m) : NAN;
+      const uint64_t sup = ballot(li < n && c > rd32(tau));
+      kappa = __popc((unsigned)(sup >> (seg * L)) & kSegMask);
+    } else {
+      // fixed-point iterations per segment over its list, until every segment has converged
+      const int nmax = (int)wave_max_f32((float)n);
+      double t = (double)t0, s, s2;
+      int c, c2;
+      seg_list_sum_count<L>(cls, n, nmax, t0, li, lane, s, c);
+      bool done = n == 0;
+      for (int it = 0; it <= nmax + 1; ++it) {
+        if (ballot(!done) == 0) break;
+        const double tn = (s - 1.0) / (double)c;
+        seg_list_sum_count<L>(cls, n, nmax, rd32(tn), li, lane, s2, c2);
+        if (!done) {
+          if (c2 == c || !(tn > t)) {
+            tau = tn;
+            kappa = c2;
+            done = true;
+          } else {
+            t = tn;
+            s = s2;
+            c = c2;
+          }
+        }
+      }
+      const double tc = n > 0 ? clamp_below_max(tau, m) : tau;
+      const bool clamped = tc != tau && n > 0;
+      if (ballot(clamped) != 0) {
+        double s3;
+        int k3;
+        seg_list_sum_count<L>(cls, n, nmax, rd32(tc), li, lane, s3, k3);
+        if (clamped) kappa = k3;
+      }
+      tau = tc;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float Hf = rd32(tau);
+    const float inv = (float)(o.scale / (double)kappa);
+    const int64_t row0 = (w + (int64_t)k * stride) * R;   // first row of this group
+    const int qy = yr / U, ky = yr >= 0 ? qy / L : -1, lyl = qy % L, ey = yr % U;
+    if constexpr (MODE == kGrad) {
+      const rsrc_t outr = make_rsrc(static_cast<char*>(o.grad) + row0 * (int64_t)row_bytes,
+                                    (uint32_t)rows * row_bytes);
+      const uint32_t b_inv = encode<T>(inv), b_lab_in = encode<T>(inv - o.scale_f);
+      const uint32_t b_lab_out = encode<T>(0.0f - o.scale_f);
+#pragma unroll
+      for (int kk = 0; kk < NV; ++kk) {
+        const int u = li + L * kk;
+        uint32_t g[U];
+#pragma unroll
+        for (int e = 0; e < U; ++e) g[e] = x[U * kk + e] > Hf ? b_inv : 0u;
+        if (kk == ky && li == lyl) {
+#pragma unroll
+          for (int e = 0; e < U; ++e) g[e] = e == ey ? (x[U * kk + e] > Hf ? b_lab_in : b_lab_out) : g[e];
+        }
+        store_unit_bits<T, V4>(outr, u < units_row ? (uint32_t)(seg * units_row + u) : (kOffNone >> 4), g);
+      }
+    } else {
+      const rsrc_t outr = make_rsrc(o.mask + row0 * (int64_t)C, (uint32_t)(rows * C));
+#pragma unroll
+      for (int kk = 0; kk < NV; ++kk) {
+        const int u = li + L * kk;
+        if constexpr (V4) {
+          const unsigned mk = (unsigned)(x[4 * kk] > Hf) | ((unsigned)(x[4 * kk + 1] > Hf) << 8) |
+                              ((unsigned)(x[4 * kk + 2] > Hf) << 16) | ((unsigned)(x[4 * kk + 3] > Hf) << 24);
+          __builtin_amdgcn_raw_buffer_store_b32(mk, outr, u < units_row ? (uint32_t)(seg * C + 4 * u) : kOffNone, 0,
+                                                kNonTemporal);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b8((unsigned char)(x[kk] > Hf), outr,
+                                               u < units_row ? (uint32_t)(seg * C + u) : kOffNone, 0, kNonTemporal);
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // per-row results, written by lane 0 of each segment
+    if (li == 0 && seg < rows) {
+      const float loss = (float)((1.0 - (double)(yok ? zy : NAN)) + tau);
+      const int64_t r = row0 + seg;
+      if (o.H) o.H[r] = Hf;
+      if (o.loss) o.loss[r] = loss;
+      if (o.kappa) o.kappa[r] = kappa;
+      lsum += (double)loss;
+    }
+  };
   if (ngroups > 0) {
     rsrc_t rs = group_rsrc(0);
-    load_group(rs, x);
-    float zy_next = load_one<T>(rs, label_off(seg_label(0)));
+    load_group(rs, xa);
+    zy_next = load_one<T>(rs, label_off(seg_label(0)));
     __builtin_amdgcn_sched_barrier(0);   // mirror of the loop's stores (see mirror_row_stores)
     {
       const rsrc_t none = make_rsrc(nullptr, 0u);
@@ -1073,177 +1248,15 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
     }
     __builtin_amdgcn_sched_barrier(0);
     int k = 0;
-    do {
-      const int rows = group_rows(k);
-      const bool valid = seg < rows;
-      const int64_t y64 = seg_label(k);
-      const bool yok = y64 >= 0 && y64 < C;
-      const int yr = yok ? (int)y64 : -1;
-      const float zy = zy_next;
-      // mask units past the row end and phantom segments
-#pragma unroll
-      for (int kk = 0; kk < NV; ++kk) {
-        const bool ok = valid && li + L * kk < units_row;
-#pragma unroll
-        for (int e = 0; e < U; ++e) x[U * kk + e] = ok ? x[U * kk + e] : -INFINITY;
-      }
-      float lm = x[0];
-#pragma unroll
-      for (int i = 1; i < E; ++i) lm = fmaxf(lm, x[i]);
-      const float m = seg_max_f32<L>(lm, lane);
-      const float t0 = bound_below_max(m);
-      unsigned cm = 0;
-#pragma unroll
-      for (int i = 0; i < E; ++i) cm |= (unsigned)(x[i] > t0) << i;
-      const int cnt = __popc(cm);
-      const int base = seg_excl_scan_i32<L>(cnt);
-      const int n = seg_sum_i32<L>(cnt, lane);
-      float* cls = cl + seg * (L * E);   // this segment's list
-      {
-        int pos = base;
-#pragma unroll
-        for (int i = 0; i < E; ++i) {
-          const int bit = (cm >> i) & 1;
-          cl[bit ? seg * (L * E) + pos : E * kWave + lane] = x[i];
-          pos += bit;
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
-      // next group's loads into the same registers
-      const rsrc_t rs_next = group_rsrc(k + 1 < ngroups ? k + 1 : 0);
-      const bool has_next = k + 1 < ngroups;
-      load_group(has_next ? rs_next : make_rsrc(z, 0u), x);
-      zy_next = load_one<T>(has_next ? rs_next : make_rsrc(z, 0u), label_off(seg_label(k + 1 < ngroups ? k + 1 : k)));
-
-      double tau = NAN;
-      int kappa = 0;
-      unsigned sm = 0;
-      const bool big = ballot(n > L) != 0;
-      if (!big) {
-        const float c = li < n ? cls[li] : -INFINITY;
-        float v = li < n ? c + 0.0f : -INFINITY;   // + 0.0f: -0.0 -> +0.0 before min/max
-        v = seg_sort_desc<L>(v, lane);
-        const double S = scan_f64<L>(li < n ? (double)v : 0.0);
-        const double f = (S - 1.0) / (double)(li + 1);
-        const double fmax_seg = seg_max_f64<L>(li < n ? f : -INFINITY, lane);   // every lane takes part
-        tau = n > 0 ? clamp_below_max(fmax_seg, m) : NAN;
-        const uint64_t sup = ballot(li < n && c > rd32(tau));
-        const unsigned segbits = (unsigned)((sup >> (seg * L)) & (L == 32 ? 0xFFFFFFFFull : 0xFFFFull));
-        kappa = __popc(segbits);
-        unsigned sb = base < L ? segbits >> base : 0u;
-#pragma unroll
-        for (int i = 0; i < E; ++i) {
-          const unsigned bit = (cm >> i) & 1u;
-          sm |= (bit & sb) << i;
-          sb >>= bit;
-        }
-      } else {
-        // fixed-point iterations per segment over its list, until every segment has converged
-        const int nmax = (int)wave_max_f32((float)n);
-        double t = (double)t0, s, s2;
-        int c, c2;
-        seg_list_sum_count<L>(cls, n, nmax, t0, li, lane, s, c);
-        bool done = n == 0;
-        for (int it = 0; it <= nmax + 1; ++it) {
-          if (ballot(!done) == 0) break;
-          const double tn = (s - 1.0) / (double)c;
-          seg_list_sum_count<L>(cls, n, nmax, rd32(tn), li, lane, s2, c2);
-          if (!done) {
-            if (c2 == c || !(tn > t)) {
-              tau = tn;
-              kappa = c2;
-              done = true;
-            } else {
-              t = tn;
-              s = s2;
-              c = c2;
-            }
-          }
-        }
-        const double tc = n > 0 ? clamp_below_max(tau, m) : tau;
-        const bool clamped = tc != tau && n > 0;
-        if (ballot(clamped) != 0) {
-          double s3;
-          int k3;
-          seg_list_sum_count<L>(cls, n, nmax, rd32(tc), li, lane, s3, k3);
-          if (clamped) kappa = k3;
-        }
-        tau = tc;
-        const float Hc = rd32(tau);
-        int pos = base;
-#pragma unroll
-        for (int i = 0; i < E; ++i) {
-          if ((cm >> i) & 1u) {
-            sm |= (unsigned)(cls[pos] > Hc) << i;
-            ++pos;
-          }
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
-      const float Hf = rd32(tau);
-      const float inv = (float)(o.scale / (double)kappa);
-      const int64_t row0 = (w + (int64_t)k * stride) * R;   // first row of this group
-      const int qy = yr / U, ky = yr >= 0 ? qy / L : -1, lyl = qy % L, ey = yr % U;
-      if constexpr (MODE == kGrad) {
-        const rsrc_t outr = make_rsrc(static_cast<char*>(o.grad) + row0 * (int64_t)row_bytes,
-                                      (uint32_t)rows * row_bytes);
-        const uint32_t b_inv = encode<T>(inv), b_lab_in = encode<T>(inv - o.scale_f);
-        const uint32_t b_lab_out = encode<T>(0.0f - o.scale_f);
-#pragma unroll
-        for (int kk = 0; kk < NV; ++kk) {
-          const int u = li + L * kk;
-          uint32_t g[U];
-#pragma unroll
-          for (int e = 0; e < U; ++e) g[e] = ((sm >> (U * kk + e)) & 1u) ? b_inv : 0u;
-          if (kk == ky && li == lyl) {
-#pragma unroll
-            for (int e = 0; e < U; ++e) g[e] = e == ey ? (((sm >> (U * kk + e)) & 1u) ? b_lab_in : b_lab_out) : g[e];
-          }
-          store_unit_bits<T, V4>(outr, u < units_row ? (uint32_t)(seg * units_row + u) : (kOffNone >> 4), g);
-        }
-      } else {
-        const rsrc_t outr = make_rsrc(o.mask + row0 * (int64_t)C, (uint32_t)(rows * C));
-#pragma unroll
-        for (int kk = 0; kk < NV; ++kk) {
-          const int u = li + L * kk;
-          if constexpr (V4) {
-            const unsigned b4 = (sm >> (4 * kk)) & 0xFu;
-            const unsigned mk = (b4 & 1u) | ((b4 & 2u) << 7) | ((b4 & 4u) << 14) | ((b4 & 8u) << 21);
-            __builtin_amdgcn_raw_buffer_store_b32(mk, outr, u < units_row ? (uint32_t)(seg * C + 4 * u) : kOffNone, 0,
-                                                  kNonTemporal);
-          } else {
-            __builtin_amdgcn_raw_buffer_store_b8((unsigned char)((sm >> kk) & 1u), outr,
-                                                 u < units_row ? (uint32_t)(seg * C + u) : kOffNone, 0, kNonTemporal);
-          }
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
-      // per-row results: segment s of group k is the wavefront's row k*R + s, kept in that lane
-      const float loss = (float)((1.0 - (double)(yok ? zy : NAN)) + tau);
-#pragma unroll
-      for (int s = 0; s < R; ++s) {
-        const float Hs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(Hf), s * L));
-        const float Ls = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(loss), s * L));
-        const int Ks = __builtin_amdgcn_readlane(kappa, s * L);
-        if (s < rows) lsum += (double)Ls;
-        if (lane == k * R + s) {
-          my_H = Hs;
-          my_loss = Ls;
-          my_kappa = Ks;
-        }
-      }
-    } while (++k < ngroups);
-  }
-  {
-    const int kk = lane / R, ss = lane % R;
-    const int64_t r = (w + (int64_t)kk * stride) * R + ss;
-    if (kk < ngroups && r < N) {
-      if (o.H) o.H[r] = my_H;
-      if (o.loss) o.loss[r] = my_loss;
-      if (o.kappa) o.kappa[r] = my_kappa;
+    while (true) {
+      group(k, xa, xb);
+      if (++k >= ngroups) break;
+      group(k, xb, xa);
+      if (++k >= ngroups) break;
     }
   }
-  if (lane == 0) s_wsum[wid] = lsum;
+  const double wsum = wave_sum_f64(lsum);
+  if (lane == 0) s_wsum[wid] = wsum;
   __syncthreads();
   const double bsum = (s_wsum[0] + s_wsum[1]) + (s_wsum[2] + s_wsum[3]);
   mean_epilogue(bsum, o);
