@@ -187,7 +187,9 @@ constexpr int kMaxBlocksWave = 2048;   // grid cap of fwl_wave_rows (4 rows in f
 constexpr int kMaxBlocksRow = 4096;    // grid cap of fwl_block_rows
 constexpr int kStreamUnroll = 4;       // 128-bit loads per lane per streaming round
 constexpr int kRoundSlotsV1 = 16;      // 32-bit loads per lane per streaming round (unaligned rows)
-constexpr size_t kWsHeader = 256;      // ticket counter, then fp64 partial sums
+constexpr size_t kWsHeader = 256;      // the final ticket counter; then the mean's partial sums
+constexpr int kTicketGroup = 32;       // blocks per first-level ticket of the mean
+constexpr int kTicketStride = 16;      // first-level tickets 64 bytes apart
 
 enum Mode : int { kGrad = 0, kMask = 1, kCand = 2 };
 
@@ -204,8 +206,10 @@ struct Outs {
   double scale;        // gradient scale (1/N for the mean reduction)
   double reduce_div;   // mean = sum(losses) / reduce_div
   float scale_f;
-  unsigned* ticket;
-  double* partials;
+  unsigned* ticket;     // final ticket
+  double* partials;     // one per block
+  double* gpartials;    // one per group of kTicketGroup blocks
+  unsigned* gtickets;   // one per group (kTicketStride apart)
   int force_generic;
   int cap;             // LDS candidate capacity per wavefront (<= kCapMax)
 };
@@ -509,20 +513,51 @@ __device__ void mean_epilogue(double bsum, const Outs& o) {
   __shared__ int s_last;
   __shared__ double s_red[kBlock];
   if (o.mean == nullptr) return;
-  if (threadIdx.x == 0) {
-    // The partial is an agent-scope atomic store (coherent across the XCDs' L2 caches); once it
-    // has completed, the ticket increment publishes it.  A device-scope fence here would write
-    // back the whole L2 of the XCD at the end of every block.
-    __hip_atomic_store(o.partials + blockIdx.x, bsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    wait_vmem();
-    const unsigned t = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (t == gridDim.x - 1);
+  // Two ticket levels: the last block of each group of kTicketGroup blocks sums the group's
+  // partials (in block order) and takes the final ticket; the last of those sums the group sums.
+  // When many blocks finish together, no single counter serialises more than
+  // max(kTicketGroup, groups) atomics.
+  const unsigned nb = gridDim.x;
+  const unsigned g = blockIdx.x / kTicketGroup;
+  const unsigned ng = (nb + kTicketGroup - 1) / kTicketGroup;
+  const unsigned g0 = g * kTicketGroup;
+  const unsigned gsize = nb - g0 < (unsigned)kTicketGroup ? nb - g0 : (unsigned)kTicketGroup;
+  if (threadIdx.x < kWave) {   // wavefront 0
+    const int lane = (int)threadIdx.x;
+    unsigned* gt = o.gtickets + (size_t)g * kTicketStride;
+    unsigned t = 0;
+    if (lane == 0) {
+      // The partial is an agent-scope atomic store (coherent across the XCDs' L2 caches); once it
+      // has completed, the ticket increment publishes it.  A device-scope fence here would write
+      // back the whole L2 of the XCD at the end of every block.
+      __hip_atomic_store(o.partials + blockIdx.x, bsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wait_vmem();
+      t = __hip_atomic_fetch_add(gt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    t = (unsigned)__builtin_amdgcn_readfirstlane((int)t);
+    int last = 0;
+    if (t == gsize - 1) {
+      // the group's partials, one per lane, summed in a fixed order
+      const double v = lane < (int)gsize
+                           ? __hip_atomic_load(o.partials + g0 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : 0.0;
+      const double gs = wave_sum_f64(v);
+      unsigned t2 = 0;
+      if (lane == 0) {
+        __hip_atomic_store(o.gpartials + g, gs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_vmem();
+        t2 = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      last = (unsigned)__builtin_amdgcn_readfirstlane((int)t2) == ng - 1;
+    }
+    if (lane == 0) s_last = last;
   }
   __syncthreads();
   if (!s_last) return;
   double acc = 0.0;
-  for (unsigned i = threadIdx.x; i < gridDim.x; i += kBlock)
-    acc += __hip_atomic_load(o.partials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (unsigned i = threadIdx.x; i < ng; i += kBlock)
+    acc += __hip_atomic_load(o.gpartials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   s_red[threadIdx.x] = acc;
   __syncthreads();
   for (int s = kBlock / 2; s > 0; s >>= 1) {
@@ -2549,6 +2584,13 @@ int64_t partial_slots(int64_t N) {
   return wave_max > b ? wave_max : b;
 }
 
+// the mean's part of the workspace: final ticket, block partials, group partials, group tickets
+size_t mean_ws_bytes(int64_t N) {
+  const size_t P = (size_t)partial_slots(N);
+  const size_t G = (P + kTicketGroup - 1) / kTicketGroup;
+  return kWsHeader + sizeof(double) * P + sizeof(double) * G + sizeof(unsigned) * kTicketStride * G;
+}
+
 size_t split_scratch_bytes(int64_t N, int64_t C) {
   const int64_t items = N * split_chunks_bound(N, C, kSplitMinChunk);
   return (size_t)items * (sizeof(double) + sizeof(int) + (size_t)kSplitCap * (sizeof(float) + sizeof(int)));
@@ -2560,7 +2602,7 @@ void launch_split(const void* z, const int64_t* y, int64_t N, int C, const Outs&
   static_assert(kRound >= kSplitMinChunk, "the workspace bound assumes rounds of >= kSplitMinChunk elements");
   const SplitPlan pl = split_plan(N, C, kRound);
   const int64_t items = N * split_chunks_bound(N, C, kSplitMinChunk);   // the workspace layout
-  char* base = static_cast<char*>(ws) + kWsHeader + sizeof(double) * (size_t)partial_slots(N);
+  char* base = static_cast<char*>(ws) + mean_ws_bytes(N);
   SplitScratch sc;
   sc.tau = reinterpret_cast<double*>(base);
   sc.count = reinterpret_cast<int*>(base + sizeof(double) * items);
@@ -2592,8 +2634,13 @@ int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scal
   o.force_generic = g_path == 3 || g_path == 5;
   if (o.mean != nullptr) {
     if (ws == nullptr || ws_bytes < fwl_workspace_bytes(N, C64) || !aligned(ws, 8)) return FWL_ERR_WORKSPACE;
-    o.ticket = static_cast<unsigned*>(ws);
-    o.partials = reinterpret_cast<double*>(static_cast<char*>(ws) + kWsHeader);
+    const size_t P = (size_t)partial_slots(N);
+    const size_t G = (P + kTicketGroup - 1) / kTicketGroup;
+    char* wb = static_cast<char*>(ws);
+    o.ticket = reinterpret_cast<unsigned*>(wb);
+    o.partials = reinterpret_cast<double*>(wb + kWsHeader);
+    o.gpartials = reinterpret_cast<double*>(wb + kWsHeader + sizeof(double) * P);
+    o.gtickets = reinterpret_cast<unsigned*>(wb + kWsHeader + sizeof(double) * (P + G));
   }
   if (N == 0) {
     if (o.mean != nullptr) hipLaunchKernelGGL(fwl_empty_mean, dim3(1), dim3(1), 0, s, o.mean, reduce_div);
@@ -2672,7 +2719,7 @@ const char* fwl_status_string(int status) {
 size_t fwl_workspace_bytes(int64_t N, int64_t C) {
   if (N < 0) N = 0;
   // the completion counter, the fp64 partials of the mean, then the split rows' scratch
-  size_t b = kWsHeader + sizeof(double) * (size_t)partial_slots(N);
+  size_t b = mean_ws_bytes(N);
   if (split_rows(N, C, 4, g_path)) b += split_scratch_bytes(N, C);
   return b;
 }
