@@ -29,8 +29,9 @@
 //                   tightened by fixed-point iterations on the list; a list that cannot be
 //                   tightened sends the row to the generic multi-pass path.
 //   fwl_mask_to_grad, fwl_cand_to_grad   the two-op backward of the drop-in interface.
-// The mean loss is reduced in fp64 in a fixed order: per-block partial sums, then the last block
-// to finish (ticket counter in the caller's workspace) sums the partials and resets the counter.
+// The mean loss is reduced in fp64 in a fixed order: per-block partial sums, per-group sums by the
+// last block of each group of 32, then the last group finisher sums the group sums (ticket
+// counters in the caller's workspace, each reset by its last user).
 //
 // Compile with -Xclang -target-feature -Xclang -packed-fp32-ops (see fwloss_build.py).
 #include <hip/hip_runtime.h>

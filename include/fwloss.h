@@ -22,10 +22,10 @@
  *   - all pointers are device pointers; logits and grad are row-major [N, C], contiguous;
  *   - every call is asynchronous on `stream` and allocates nothing;
  *   - `workspace` is caller-provided device memory of at least fwl_workspace_bytes(N, C) bytes,
- *     8-byte aligned and zero-filled before its first use.  Its first 256 bytes hold a completion
- *     counter that every call returns to zero; the rest is scratch (per-block partial sums, and
- *     for few long rows the chunk thresholds and supports), written before it is read.  Calls
- *     that run concurrently (different streams) must not share one workspace;
+ *     8-byte aligned and zero-filled before its first use.  It holds completion counters, which
+ *     every call returns to zero, and scratch that every call writes before reading it (partial
+ *     sums of the mean; for few long rows the chunk thresholds and supports).  Calls that run
+ *     concurrently (different streams) must not share one workspace;
  *   - targets outside [0, C) do not fault: that row gets loss = NaN and no label term in grad;
  *   - NaN logits are never selected; rows without a finite maximum give kappa = 0, H = NaN;
  *   - the return value is FWL_OK or an fwl_status (argument errors are detected before launch).
@@ -62,9 +62,10 @@ enum fwl_dtype {
 const char* fwl_status_string(int status);
 
 /* Bytes of device workspace the forward entry points need for an [N, C] problem: 256 bytes, one
- * fp64 per block of the largest grid (>= 4096), and for at most 128 rows of >= 24576 elements
- * 524 bytes per (row, chunk).  The answer follows the current fwl_set_params switches (forcing
- * path 7 needs the chunk scratch for rows of any length). */
+ * fp64 per block of the largest grid (>= 4096 blocks), 72 bytes per group of 32 blocks, and for
+ * at most 128 rows of >= 24576 elements 524 bytes per (row, chunk).  The answer follows the
+ * current fwl_set_params switches (forcing path 7 needs the chunk scratch for rows of any
+ * length). */
 size_t fwl_workspace_bytes(int64_t N, int64_t C);
 
 /* Fused forward + backward: the whole hot path in one launch, reading logits once and writing the
