@@ -49,6 +49,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--rows", type=int, default=None,
+                    help="rows of the batch (default: the configuration's N; few rows of a long "
+                         "configuration run the split-row kernels)")
     ap.add_argument("--sets", type=int, default=3, help="rotated input/output buffer sets")
     ap.add_argument("--dtype", default="f32", choices=["f32", "bf16", "f16"],
                     help="element type of the logits and the gradient (decisions are fp32/fp64)")
@@ -139,8 +142,9 @@ def main():
         return
 
     dev = torch.device("cuda:0")
-    z_np, y_np = fwloss_data.make(args.config, seed=0)
+    z_np, y_np = fwloss_data.make(args.config, N=args.rows, seed=0)
     N, C = z_np.shape
+    cfg_tag = args.config if args.rows is None else f"{args.config}_{N}rows"
     tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[args.dtype]
     sets = []
     for s in range(args.sets):
@@ -195,13 +199,15 @@ def main():
         torch.cuda.synchronize()
         two_op_ms = (time.perf_counter() - t1) * 1e3 / args.steps
 
-    # the kernel the automatic dispatch runs for this row length (16-byte aligned rows)
+    # the (dominant) kernel the automatic dispatch runs for this shape (16-byte aligned rows)
     unit = 16 // ELEM_BYTES[args.dtype]
-    if C % unit == 0 and C // unit <= 64:
+    if N <= 128 and C * ELEM_BYTES[args.dtype] >= 96 * 1024:
+        tag = "fwl_split_chunks"
+    elif C % unit == 0 and C // unit <= 64:
         tag = "fwl_seg_rows"
     else:
         tag = "fwl_wave_rows" if C <= 2048 else ("fwl_wave_stream_rows" if C <= 8192 else "fwl_block_rows")
-    traffic = traffic_for(tag, args.config if args.dtype == "f32" else f"{args.config}_{args.dtype}")
+    traffic = traffic_for(tag, cfg_tag if args.dtype == "f32" else f"{cfg_tag}_{args.dtype}")
     result = {
         "metric": METRIC,
         "value": N * args.steps / wall,
@@ -215,7 +221,7 @@ def main():
         "vs_baseline": None,
         "dtype": args.dtype,
         "data": "synthetic",
-        "config": {"workload": f"{args.config} fused FW loss forward+backward, N={N} C={C} {args.dtype} logits "
+        "config": {"workload": f"{cfg_tag} fused FW loss forward+backward, N={N} C={C} {args.dtype} logits "
                                "(fwloss_data.make), labels uniform int64, buffers rotated over "
                                f"{args.sets} sets", "N": N, "C": C, "op": "fw_forward_backward",
                    "parallelism": "single GPU"},

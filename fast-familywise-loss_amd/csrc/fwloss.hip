@@ -191,6 +191,7 @@ constexpr int kRoundSlotsV1 = 16;      // 32-bit loads per lane per streaming ro
 constexpr size_t kWsHeader = 256;      // the final ticket counter; then the mean's partial sums
 constexpr int kTicketGroup = 32;       // blocks per first-level ticket of the mean
 constexpr int kTicketStride = 16;      // first-level tickets 64 bytes apart
+constexpr uint32_t kOffNone = 0x7FFFFFF0u;   // a buffer offset past every resource: access dropped
 
 enum Mode : int { kGrad = 0, kMask = 1, kCand = 2 };
 
@@ -213,6 +214,8 @@ struct Outs {
   unsigned* gtickets;   // one per group (kTicketStride apart)
   int force_generic;
   int cap;             // LDS candidate capacity per wavefront (<= kCapMax)
+  int cstride;         // candidate-list mode: row stride of cval/cidx (C for the drop-in op)
+  int ccap;            // candidate-list mode: entries kept per row (further ones are dropped)
 };
 
 // ------------------------------------------------------------------------------------------------
@@ -702,7 +705,7 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
                                                  const Outs& o) {
   constexpr int U = kUnit<T, V4>;
   constexpr int E = U * NV;
-  static_assert(std::is_same<T, float>::value || MODE == kGrad, "16-bit logits: fused op only");
+  static_assert(std::is_same<T, float>::value || MODE != kMask, "16-bit logits: no mask output");
   const bool yok = y64 >= 0 && y64 < C;
   const int yr = yok ? (int)y64 : -1;
 #pragma unroll
@@ -778,15 +781,15 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
   } else {
     // the support list, in the (deterministic) order of the candidate list; lanes without an
     // entry store past the end of the resource (dropped)
-    const rsrc_t outv = make_rsrc(o.cval + r * (int64_t)C, 4u * (uint32_t)C);
-    const rsrc_t outi = make_rsrc(o.cidx + r * (int64_t)C, 4u * (uint32_t)C);
+    const rsrc_t outv = make_rsrc(o.cval + r * (int64_t)o.cstride, 4u * (uint32_t)o.ccap);
+    const rsrc_t outi = make_rsrc(o.cidx + r * (int64_t)o.cstride, 4u * (uint32_t)o.ccap);
     int out = 0;
     for (int p0 = 0; p0 < n; p0 += kWave) {
       const int p = p0 + lane;
       const float v = p < n ? cl[p] : -INFINITY;
       const bool k = v > Hf;
       const uint64_t b = ballot(k);
-      const uint32_t at = k ? 4u * (uint32_t)(out + rank_in(b)) : 4u * (uint32_t)C;
+      const uint32_t at = k ? 4u * (uint32_t)(out + rank_in(b)) : kOffNone;
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), outv, at, 0, 0);
       __builtin_amdgcn_raw_buffer_store_b32((unsigned)(p < n ? ci_lds[p] : 0), outi, at, 0, 0);
       out += __popcll(b);
@@ -1057,7 +1060,6 @@ __device__ __forceinline__ float load_one(rsrc_t r, uint32_t byte_off) {
     return widen16<T>(__builtin_amdgcn_raw_buffer_load_b16(r, byte_off, 0, 0));
 }
 
-constexpr uint32_t kOffNone = 0x7FFFFFF0u;   // a buffer offset past every resource: access dropped
 
 // A wavefront handles groups g = w + k*stride of R consecutive rows (rows g*R + s, s < R); lane j
 // holds the label of the wavefront's row j = k*R + s.  The group's rows share one buffer resource;
@@ -1652,8 +1654,8 @@ __device__ void generic_row(const void* __restrict__ row, int64_t r, int C, int 
     for (int j = threadIdx.x; j < C; j += kBlock)
       if (j != yr) mk[j] = (uint8_t)(load_elem<T>(row, j) > Hf);
   } else {
-    float* cv = o.cval + r * (int64_t)C;
-    int32_t* ci = o.cidx + r * (int64_t)C;
+    float* cv = o.cval + r * (int64_t)o.cstride;
+    int32_t* ci = o.cidx + r * (int64_t)o.cstride;
     int base = 0;
     for (int j0 = 0; j0 < C; j0 += kBlock) {
       const int j = j0 + (int)threadIdx.x;
@@ -1665,7 +1667,7 @@ __device__ void generic_row(const void* __restrict__ row, int64_t r, int C, int 
       __syncthreads();
       int off = base;
       for (int w = 0; w < wid; ++w) off += sh.wsel[w];
-      if (p) {
+      if (p && off + rank_in(b) < o.ccap) {
         const int pos = off + rank_in(b);
         cv[pos] = v;
         ci[pos] = j;
@@ -1733,14 +1735,14 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
         __syncthreads();
         int off = 0;
         for (int w = 0; w < wid; ++w) off += sh.wsel[w];
-        float* cv = o.cval + r * (int64_t)C;
-        int32_t* ci = o.cidx + r * (int64_t)C;
+        float* cv = o.cval + r * (int64_t)o.cstride;
+        int32_t* ci = o.cidx + r * (int64_t)o.cstride;
         for (int p0 = 0; p0 < n; p0 += kWave) {
           const int p = p0 + lane;
           const float v = p < n ? bv[p] : -INFINITY;
           const bool k = v > Hf;
           const uint64_t b = ballot(k);
-          if (k) {
+          if (k && off + rank_in(b) < o.ccap) {
             const int pos = off + rank_in(b);
             cv[pos] = v;
             ci[pos] = bi[p];
@@ -1905,9 +1907,9 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
           const float v = p < n ? bv[p] : -INFINITY;
           const bool sel = v > Hf;
           const uint64_t b = ballot(sel);
-          if (sel) {
-            o.cval[r * (int64_t)C + out + rank_in(b)] = v;
-            o.cidx[r * (int64_t)C + out + rank_in(b)] = bi[p];
+          if (sel && out + rank_in(b) < o.ccap) {
+            o.cval[r * (int64_t)o.cstride + out + rank_in(b)] = v;
+            o.cidx[r * (int64_t)o.cstride + out + rank_in(b)] = bi[p];
           }
           out += __popcll(b);
         }
@@ -1926,9 +1928,9 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
           const float v = j < C ? load_elem<T>(row, j) : -INFINITY;
           const bool sel = v > Hf;
           const uint64_t b = ballot(sel);
-          if (sel) {
-            o.cval[r * (int64_t)C + out + rank_in(b)] = v;
-            o.cidx[r * (int64_t)C + out + rank_in(b)] = j;
+          if (sel && out + rank_in(b) < o.ccap) {
+            o.cval[r * (int64_t)o.cstride + out + rank_in(b)] = v;
+            o.cidx[r * (int64_t)o.cstride + out + rank_in(b)] = j;
           }
           out += __popcll(b);
         }
@@ -2196,9 +2198,9 @@ __global__ __launch_bounds__(kBlock) void fwl_split_finish(const void* __restric
           __syncthreads();
           int q = base;
           for (int w = 0; w < wid; ++w) q += sh.wsel[w];
-          if (sel) {
-            o.cval[r * (int64_t)C + q + rank_in(b)] = v;
-            o.cidx[r * (int64_t)C + q + rank_in(b)] = cx[p];
+          if (sel && q + rank_in(b) < o.ccap) {
+            o.cval[r * (int64_t)o.cstride + q + rank_in(b)] = v;
+            o.cidx[r * (int64_t)o.cstride + q + rank_in(b)] = cx[p];
           }
           base += (sh.wsel[0] + sh.wsel[1]) + (sh.wsel[2] + sh.wsel[3]);
           __syncthreads();
@@ -2345,6 +2347,74 @@ __global__ __launch_bounds__(kBlock) void fwl_cand_to_grad(
     }
     if (threadIdx.x == 0 && yr >= 0) gr[yr] = (z[r * (int64_t)C + yr] > h ? inv : 0.0f) - scale_f;
     __syncthreads();
+  }
+}
+
+// Second pass of the fused op for long rows.  A read pass over the logits (the candidate-list
+// kernel, with its lists cut at kTwoPassCap entries in the workspace) leaves every row's H, kappa
+// and support; this kernel then writes the dense gradient, each 128-bit unit once with its final
+// value, from an LDS bitmap of the row's support.  Rows whose support exceeds the list, and rows
+// longer than the bitmap, are recomputed from the logits (z > H).  Separating the read stream
+// from the write stream lets each run at its own rate instead of interleaving them.
+constexpr int kTwoPassCap = 64;          // support entries kept per row between the passes
+constexpr int kBitmapBits = 1 << 18;     // longest row with an LDS bitmap (32 KB)
+
+template <typename T, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_support_to_grad(
+    const void* __restrict__ z, const int64_t* __restrict__ tgt, const float* __restrict__ Hin,
+    const int32_t* __restrict__ kap_in, const int32_t* __restrict__ cidx, int64_t N, int C, double scale,
+    float scale_f, void* __restrict__ grad) {
+  constexpr int U = kUnit<T, V4>;
+  __shared__ uint32_t bits[kBitmapBits / 32];
+  const bool use_bits = C <= kBitmapBits;
+  if (use_bits)
+    for (int i = threadIdx.x; i < (C + 31) / 32; i += kBlock) bits[i] = 0u;
+  __syncthreads();
+  const int units = (C + U - 1) / U;
+  const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
+  for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
+    const int kap = kap_in[r];
+    const float Hf = Hin[r];
+    const int64_t y64 = tgt[r];
+    const int yr = (y64 >= 0 && y64 < C) ? (int)y64 : -1;
+    const int uy = yr >= 0 ? yr / U : -1, ey = yr >= 0 ? yr % U : 0;
+    const float inv = (float)(scale / (double)kap);
+    const uint32_t b_inv = encode<T>(inv), b_lab_in = encode<T>(inv - scale_f);
+    const uint32_t b_lab_out = encode<T>(0.0f - scale_f);
+    const rsrc_t out = make_rsrc(static_cast<char*>(grad) + r * (int64_t)row_bytes, row_bytes);
+    if (use_bits && kap <= kTwoPassCap) {
+      const int32_t* ids = cidx + r * (int64_t)kTwoPassCap;
+      for (int p = threadIdx.x; p < kap; p += kBlock) atomicOr(&bits[ids[p] >> 5], 1u << (ids[p] & 31));
+      __syncthreads();
+      for (int u = threadIdx.x; u < units; u += kBlock) {
+        const uint32_t w = bits[(U * u) >> 5] >> ((U * u) & 31);
+        uint32_t g[U];
+#pragma unroll
+        for (int e = 0; e < U; ++e) g[e] = ((w >> e) & 1u) ? b_inv : 0u;
+        if (u == uy) {
+#pragma unroll
+          for (int e = 0; e < U; ++e) g[e] = e == ey ? (((w >> e) & 1u) ? b_lab_in : b_lab_out) : g[e];
+        }
+        store_unit_bits<T, V4>(out, (uint32_t)u, g);
+      }
+      __syncthreads();
+      for (int p = threadIdx.x; p < kap; p += kBlock) bits[ids[p] >> 5] = 0u;
+      __syncthreads();
+    } else {
+      const rsrc_t in = make_rsrc(static_cast<const char*>(z) + r * (int64_t)row_bytes, row_bytes);
+      for (int u = threadIdx.x; u < units; u += kBlock) {
+        float v[U];
+        load_unit<T, V4>(in, (uint32_t)u, v);
+        uint32_t g[U];
+#pragma unroll
+        for (int e = 0; e < U; ++e) g[e] = v[e] > Hf ? b_inv : 0u;
+        if (u == uy) {
+#pragma unroll
+          for (int e = 0; e < U; ++e) g[e] = e == ey ? (v[e] > Hf ? b_lab_in : b_lab_out) : g[e];
+        }
+        store_unit_bits<T, V4>(out, (uint32_t)u, g);
+      }
+    }
   }
 }
 
@@ -2541,6 +2611,30 @@ void launch_block(const void* z, const int64_t* y, int64_t N, int C, const Outs&
   hipLaunchKernelGGL((fwl_block_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
 }
 
+size_t mean_ws_bytes(int64_t N);
+
+// The fused op in two passes: the candidate-list kernel (lists cut at kTwoPassCap, kept in the
+// workspace after the mean's part), then fwl_support_to_grad.
+template <typename T, bool V4>
+void launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, void* ws, hipStream_t s) {
+  char* base = static_cast<char*>(ws) + mean_ws_bytes(N);
+  const size_t L = (size_t)N * kTwoPassCap;
+  Outs o1 = o;
+  o1.cval = reinterpret_cast<float*>(base);
+  o1.cidx = reinterpret_cast<int32_t*>(base + sizeof(float) * L);
+  o1.ccnt = reinterpret_cast<int32_t*>(base + (sizeof(float) + sizeof(int32_t)) * L);
+  float* Hs = reinterpret_cast<float*>(base + (sizeof(float) + sizeof(int32_t)) * L + sizeof(int32_t) * (size_t)N);
+  o1.cstride = kTwoPassCap;
+  o1.ccap = kTwoPassCap;
+  if (o1.H == nullptr) o1.H = Hs;
+  o1.grad = nullptr;
+  launch_block<T, kCand, V4>(z, y, N, C, o1, s);
+  const void* k = reinterpret_cast<const void*>(&fwl_support_to_grad<T, V4>);
+  const int grid = persistent_grid(N, 1, resident_blocks(k), kMaxBlocksRow);
+  hipLaunchKernelGGL((fwl_support_to_grad<T, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, o1.H, o1.ccnt, o1.cidx, N, C,
+                     o.scale, o.scale_f, o.grad);
+}
+
 template <typename T, int MODE, bool V4>
 void launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<T, MODE, V4>);
@@ -2590,6 +2684,23 @@ size_t mean_ws_bytes(int64_t N) {
   const size_t P = (size_t)partial_slots(N);
   const size_t G = (P + kTicketGroup - 1) / kTicketGroup;
   return kWsHeader + sizeof(double) * P + sizeof(double) * G + sizeof(unsigned) * kTicketStride * G;
+}
+
+// Whether the fused op may run in two passes (the long-row block path) under switch `path`.
+// Measured on MI355X (fp32): 8192 x 32000 424 -> 403 us, 2048 x 131072 397 -> 378 us, 520 x
+// 128256 144 -> 133 us; but 4096 x 16384, 6553 x 10000 and 256 x 128256 lost 9-19% (the read pass
+// runs below the read rate there), and bf16 8192 x 32000 lost 23% (its read pass is issue-bound).
+// Automatic dispatch: fp32 rows of >= 32000 elements, >= 512 of them; forced paths 2 and 3 always
+// (their tests exercise both passes in every element type).
+constexpr int64_t kTwoPassMinC = 32000;
+constexpr int64_t kTwoPassMinRows = 512;
+bool two_pass_rows(int64_t N, int64_t C, int64_t elem, int path) {
+  return path == 2 || path == 3 || (path == 0 && elem == 4 && C >= kTwoPassMinC && N >= kTwoPassMinRows);
+}
+
+// the two passes' scratch: cut candidate lists (values, indices), kappa and H per row
+size_t two_pass_bytes(int64_t N) {
+  return (size_t)N * (kTwoPassCap * (sizeof(float) + sizeof(int32_t)) + sizeof(int32_t) + sizeof(float));
 }
 
 size_t split_scratch_bytes(int64_t N, int64_t C) {
@@ -2675,6 +2786,10 @@ int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scal
   } else if (path == 4 || path == 5) {
     if (v4) launch_wave_stream<T, MODE, true>(z, y, N, C, o, s);
     else launch_wave_stream<T, MODE, false>(z, y, N, C, o, s);
+  } else if (MODE == kGrad && two_pass_rows(N, C, kElemBytes<T>, g_path) && ws != nullptr && aligned(ws, 8) &&
+             ws_bytes >= mean_ws_bytes(N) + two_pass_bytes(N)) {
+    if (v4) launch_two_pass<T, true>(z, y, N, C, o, ws, s);
+    else launch_two_pass<T, false>(z, y, N, C, o, ws, s);
   } else {
     if (v4) launch_block<T, MODE, true>(z, y, N, C, o, s);
     else launch_block<T, MODE, false>(z, y, N, C, o, s);
@@ -2721,8 +2836,11 @@ size_t fwl_workspace_bytes(int64_t N, int64_t C) {
   if (N < 0) N = 0;
   // the completion counter, the fp64 partials of the mean, then the split rows' scratch
   size_t b = mean_ws_bytes(N);
-  if (split_rows(N, C, 4, g_path)) b += split_scratch_bytes(N, C);
-  return b;
+  // the split rows' scratch and the two passes' scratch share the space after the mean's part
+  size_t extra = 0;
+  if (split_rows(N, C, 4, g_path)) extra = split_scratch_bytes(N, C);
+  if (two_pass_rows(N, C, 4, g_path) && two_pass_bytes(N) > extra) extra = two_pass_bytes(N);
+  return b + extra;
 }
 
 int fwl_forward_backward(const float* logits, const int64_t* targets, int64_t N, int64_t C,
@@ -2801,6 +2919,8 @@ int fwl_forward_large(const float* logits, const int64_t* targets, int64_t N, in
   o.cval = cand_values;
   o.cidx = cand_indices;
   o.ccnt = cand_counts;
+  o.cstride = (int)(C > 0 && C <= kMaxC ? C : 0);   // whole rows (checked again by forward)
+  o.ccap = o.cstride;
   return forward<float, kCand>(logits, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o, true,
                         workspace, workspace_bytes, stream);
 }

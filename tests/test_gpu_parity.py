@@ -542,3 +542,33 @@ def test_c_abi_direct(ext, dev):
     torch.cuda.synchronize()
     got = {k: (v.cpu().numpy() if v.dim() else float(v.cpu())) for k, v in out.items()}
     assert_parity(got, oracle.definition(z, y), z)
+
+
+@pytest.mark.parametrize("C", [32000, 40000])
+def test_long_rows_one_pass_without_workspace(ext, dev, C):
+    # >= 512 rows of >= 32000 elements run in two passes when the workspace has room; without a
+    # workspace (no mean requested) the one-pass block kernel runs: both against the oracle
+    import ctypes
+    rng = np.random.default_rng(C)
+    N = 520
+    z = rng.standard_normal((N, C)).astype(np.float32)
+    z[::7] *= np.float32(0.01)
+    y = rng.integers(0, C, N)
+    zt, yt = to_dev(dev, z, y)
+    ref = oracle.definition(z, y)
+    L = fwloss_capi.lib()
+    H = torch.empty(N, device=dev)
+    loss = torch.empty(N, device=dev)
+    kappa = torch.empty(N, dtype=torch.int32, device=dev)
+    grad = torch.empty_like(zt)
+    P = ctypes.c_void_p
+    print(f"one pass without workspace C={C}", flush=True)
+    rc = L.fwl_forward_backward(P(zt.data_ptr()), P(yt.data_ptr()), N, C, 1.0 / N, float(N), P(H.data_ptr()),
+                                P(loss.data_ptr()), None, P(kappa.data_ptr()), P(grad.data_ptr()), None, 0,
+                                P(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert_parity(dict(H=H.cpu().numpy(), loss=loss.cpu().numpy(), kappa=kappa.cpu().numpy(),
+                       grad=grad.cpu().numpy()), ref, z)
+    print(f"two passes C={C}", flush=True)
+    assert_parity(fused(ext, zt, yt), ref, z)

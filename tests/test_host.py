@@ -153,7 +153,9 @@ def test_set_params_validation_and_round_trip():
 def test_workspace_sizes():
     """The split-row scratch is counted exactly where the split kernels may run: few rows (<= 128)
     of at least 96 KiB (24576 fp32 elements; the size covers every element type), or rows of any
-    length when path 7 is forced."""
+    length when path 7 is forced; the two-pass scratch where the fused op may run in two passes
+    (>= 512 rows of >= 32000 elements, or path 2/3 forced).  The two share one region (the larger
+    is counted)."""
     L = capi.lib()
     p, c = ctypes.c_int(-1), ctypes.c_int(-1)
     L.fwl_get_params(ctypes.byref(p), ctypes.byref(c))
@@ -163,8 +165,15 @@ def test_workspace_sizes():
         base = L.fwl_workspace_bytes(4096, 1000)
         assert base >= 256 + 8 * 4096
         assert L.fwl_workspace_bytes(16, 1000) == base           # short rows: no scratch
-        assert L.fwl_workspace_bytes(2048, 131072) == base       # many rows: no scratch
+        assert L.fwl_workspace_bytes(65536, 8192) == base
         assert L.fwl_workspace_bytes(0, 131072) == base
+        # >= 512 rows of >= 32000 elements run the fused op in two passes: per row 64 support
+        # values and indices, kappa and H
+        row = 64 * 8 + 4 + 4
+        assert L.fwl_workspace_bytes(2048, 131072) - base == 2048 * row
+        assert L.fwl_workspace_bytes(512, 32000) - base == 512 * row
+        assert L.fwl_workspace_bytes(511, 32000) == base
+        assert L.fwl_workspace_bytes(65536, 31999) == base
         assert L.fwl_workspace_bytes(129, 24576) == base
         assert L.fwl_workspace_bytes(128, 24575) == base
         # (row, chunk) items: about 1024 in all, chunks of at least 4096 elements, <= 256 per row;
@@ -175,6 +184,8 @@ def test_workspace_sizes():
         assert L.fwl_workspace_bytes(1, 2 ** 29) - base == 1 * 256 * item
         assert L.fwl_workspace_bytes(128, 24576) - base == 128 * 6 * item
         assert L.fwl_workspace_bytes(100, 40000) - base == 100 * 10 * item
+        L.fwl_set_params(2, 512)                                  # forced block path: two passes
+        assert L.fwl_workspace_bytes(16, 1000) - base == 16 * row
         L.fwl_set_params(7, 512)
         assert L.fwl_workspace_bytes(16, 1000) - base == 16 * 1 * item
         assert L.fwl_workspace_bytes(4, 30000) - base == 4 * 8 * item
