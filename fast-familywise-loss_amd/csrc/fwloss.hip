@@ -1448,9 +1448,16 @@ __device__ __forceinline__ bool scan_round(Round<T, VEC>& a, int round, int C, i
 // and every output element gets its zero placeholder.  Returns false if the list overflowed.
 // (`out_row`: the row's dense output -- gradient or mask -- or null in candidate-list mode; a
 // stretch of a row streams the same way, with `row`, `out_row` and C narrowed to it)
+// the first round of a row (or stretch), loaded ahead of stream_span (C = 0: no row, no traffic)
+template <int W, typename T, bool VEC>
+__device__ __forceinline__ void stream_first(const void* __restrict__ row, int C, int lane, int wid, Round<T, VEC>& a) {
+  load_round<W, T, VEC>(make_rsrc(row, (uint32_t)(kElemBytes<T> * C)), 0, wid, lane, a);
+}
+
+// (`a` holds the span's first round, from stream_first)
 template <int W, typename T, int MODE, bool VEC>
 __device__ __forceinline__ bool stream_span(const void* __restrict__ row, void* out_row, int C, int lane, int wid, float* bv,
-                            int* bi, int cap, int& n, float& m, float& t) {
+                            int* bi, int cap, int& n, float& m, float& t, Round<T, VEC>& a) {
   constexpr int per_round = kWave * W * Round<T, VEC>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
@@ -1458,8 +1465,7 @@ __device__ __forceinline__ bool stream_span(const void* __restrict__ row, void* 
   rsrc_t out = make_rsrc(nullptr, 0u);
   if constexpr (MODE == kGrad) out = make_rsrc(out_row, row_bytes);
   else if constexpr (MODE == kMask) out = make_rsrc(out_row, (uint32_t)C);
-  Round<T, VEC> a, b;
-  load_round<W, T, VEC>(in, 0, wid, lane, a);
+  Round<T, VEC> b;
   // stores to a zero-size resource (no traffic) so that the wait counts on entry match those of
   // the loop's back edge (a round's loads, then a round's stores)
   __builtin_amdgcn_sched_barrier(0);
@@ -1480,12 +1486,12 @@ __device__ __forceinline__ bool stream_span(const void* __restrict__ row, void* 
 }
 
 template <int W, typename T, int MODE, bool VEC>
-__device__ bool stream_row(const void* __restrict__ row, int64_t r, int C, int lane, int wid, float* bv,
-                           int* bi, const Outs& o, int& n, float& m, float& t) {
+__device__ __forceinline__ bool stream_row(const void* __restrict__ row, int64_t r, int C, int lane, int wid, float* bv,
+                           int* bi, const Outs& o, int& n, float& m, float& t, Round<T, VEC>& a) {
   void* out_row = nullptr;
   if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
   else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-  return stream_span<W, T, MODE, VEC>(row, out_row, C, lane, wid, bv, bi, o.cap, n, m, t);
+  return stream_span<W, T, MODE, VEC>(row, out_row, C, lane, wid, bv, bi, o.cap, n, m, t, a);
 }
 
 // block-wide fp64 sum and count of the row entries > thr (fixed order)
@@ -1685,8 +1691,13 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
   double bsum = 0.0;
+  auto row_at = [&](int64_t rr) { return static_cast<const char*>(z) + rr * (int64_t)C * kElemBytes<T>; };
+  // the first round of the next row is loaded before this row is resolved, so that the stream of
+  // every row after the first starts with its loads in flight
+  Round<T, V4> first;
+  if (blockIdx.x < N) stream_first<kWavesPerBlock, T, V4>(row_at(blockIdx.x), o.force_generic ? 0 : C, lane, wid, first);
   for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
-    const void* row = static_cast<const char*>(z) + r * (int64_t)C * kElemBytes<T>;
+    const void* row = row_at(r);
     const int64_t y64 = tgt[r];
     const bool yok = y64 >= 0 && y64 < C;
     const int yr = yok ? (int)y64 : -1;
@@ -1696,14 +1707,18 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
     int n = 0;
     float m = -INFINITY, t = -INFINITY;
     bool ok = !o.force_generic;
-    if (ok) ok = stream_row<kWavesPerBlock, T, MODE, V4>(row, r, C, lane, wid, bv, bi, o, n, m, t);
+    if (ok) ok = stream_row<kWavesPerBlock, T, MODE, V4>(row, r, C, lane, wid, bv, bi, o, n, m, t, first);
     if (lane == 0) {
       sh.wmax[wid] = m;
       sh.wn[wid] = n;
       sh.ovf[wid] = !ok;
     }
-    // every wavefront's zero placeholders have landed before any support entry is rewritten
-    wait_vmem();
+    const int64_t rn = r + gridDim.x;
+    if constexpr (MODE == kGrad || MODE == kMask) {
+      // every wavefront's zero placeholders have landed before any support entry is rewritten
+      wait_vmem();
+    }
+    if (rn < N && !o.force_generic) stream_first<kWavesPerBlock, T, V4>(row_at(rn), C, lane, wid, first);
     __syncthreads();
     const bool overflow = sh.ovf[0] | sh.ovf[1] | sh.ovf[2] | sh.ovf[3];
 
@@ -1851,9 +1866,13 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
   float my_H = 0.0f, my_loss = 0.0f;
   int my_kappa = 0;
   double lsum = 0.0;
+  auto row_at = [&](int k) { return static_cast<const char*>(z) + (w + (int64_t)k * stride) * C * kElemBytes<T>; };
+  // the next row's first round is loaded before this row is resolved (see fwl_block_rows)
+  Round<T, V4> first;
+  if (nrows > 0) stream_first<1, T, V4>(row_at(0), o.force_generic ? 0 : C, lane, 0, first);
   for (int k = 0; k < nrows; ++k) {
     const int64_t r = w + (int64_t)k * stride;
-    const void* row = static_cast<const char*>(z) + r * (int64_t)C * kElemBytes<T>;
+    const void* row = row_at(k);
     const int64_t y64 = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
                         (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
     const bool yok = y64 >= 0 && y64 < C;
@@ -1861,7 +1880,8 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
 
     int n = 0;
     float m = -INFINITY, t = -INFINITY;
-    const bool ok = !o.force_generic && stream_row<1, T, MODE, V4>(row, r, C, lane, 0, bv, bi, o, n, m, t);
+    const bool ok = !o.force_generic && stream_row<1, T, MODE, V4>(row, r, C, lane, 0, bv, bi, o, n, m, t, first);
+    if (k + 1 < nrows && !o.force_generic) stream_first<1, T, V4>(row_at(k + 1), C, lane, 0, first);
     double tau;
     int kappa;
     uint64_t support = 0;
@@ -2010,8 +2030,10 @@ __global__ __launch_bounds__(kBlock) void fwl_split_chunks(const void* __restric
     int* bi = sh.bidx[wid];
     int n = 0;
     float m = -INFINITY, t = -INFINITY;
+    Round<T, V4> first;
+    if (!o.force_generic) stream_first<kWavesPerBlock, T, V4>(span, len, lane, wid, first);
     const bool ok = !o.force_generic &&
-                    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, n, m, t);
+                    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, n, m, t, first);
     if (lane == 0) {
       sh.wmax[wid] = m;
       sh.wn[wid] = n;
