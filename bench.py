@@ -56,6 +56,8 @@ def parse():
     ap.add_argument("--dtype", default="f32", choices=["f32", "bf16", "f16"],
                     help="element type of the logits and the gradient (decisions are fp32/fp64)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-two-op", action="store_true",
+                    help="skip the timing of the reference harness's two-op sequence (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--copy-probe", action="store_true",
                     help="time a plain 1 GiB device copy instead (calibrates rocprof byte counters)")
@@ -189,7 +191,7 @@ def main():
         H, losses, mean, kappa, cb, ci, cc = fwloss.fw_forward(zt, yt)
         return fwloss.fw_backward(zt, yt, H, kappa, cb, ci, cc)
     two_op_ms = None
-    if args.dtype == "f32":
+    if args.dtype == "f32" and not args.no_two_op:
         for i in range(5):
             two_op(i)
         torch.cuda.synchronize()
@@ -203,6 +205,8 @@ def main():
     unit = 16 // ELEM_BYTES[args.dtype]
     if N <= 128 and C * ELEM_BYTES[args.dtype] >= 96 * 1024:
         tag = "fwl_split_chunks"
+    elif args.dtype == "f32" and N >= 512 and C >= 32000:
+        tag = "fwl_two_pass"      # fwl_block_rows (candidate lists) + fwl_support_to_grad
     elif C % unit == 0 and C // unit <= 64:
         tag = "fwl_seg_rows"
     else:

@@ -143,17 +143,19 @@ __device__ __forceinline__ uint32_t encode(float f) {
 }
 
 // store unit `u` from already-encoded element bit patterns
-template <typename T, bool VEC>
+// (POL: cache policy; the non-temporal hint suits streams that read and write, a pure write
+// stream runs faster without it)
+template <typename T, bool VEC, int POL = kNonTemporal>
 __device__ __forceinline__ void store_unit_bits(rsrc_t r, uint32_t u, const uint32_t* b) {
   if constexpr (VEC) {
     v4u w;
     if constexpr (std::is_same<T, float>::value) w = v4u{b[0], b[1], b[2], b[3]};
     else w = v4u{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
-    __builtin_amdgcn_raw_buffer_store_b128(w, r, 16u * u, 0, kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, 16u * u, 0, POL);
   } else if constexpr (std::is_same<T, float>::value) {
-    __builtin_amdgcn_raw_buffer_store_b32(b[0], r, 4u * u, 0, kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b32(b[0], r, 4u * u, 0, POL);
   } else {
-    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)b[0], r, 2u * u, 0, kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)b[0], r, 2u * u, 0, POL);
   }
 }
 
@@ -2375,26 +2377,29 @@ __global__ __launch_bounds__(kBlock) void fwl_cand_to_grad(
 // Second pass of the fused op for long rows.  A read pass over the logits (the candidate-list
 // kernel, with its lists cut at kTwoPassCap entries in the workspace) leaves every row's H, kappa
 // and support; this kernel then writes the dense gradient, each 128-bit unit once with its final
-// value, from an LDS bitmap of the row's support.  Rows whose support exceeds the list, and rows
-// longer than the bitmap, are recomputed from the logits (z > H).  Separating the read stream
-// from the write stream lets each run at its own rate instead of interleaving them.
+// value.  The work is flat: item i is chunk i % nch of row i / nch (kSupportUnits units per thread),
+// and the blocks of a grid-stride loop take consecutive items, so the writes in flight at any time
+// cover one narrow window of memory, as in a fill.  A row's support indices arrive one per lane
+// and are broadcast in turn; each thread marks the ones that fall into its units.  Rows whose
+// support exceeds the list are recomputed from the logits (z > H).  The stores carry no
+// non-temporal hint: measured at 8192 x 32000, 202 us with it, 174 us without.
 constexpr int kTwoPassCap = 64;          // support entries kept per row between the passes
-constexpr int kBitmapBits = 1 << 18;     // longest row with an LDS bitmap (32 KB)
+constexpr int kSupportUnits = 4;         // 128-bit units per thread per item
 
 template <typename T, bool V4>
 __global__ __launch_bounds__(kBlock) void fwl_support_to_grad(
     const void* __restrict__ z, const int64_t* __restrict__ tgt, const float* __restrict__ Hin,
-    const int32_t* __restrict__ kap_in, const int32_t* __restrict__ cidx, int64_t N, int C, double scale,
-    float scale_f, void* __restrict__ grad) {
+    const int32_t* __restrict__ kap_in, const int32_t* __restrict__ cidx, int64_t N, int C, int nch,
+    double scale, float scale_f, void* __restrict__ grad) {
   constexpr int U = kUnit<T, V4>;
-  __shared__ uint32_t bits[kBitmapBits / 32];
-  const bool use_bits = C <= kBitmapBits;
-  if (use_bits)
-    for (int i = threadIdx.x; i < (C + 31) / 32; i += kBlock) bits[i] = 0u;
-  __syncthreads();
-  const int units = (C + U - 1) / U;
+  constexpr int kChunkUnits = kBlock * kSupportUnits;
+  const int lane = lane_id();
+  const int t = (int)threadIdx.x;
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
-  for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
+  const int64_t items = N * (int64_t)nch;
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const int64_t r = it / nch;
+    const int u0 = (int)(it - r * nch) * kChunkUnits;   // first unit of the chunk
     const int kap = kap_in[r];
     const float Hf = Hin[r];
     const int64_t y64 = tgt[r];
@@ -2404,27 +2409,37 @@ __global__ __launch_bounds__(kBlock) void fwl_support_to_grad(
     const uint32_t b_inv = encode<T>(inv), b_lab_in = encode<T>(inv - scale_f);
     const uint32_t b_lab_out = encode<T>(0.0f - scale_f);
     const rsrc_t out = make_rsrc(static_cast<char*>(grad) + r * (int64_t)row_bytes, row_bytes);
-    if (use_bits && kap <= kTwoPassCap) {
-      const int32_t* ids = cidx + r * (int64_t)kTwoPassCap;
-      for (int p = threadIdx.x; p < kap; p += kBlock) atomicOr(&bits[ids[p] >> 5], 1u << (ids[p] & 31));
-      __syncthreads();
-      for (int u = threadIdx.x; u < units; u += kBlock) {
-        const uint32_t w = bits[(U * u) >> 5] >> ((U * u) & 31);
+    if (kap <= kTwoPassCap) {
+      const int my_id = lane < kap ? cidx[r * (int64_t)kTwoPassCap + lane] : -1;
+      uint32_t sel[kSupportUnits];
+#pragma unroll
+      for (int j = 0; j < kSupportUnits; ++j) sel[j] = 0u;
+      for (int p = 0; p < kap; ++p) {
+        const int id = __builtin_amdgcn_readlane(my_id, p);
+        const int d = id / U - u0;   // unit of the entry, relative to the chunk (uniform)
+        if (d >= 0 && d < kChunkUnits && t == d % kBlock) {
+#pragma unroll
+          for (int j = 0; j < kSupportUnits; ++j)
+            if (j == d / kBlock) sel[j] |= 1u << (id % U);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kSupportUnits; ++j) {
+        const int u = u0 + t + kBlock * j;
         uint32_t g[U];
 #pragma unroll
-        for (int e = 0; e < U; ++e) g[e] = ((w >> e) & 1u) ? b_inv : 0u;
+        for (int e = 0; e < U; ++e) g[e] = ((sel[j] >> e) & 1u) ? b_inv : 0u;
         if (u == uy) {
 #pragma unroll
-          for (int e = 0; e < U; ++e) g[e] = e == ey ? (((w >> e) & 1u) ? b_lab_in : b_lab_out) : g[e];
+          for (int e = 0; e < U; ++e) g[e] = e == ey ? (((sel[j] >> e) & 1u) ? b_lab_in : b_lab_out) : g[e];
         }
-        store_unit_bits<T, V4>(out, (uint32_t)u, g);
+        store_unit_bits<T, V4, 0>(out, (uint32_t)u, g);   // units past the row end are dropped
       }
-      __syncthreads();
-      for (int p = threadIdx.x; p < kap; p += kBlock) bits[ids[p] >> 5] = 0u;
-      __syncthreads();
     } else {
       const rsrc_t in = make_rsrc(static_cast<const char*>(z) + r * (int64_t)row_bytes, row_bytes);
-      for (int u = threadIdx.x; u < units; u += kBlock) {
+#pragma unroll
+      for (int j = 0; j < kSupportUnits; ++j) {
+        const int u = u0 + t + kBlock * j;
         float v[U];
         load_unit<T, V4>(in, (uint32_t)u, v);
         uint32_t g[U];
@@ -2434,7 +2449,7 @@ __global__ __launch_bounds__(kBlock) void fwl_support_to_grad(
 #pragma unroll
           for (int e = 0; e < U; ++e) g[e] = e == ey ? (v[e] > Hf ? b_lab_in : b_lab_out) : g[e];
         }
-        store_unit_bits<T, V4>(out, (uint32_t)u, g);
+        store_unit_bits<T, V4, 0>(out, (uint32_t)u, g);
       }
     }
   }
@@ -2651,10 +2666,14 @@ void launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Ou
   if (o1.H == nullptr) o1.H = Hs;
   o1.grad = nullptr;
   launch_block<T, kCand, V4>(z, y, N, C, o1, s);
-  const void* k = reinterpret_cast<const void*>(&fwl_support_to_grad<T, V4>);
-  const int grid = persistent_grid(N, 1, resident_blocks(k), kMaxBlocksRow);
+  constexpr int kChunk = kBlock * kSupportUnits * kUnit<T, V4>;   // elements per item
+  const int nch = (int)((C + kChunk - 1) / kChunk);
+  // one item per block (dispatched in order; measured at 8192 x 32000: 193 us against 202 us
+  // with a resident grid looping over the items)
+  const int64_t items = N * (int64_t)nch;
+  const int grid = (int)(items < (1 << 30) ? items : (1 << 30));
   hipLaunchKernelGGL((fwl_support_to_grad<T, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, o1.H, o1.ccnt, o1.cidx, N, C,
-                     o.scale, o.scale_f, o.grad);
+                     nch, o.scale, o.scale_f, o.grad);
 }
 
 template <typename T, int MODE, bool V4>
