@@ -205,7 +205,7 @@ def main():
     unit = 16 // ELEM_BYTES[args.dtype]
     if N <= 128 and C * ELEM_BYTES[args.dtype] >= 96 * 1024:
         tag = "fwl_split_chunks"
-    elif args.dtype == "f32" and N >= 512 and C >= 32000:
+    elif (args.dtype == "f32" and N >= 384 and C >= 32000) or (N >= 512 and C >= 65536):
         tag = "fwl_two_pass"      # fwl_block_rows (candidate lists) + fwl_support_to_grad
     elif C % unit == 0 and C // unit <= 64:
         tag = "fwl_seg_rows"

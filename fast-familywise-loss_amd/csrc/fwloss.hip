@@ -2728,15 +2728,21 @@ size_t mean_ws_bytes(int64_t N) {
 }
 
 // Whether the fused op may run in two passes (the long-row block path) under switch `path`.
-// Measured on MI355X (fp32): 8192 x 32000 424 -> 403 us, 2048 x 131072 397 -> 378 us, 520 x
-// 128256 144 -> 133 us; but 4096 x 16384, 6553 x 10000 and 256 x 128256 lost 9-19% (the read pass
-// runs below the read rate there), and bf16 8192 x 32000 lost 23% (its read pass is issue-bound).
-// Automatic dispatch: fp32 rows of >= 32000 elements, >= 512 of them; forced paths 2 and 3 always
-// (their tests exercise both passes in every element type).
+// Measured on MI355X against one pass (fp32): 8192 x 32000 423 -> 400 us, 2048 x 131072 378 ->
+// 357 us, 520 x 128256 132 -> 118 us, 400 x 50257 50.5 -> 46.8 us; but 256 x 128256 67 -> 79 us,
+// 6553 x 10000 119 -> 129 us, 4096 x 16384 110 -> 115 us and 3000 x 20000 102 -> 106 us (the read
+// pass runs below the read rate there).  bf16: 2048 x 131072 218 -> 190 us, but 8192 x 32000
+// 228 -> 264 us (its read pass is issue-bound at that length).  Automatic dispatch: rows of
+// >= 32000 elements, >= 384 of them, in fp32; rows of >= 65536 elements, >= 512 of them, in 16
+// bits.  Forced paths 2 and 3 always (their tests exercise both passes in every element type).
 constexpr int64_t kTwoPassMinC = 32000;
-constexpr int64_t kTwoPassMinRows = 512;
+constexpr int64_t kTwoPassMinRows = 384;
+constexpr int64_t kTwoPassMinC16 = 65536;
+constexpr int64_t kTwoPassMinRows16 = 512;
 bool two_pass_rows(int64_t N, int64_t C, int64_t elem, int path) {
-  return path == 2 || path == 3 || (path == 0 && elem == 4 && C >= kTwoPassMinC && N >= kTwoPassMinRows);
+  if (path == 2 || path == 3) return true;
+  if (path != 0) return false;
+  return elem == 4 ? (C >= kTwoPassMinC && N >= kTwoPassMinRows) : (C >= kTwoPassMinC16 && N >= kTwoPassMinRows16);
 }
 
 // the two passes' scratch: cut candidate lists (values, indices), kappa and H per row

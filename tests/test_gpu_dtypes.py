@@ -82,6 +82,14 @@ def test_dtype_split_rows(ext, dev, reset_params16, name, N, C, path):
 
 
 @pytest.mark.parametrize("name", sorted(DTYPES))
+def test_dtype_two_pass(ext, dev, name):
+    # >= 512 16-bit rows of >= 65536 elements: the fused op in two passes (read, then write)
+    z16, y = case(65536, 512, 21, DTYPES[name])
+    print(f"{name} two passes N=512 C=65536", flush=True)
+    check(ext, dev, z16, y)
+
+
+@pytest.mark.parametrize("name", sorted(DTYPES))
 @pytest.mark.parametrize("K", [3, 100, 1000, 40000])
 def test_dtype_row_families(ext, dev, name, K):
     # every row family, rounded to the 16-bit dtype (which adds many exact ties)

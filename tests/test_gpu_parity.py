@@ -546,7 +546,7 @@ def test_c_abi_direct(ext, dev):
 
 @pytest.mark.parametrize("C", [32000, 40000])
 def test_long_rows_one_pass_without_workspace(ext, dev, C):
-    # >= 512 rows of >= 32000 elements run in two passes when the workspace has room; without a
+    # >= 384 rows of >= 32000 elements run in two passes when the workspace has room; without a
     # workspace (no mean requested) the one-pass block kernel runs: both against the oracle
     import ctypes
     rng = np.random.default_rng(C)

@@ -154,7 +154,7 @@ def test_workspace_sizes():
     """The split-row scratch is counted exactly where the split kernels may run: few rows (<= 128)
     of at least 96 KiB (24576 fp32 elements; the size covers every element type), or rows of any
     length when path 7 is forced; the two-pass scratch where the fused op may run in two passes
-    (>= 512 rows of >= 32000 elements, or path 2/3 forced).  The two share one region (the larger
+    (>= 384 rows of >= 32000 elements, or path 2/3 forced).  The two share one region (the larger
     is counted)."""
     L = capi.lib()
     p, c = ctypes.c_int(-1), ctypes.c_int(-1)
@@ -167,12 +167,12 @@ def test_workspace_sizes():
         assert L.fwl_workspace_bytes(16, 1000) == base           # short rows: no scratch
         assert L.fwl_workspace_bytes(65536, 8192) == base
         assert L.fwl_workspace_bytes(0, 131072) == base
-        # >= 512 rows of >= 32000 elements run the fused op in two passes: per row 64 support
-        # values and indices, kappa and H
+        # >= 384 rows of >= 32000 elements (the fp32 rule, which covers the 16-bit one) run the
+        # fused op in two passes: per row 64 support values and indices, kappa and H
         row = 64 * 8 + 4 + 4
         assert L.fwl_workspace_bytes(2048, 131072) - base == 2048 * row
-        assert L.fwl_workspace_bytes(512, 32000) - base == 512 * row
-        assert L.fwl_workspace_bytes(511, 32000) == base
+        assert L.fwl_workspace_bytes(384, 32000) - base == 384 * row
+        assert L.fwl_workspace_bytes(383, 32000) == base
         assert L.fwl_workspace_bytes(65536, 31999) == base
         assert L.fwl_workspace_bytes(129, 24576) == base
         assert L.fwl_workspace_bytes(128, 24575) == base
