@@ -2648,6 +2648,13 @@ void launch_block(const void* z, const int64_t* y, int64_t N, int C, const Outs&
   hipLaunchKernelGGL((fwl_block_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
 }
 
+template <typename T, int MODE, bool V4>
+void launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+  const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<T, MODE, V4>);
+  const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
+  hipLaunchKernelGGL((fwl_wave_stream_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+}
+
 size_t mean_ws_bytes(int64_t N);
 
 // The fused op in two passes: the candidate-list kernel (lists cut at kTwoPassCap, kept in the
@@ -2665,7 +2672,11 @@ void launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Ou
   o1.ccap = kTwoPassCap;
   if (o1.H == nullptr) o1.H = Hs;
   o1.grad = nullptr;
-  launch_block<T, kCand, V4>(z, y, N, C, o1, s);
+  // The read pass streams one row per wavefront when there are rows for two wavefronts per SIMD
+  // (8192 x 32000: 178 us against 206 us with one block per row; 2048 x 131072: equal), else one
+  // row per block (520 x 128256: 181 us with one row per wavefront, 119 us per block).
+  if (N >= 2 * 4 * (int64_t)device_cus()) launch_wave_stream<T, kCand, V4>(z, y, N, C, o1, s);
+  else launch_block<T, kCand, V4>(z, y, N, C, o1, s);
   constexpr int kChunk = kBlock * kSupportUnits * kUnit<T, V4>;   // elements per item
   const int nch = (int)((C + kChunk - 1) / kChunk);
   // one item per block (dispatched in order; measured at 8192 x 32000: 193 us against 202 us
@@ -2676,12 +2687,6 @@ void launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Ou
                      nch, o.scale, o.scale_f, o.grad);
 }
 
-template <typename T, int MODE, bool V4>
-void launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
-  const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<T, MODE, V4>);
-  const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
-  hipLaunchKernelGGL((fwl_wave_stream_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
-}
 
 // Split rows: chunks of whole streaming rounds (`round` elements; 16-byte aligned whenever the
 // row is), about kSplitTargetItems (row, chunk) items in all, at most kSplitMaxChunks per row.
