@@ -2256,6 +2256,8 @@ __global__ __launch_bounds__(kBlock) void fwl_split_finish(const void* __restric
 // two-op backward kernels of the drop-in interface
 
 // grad = (mask ? inv : 0) - [j == y] * scale, one wavefront per row (rows w + k*stride, k < 64).
+// The gradient stores carry no non-temporal hint (measured at cfg2, two-op sequence 132 -> 118 us;
+// the mask loads keep it).
 // The wavefront's rows form one sequence of rounds (kMaskSlots mask units per lane, a unit being 4
 // mask bytes and 16 gradient bytes, or 1 and 4 for rows that are not 16-byte aligned); the mask
 // loads of the next round are issued before the gradient stores of the current one.
@@ -2284,11 +2286,11 @@ __device__ __forceinline__ void mask_round_store(rsrc_t g, int round, int lane, 
         const bool sel = ((mk[u] >> (8 * e)) & 0xFFu) != 0u;
         w[e] = 4 * q + e == yr ? (sel ? b_lab_in : b_lab_out) : (sel ? b_inv : 0u);
       }
-      __builtin_amdgcn_raw_buffer_store_b128(v4u{w[0], w[1], w[2], w[3]}, g, 16u * (uint32_t)q, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(v4u{w[0], w[1], w[2], w[3]}, g, 16u * (uint32_t)q, 0, 0);
     } else {
       const bool sel = (mk[u] & 0xFFu) != 0u;
       const uint32_t w = q == yr ? (sel ? b_lab_in : b_lab_out) : (sel ? b_inv : 0u);
-      __builtin_amdgcn_raw_buffer_store_b32(w, g, 4u * (uint32_t)q, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b32(w, g, 4u * (uint32_t)q, 0, 0);
     }
   }
 }
