@@ -82,6 +82,27 @@ def test_dtype_split_rows(ext, dev, reset_params16, name, N, C, path):
 
 
 @pytest.mark.parametrize("name", sorted(DTYPES))
+@pytest.mark.parametrize("N,C,last", [(3, 999, "free"), (5, 7, "label"), (7, 33, "support"), (1, 1, "label")])
+def test_dtype_two_pass_odd_sizes(ext, dev, reset_params16, name, N, C, last):
+    # forced two passes with a 16-bit gradient of an odd number of elements: the zero fill writes
+    # whole dwords, the last element comes from the scatter (as a free entry, the label, or a
+    # support entry)
+    z16, y = case(C, N, N * 100 + C, DTYPES[name])
+    if last == "label":
+        y[-1] = C - 1
+    elif last == "support":
+        z = z16.float()
+        z[-1, -1] = z[-1].max() + 2.0     # the row's only support entry
+        z16 = z.to(DTYPES[name])
+        y[-1] = 0
+    else:
+        y[-1] = 0
+    print(f"{name} two passes odd N={N} C={C} last={last}", flush=True)
+    ext.set_params(2, 512)
+    check(ext, dev, z16, y)
+
+
+@pytest.mark.parametrize("name", sorted(DTYPES))
 def test_dtype_two_pass(ext, dev, name):
     # >= 512 16-bit rows of >= 65536 elements: the fused op in two passes (read, then write)
     z16, y = case(65536, 512, 21, DTYPES[name])
