@@ -444,11 +444,13 @@ def test_large_batches(ext, dev, N, C):
 
 # ---------------------------------------------------------------- graphs and streams
 
-def test_graph_capture_replays(ext, dev):
-    """The fused op allocates nothing on the device path and leaves its workspace zeroed, so it can be
-    captured in a HIP graph: every replay must equal the eager result (the mean's ticket counter
-    resets inside the kernel)."""
-    z, y = data.make("cfg2", N=1000, seed=21)
+@pytest.mark.parametrize("cfg,N", [("cfg2", 1000), ("cfg3", 1000), ("cfg4", 512), ("cfg5", 16)])
+def test_graph_capture_replays(ext, dev, cfg, N):
+    """The fused op allocates nothing on the device path and returns its workspace counters to
+    zero, so it can be captured in a HIP graph: every replay must equal the eager result (the
+    mean's tickets reset inside the kernels).  The shapes take the register, segmented, two-pass
+    (read, fill, scatter) and split-row paths."""
+    z, y = data.make(cfg, N=N, seed=21)
     zt, yt = to_dev(dev, z, y)
     eager = ext.fw_forward_backward(zt, yt)
     torch.cuda.synchronize()
@@ -462,7 +464,7 @@ def test_graph_capture_replays(ext, dev):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         out = ext.fw_forward_backward(zt, yt)
-    print("graph replays", flush=True)
+    print(f"graph replays {cfg} N={N}", flush=True)
     for it in range(5):
         g.replay()
         torch.cuda.synchronize()
