@@ -75,14 +75,27 @@ def traffic_for(kernel_tag, cfg):
     return int(m.group(1)) if m else None
 
 
+def _median_time(call, seconds, min_calls):
+    call()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < min_calls or (time.perf_counter() < t_end and len(times) < 5000):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
 def cpu_baseline(z_np, y_np, seconds):
-    """Time the reference CPU path (oracle/_ref) or the C restatement on the same inputs."""
+    """Time the reference CPU path (oracle/_ref) or the C restatement on the same inputs, on all
+    of torch's threads and then on one thread (a shorter sample)."""
     import numpy as np
     import torch
     import oracle
     N, C = z_np.shape
     threads = torch.get_num_threads()
     ref = oracle.load_ref()
+    nthreads = [threads]
     if ref is not None:
         Z = torch.from_numpy(z_np)
         Y = torch.from_numpy(y_np)
@@ -95,20 +108,22 @@ def cpu_baseline(z_np, y_np, seconds):
         kind, label = "reference", f"oracle/_ref {oracle.ref_variant()} (src/cpu/fw_cpu.cpp)"
     else:
         def call():
-            return oracle.single_pass(z_np, y_np, scale=1.0, nthreads=threads)
+            return oracle.single_pass(z_np, y_np, scale=1.0, nthreads=nthreads[0])
         kind, label = "port", "oracle/fwl_oracle.c fwo_single_pass"
-    call()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 5000):
-        t0 = time.perf_counter()
-        call()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    med, times = _median_time(call, seconds, 10)
+    # one thread: the reference splits rows with at::parallel_for, which follows torch's thread count
+    torch.set_num_threads(1)
+    nthreads[0] = 1
+    try:
+        med1, times1 = _median_time(call, seconds / 3, 3)
+    finally:
+        torch.set_num_threads(threads)
     return {"value": N / med, "unit": "rows/s", "cores": threads, "kind": kind,
             "sample": f"{label}: full {N}x{C} batch, loss + dense gradient per call, median of {len(times)} "
                       f"calls ({sum(times):.1f} s of CPU work), {threads} threads",
-            "ms_per_call": med * 1e3, "gbps": alg_bytes(N, C) / med / 1e9}
+            "ms_per_call": med * 1e3, "gbps": alg_bytes(N, C) / med / 1e9,
+            "one_thread": {"value": N / med1, "unit": "rows/s", "ms_per_call": med1 * 1e3,
+                           "sample": f"median of {len(times1)} calls ({sum(times1):.1f} s), 1 thread"}}
 
 
 def copy_probe(args):
