@@ -8,8 +8,9 @@ configuration N=65536, C=1000 fp32 (logits N(0,1), labels uniform).  Input/outpu
 rotated between steps so the 256 MB Infinity Cache cannot hold a step's data from the previous use.
 
 Prints one JSON line.  ``roofline.achieved`` = algorithmic bytes per launch (read logits once,
-write the gradient once, read labels, write H/loss/kappa: 8*N*C + 20*N bytes) / the kernel's mean
-duration measured with HIP events on the stream the kernel runs on.  ``roofline.traffic`` is the
+write the gradient once, read labels, write H/loss/kappa: 8*N*C + 20*N bytes) / the mean duration
+of a launch, measured with one HIP event pair around the timed region on the stream the kernels run
+on (region GPU time / K).  ``roofline.traffic`` is the
 HBM bytes per launch measured with rocprofv3 counters (profiles/<kernel>_<config>.md), or null.
 ``cpu_baseline`` times the reference's own CPU path (compiled into oracle/_ref) on this host's cores,
 on the same host-generated inputs, as loss + full gradient per call (benchmarks/cpu_benchmarks/
@@ -178,20 +179,23 @@ def main():
         out = step(i)
     del out
     torch.cuda.synchronize()
+    # One HIP event pair on the launch stream brackets the K launches: their mean duration is the
+    # GPU time of the region / K, gaps between launches included.  (An event pair around every
+    # launch adds about 7 us per step at cfg2 on MI355X: the event markers serialise the queue.)
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     keep = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record(stream)
     for i in range(args.steps):
-        ev[i][0].record(stream)
         o = step(i)
-        ev[i][1].record(stream)
         keep.append(o[1])  # hold the losses so the allocator cannot reuse them within the region
         del o
+    ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    kern_ms = ev0.elapsed_time(ev1) / args.steps
     ms_per_step = wall * 1e3 / args.steps
     nbytes = alg_bytes(N, C, ELEM_BYTES[args.dtype])
     achieved = nbytes / (kern_ms * 1e-3) / 1e9
