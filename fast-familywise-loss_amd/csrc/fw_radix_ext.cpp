@@ -227,6 +227,111 @@ at::Tensor fw_scale_grad(at::Tensor grad, at::Tensor grad_output) {
   return grad;
 }
 
+// ---- the linear layer fused with the loss (logits = hidden @ weight^T, one vocabulary chunk at a
+// time; no counterpart in the reference, whose ops take materialised logits)
+
+// per-row state for a batch of N rows, initialised
+at::Tensor fw_linear_state(at::Tensor like, int64_t N) {
+  TORCH_CHECK(like.is_cuda(), "fw_linear_state: like must be a CUDA tensor");
+  c10::DeviceGuard guard(like.device());
+  at::Tensor st = torch::empty({(int64_t)fwl_linear_state_bytes(N) + 16}, like.options().dtype(torch::kUInt8));
+  check_status(fwl_linear_begin(st.data_ptr(), N, current_stream(like)), "fw_linear_state");
+  return st;
+}
+
+// merge the chunk logits [N, Vc] (columns v0 .. v0 + Vc - 1) into the state
+void fw_linear_chunk(at::Tensor state, at::Tensor logits, at::Tensor targets, int64_t v0, int64_t V) {
+  TORCH_CHECK(logits.is_cuda() && logits.dim() == 2, "logits chunk must be a CUDA tensor [N, Vc]");
+  c10::DeviceGuard guard(logits.device());
+  check_rows(targets, logits, torch::kInt64, "targets");
+  TORCH_CHECK(state.device() == logits.device() && state.scalar_type() == torch::kUInt8 &&
+                  (size_t)state.numel() >= fwl_linear_state_bytes(logits.size(0)),
+              "state must come from fw_linear_state for these rows");
+  at::Tensor z = logits.stride(1) == 1 ? logits : logits.contiguous();
+  at::Tensor y = targets.contiguous();
+  check_status(fwl_linear_chunk(fwl_dtype_of(z), z.data_ptr(), z.size(0), z.size(1), z.stride(0), v0, V,
+                                y.data_ptr<int64_t>(), state.data_ptr(), current_stream(z)),
+               "fw_linear_chunk");
+}
+
+// [H, losses, kappa, support [N, cap] int32, overflow [N] int32] after the last chunk
+std::vector<at::Tensor> fw_linear_finish(at::Tensor state, at::Tensor targets, int64_t V) {
+  TORCH_CHECK(targets.is_cuda() && targets.dim() == 1 && targets.scalar_type() == torch::kInt64,
+              "targets must be a CUDA int64 tensor [N]");
+  c10::DeviceGuard guard(targets.device());
+  const int64_t N = targets.size(0);
+  TORCH_CHECK(state.device() == targets.device() && state.scalar_type() == torch::kUInt8 &&
+                  (size_t)state.numel() >= fwl_linear_state_bytes(N),
+              "state must come from fw_linear_state for these rows");
+  at::Tensor y = targets.contiguous();
+  const auto f32 = y.options().dtype(torch::kFloat32), i32 = y.options().dtype(torch::kInt32);
+  at::Tensor H = torch::empty({N}, f32), losses = torch::empty({N}, f32), kappa = torch::empty({N}, i32);
+  at::Tensor support = torch::empty({N, (int64_t)fwl_linear_support_cap()}, i32);
+  at::Tensor overflow = torch::empty({N}, i32);
+  check_status(fwl_linear_finish(state.data_ptr(), y.data_ptr<int64_t>(), N, V, H.data_ptr<float>(),
+                                 losses.data_ptr<float>(), kappa.data_ptr<int32_t>(), support.data_ptr<int32_t>(),
+                                 overflow.data_ptr<int32_t>(), current_stream(y)),
+               "fw_linear_finish");
+  return {H, losses, kappa, support, overflow};
+}
+
+// [dhidden, dweight] of the rows with kappa > 0 (rows with kappa 0 contribute nothing), for the
+// gradient with per-row scale row_scale (one value, or one per row)
+std::vector<at::Tensor> fw_linear_grads(at::Tensor hidden, at::Tensor weight, at::Tensor targets, at::Tensor kappa,
+                                        at::Tensor support, at::Tensor row_scale, bool want_dh, bool want_dw) {
+  TORCH_CHECK(hidden.is_cuda() && hidden.dim() == 2 && weight.dim() == 2 && hidden.size(1) == weight.size(1),
+              "hidden [N, d] and weight [V, d] must be CUDA tensors with the same d");
+  TORCH_CHECK(hidden.scalar_type() == weight.scalar_type(), "hidden and weight must have one dtype");
+  c10::DeviceGuard guard(hidden.device());
+  const int64_t N = hidden.size(0), d = hidden.size(1), V = weight.size(0);
+  const int dt = fwl_dtype_of(hidden);
+  at::Tensor h = hidden.contiguous(), w = weight.contiguous(), y = targets.contiguous();
+  at::Tensor kap = kappa.contiguous(), sup = support.contiguous();
+  TORCH_CHECK(y.size(0) == N && kap.size(0) == N && sup.size(0) == N &&
+                  sup.size(1) == (int64_t)fwl_linear_support_cap() && kap.scalar_type() == torch::kInt32 &&
+                  sup.scalar_type() == torch::kInt32,
+              "targets, kappa and support must come from fw_linear_finish for these rows");
+  at::Tensor rs = row_scale.to(torch::kFloat32).contiguous();
+  TORCH_CHECK(rs.numel() == 1 || rs.numel() == N, "row_scale must have one value or one per row");
+  const int64_t rs_stride = rs.numel() == 1 ? 0 : 1;
+  const hipStream_t s = current_stream(h);
+  at::Tensor dh, dW;
+  if (want_dh) {
+    dh = torch::zeros_like(h);
+    check_status(fwl_linear_dhidden(dt, w.data_ptr(), V, d, y.data_ptr<int64_t>(), kap.data_ptr<int32_t>(),
+                                    sup.data_ptr<int32_t>(), rs.data_ptr<float>(), rs_stride, N, dh.data_ptr(), s),
+                 "fw_linear_grads (dhidden)");
+  }
+  if (want_dw) {
+    dW = torch::zeros_like(w);
+    // entries per row: the support, plus the label when it lies outside the support
+    const int64_t cap = sup.size(1);
+    at::Tensor live = kap > 0;
+    at::Tensor pos = torch::arange(cap, kap.options()).unsqueeze(0) < kap.unsqueeze(1);
+    at::Tensor lab_in = ((sup == y.unsqueeze(1).to(torch::kInt32)) & pos).any(1);
+    at::Tensor lab_ok = (y >= 0) & (y < V);
+    at::Tensor cnt = (kap.clamp_min(0).to(torch::kInt64) + (live & lab_ok & lab_in.logical_not()).to(torch::kInt64));
+    at::Tensor incl = cnt.cumsum(0);
+    const int64_t P = N > 0 ? incl[N - 1].item<int64_t>() : 0;
+    if (P > 0) {
+      at::Tensor offsets = incl - cnt;
+      at::Tensor keys = torch::empty({P}, y.options());
+      at::Tensor vals = torch::empty({P}, y.options().dtype(torch::kFloat32));
+      check_status(fwl_linear_coo(y.data_ptr<int64_t>(), N, V, kap.data_ptr<int32_t>(), sup.data_ptr<int32_t>(),
+                                  offsets.data_ptr<int64_t>(), rs.data_ptr<float>(), rs_stride,
+                                  keys.data_ptr<int64_t>(), vals.data_ptr<float>(), s),
+                   "fw_linear_grads (entries)");
+      auto sorted = keys.sort();
+      at::Tensor skeys = std::get<0>(sorted).contiguous();
+      at::Tensor svals = vals.index_select(0, std::get<1>(sorted)).contiguous();
+      check_status(fwl_linear_dweight(dt, h.data_ptr(), N, V, d, skeys.data_ptr<int64_t>(), svals.data_ptr<float>(),
+                                      P, dW.data_ptr(), s),
+                   "fw_linear_grads (dweight)");
+    }
+  }
+  return {dh, dW};
+}
+
 void set_params(int64_t path, int64_t cand_cap) {
   check_status(fwl_set_params((int)path, (int)cand_cap), "set_params");
 }
@@ -246,6 +351,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("fw_backward_small", &fw_backward_small, "FW loss backward from the support mask (MI355X)");
   m.def("fw_forward_backward", &fw_forward_backward, "Fused FW loss forward + backward (MI355X)",
         py::arg("logits"), py::arg("targets"), py::arg("scale") = -1.0, py::arg("reduce_div") = -1.0);
+  m.def("fw_linear_state", &fw_linear_state, "Per-row state of the linear layer fused with the loss");
+  m.def("fw_linear_chunk", &fw_linear_chunk, "Merge one vocabulary chunk of logits into the state");
+  m.def("fw_linear_finish", &fw_linear_finish, "H, losses, kappa, support columns and overflow flags");
+  m.def("fw_linear_grads", &fw_linear_grads, "Sparse dhidden and dweight from the supports",
+        py::arg("hidden"), py::arg("weight"), py::arg("targets"), py::arg("kappa"), py::arg("support"),
+        py::arg("row_scale"), py::arg("want_dh") = true, py::arg("want_dw") = true);
   m.def("fw_scale_grad", &fw_scale_grad, "In-place grad *= grad_output (device-side skip when 1)");
   m.def("set_params", &set_params, "Dispatch switches: path (0 auto, 1 wave registers, 2 block stream, 3 block generic, "
         "4 wave stream, 5 wave generic, 6 short-row segments, 7 split rows), cand_cap",

@@ -100,6 +100,96 @@ def fw_loss_grad(Z, y, scale=1.0, flat_kmax=None, serial_below=None, use_chunked
     return losses.double(), grad, kappa.long()
 
 
+def linear_forward(hidden, weight, target, chunk=8192):
+    """The loss side of ``familywise_linear_loss``: logits = hidden @ weight.T one vocabulary chunk
+    of ``chunk`` columns at a time (each chunk's logits exist only while it is merged), then the
+    threshold of every row from its carried list.  Returns a dict with H, losses, kappa (int32),
+    support (int32 [N, cap], the first kappa entries valid), overflow (rows solved on their
+    materialised logits instead) and dense = (rows, grad of those rows with scale 1) or None.
+    H, losses and kappa are those ``fw_forward_backward`` gives on the concatenated chunk logits."""
+    if not (hidden.is_cuda and weight.is_cuda):
+        raise RuntimeError("familywise_linear_loss: hidden and weight must be CUDA (ROCm) tensors")
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError("hidden must be [N, d] and weight [V, d]")
+    if chunk < 1:
+        raise ValueError("chunk must be >= 1")
+    N, V = hidden.shape[0], weight.shape[0]
+    h = hidden.detach().contiguous()
+    w = weight.detach().contiguous()
+    y = target.contiguous()
+    state = _ext.fw_linear_state(h, N)
+    for v0 in range(0, V, chunk):
+        _ext.fw_linear_chunk(state, torch.nn.functional.linear(h, w[v0:v0 + chunk]), y, v0, V)
+    H, losses, kappa, support, overflow = _ext.fw_linear_finish(state, y, V)
+    rows = overflow.nonzero().flatten()
+    dense = None
+    kappa_sparse = kappa
+    if rows.numel():
+        # rows whose lists outgrew the state: their logits in full, through the fused op
+        Hr, lr, _, kr, gr = _ext.fw_forward_backward(torch.nn.functional.linear(h[rows], w), y[rows], 1.0, 1.0)
+        H[rows] = Hr
+        losses[rows] = lr
+        kappa_sparse = kappa.clone()   # 0: the sparse gradient kernels skip these rows
+        kappa[rows] = kr
+        dense = (rows, gr)
+    return {"H": H, "losses": losses, "kappa": kappa, "kappa_sparse": kappa_sparse, "support": support,
+            "overflow": overflow, "dense": dense}
+
+
+class FWLinearFunction(torch.autograd.Function):
+    """FW loss of hidden @ weight.T without materialising the logits.  The gradient with respect to
+    the logits has kappa + 1 non-zeros per row, so the backward gathers and scatters weight and
+    hidden rows instead of running the two GEMMs of an unfused backward."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, target, reduction, chunk):
+        res = linear_forward(hidden, weight, target, chunk)
+        losses = res["losses"]
+        N = hidden.shape[0]
+        if reduction == "none":
+            out = losses
+        else:
+            total = losses.double().sum()
+            out = (total / N if (reduction == "mean" and N) else total).float()
+        ctx.save_for_backward(hidden.detach(), weight.detach(), target, res["kappa_sparse"], res["support"])
+        ctx.dense = res["dense"]
+        ctx.reduction = reduction
+        return out.to(hidden.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        h, w, y, kappa, support = ctx.saved_tensors
+        want_dh, want_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (want_dh or want_dw):
+            return None, None, None, None, None
+        N = h.shape[0]
+        go = grad_output.detach().float()
+        if ctx.reduction == "mean":
+            rs = (go / N if N else go).reshape(1)
+        else:
+            rs = go.reshape(-1)
+        dh, dw = _ext.fw_linear_grads(h, w, y, kappa, support, rs, want_dh, want_dw)
+        if ctx.dense is not None:
+            rows, gr = ctx.dense
+            g = gr.float() * (rs if rs.numel() == 1 else rs[rows]).reshape(-1, 1)
+            if want_dh:
+                dh[rows] += (g @ w.float()).to(dh.dtype)
+            if want_dw:
+                dw += (g.t() @ h[rows].float()).to(dw.dtype)
+        return (dh if want_dh else None), (dw if want_dw else None), None, None, None
+
+
+def familywise_linear_loss(hidden, weight, target, reduction="mean", chunk=8192):
+    """FW loss of the logits hidden @ weight.T (an LM head: hidden [N, d], weight [V, d], one dtype:
+    float32, bfloat16 or float16) and int64 targets [N], computed one vocabulary chunk of
+    ``chunk`` columns at a time.  The loss equals ``familywise_loss(hidden @ weight.T, target,
+    reduction)`` on the same chunk logits; the gradients of hidden and weight come from the
+    loss's sparse logit gradient (kappa + 1 non-zeros per row) without an [N, V] tensor."""
+    if reduction not in _REDUCTIONS:
+        raise ReductionError(f"Invalid reduction mode: {reduction!r} (expected 'mean', 'sum' or 'none')")
+    return FWLinearFunction.apply(hidden, weight, target, reduction, chunk)
+
+
 def native_libraries():
     """Paths of the native libraries this module runs on (for load checks)."""
     return [os.path.join(_HERE, "libfwloss.so"), _ext.__file__]

@@ -140,6 +140,49 @@ int fwl_scale_grad(float* grad, const float* grad_output, int64_t go_stride, int
 int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_t go_stride, int64_t N,
                          int64_t C, hipStream_t stream);
 
+/* ---- The linear layer that produces the logits, fused with the loss ("LM head").
+ * No counterpart in the reference: its losses take materialised logits (reference_impl.py:11-35,
+ * src/cpu/fw_cpu.cpp:721-741, src/cuda/fw_radix_argmax.cu:1381-1496).  For hidden [N, d] and
+ * weight [V, d], logits = hidden @ weight^T are handed over one vocabulary chunk at a time
+ * (columns v0 .. v0 + Vc - 1), so no [N, V] tensor is needed:
+ *   fwl_linear_begin    once per batch (state: fwl_linear_state_bytes(N) bytes, 16-byte aligned);
+ *   fwl_linear_chunk    once per chunk (logits [N, Vc] with row stride ld, v0 + Vc <= V), in
+ *                       any order, each column exactly once;
+ *   fwl_linear_finish   H, losses, kappa and the support's columns (support[r * cap + p],
+ *                       p < kappa[r], cap = fwl_linear_support_cap()) of every row.  Rows with
+ *                       overflow[r] = 1 (more than cap entries within 1 of the maximum after
+ *                       tightening, or no finite maximum) are not solved: the caller runs them
+ *                       through fwl_forward_backward_typed on their materialised logits;
+ *   fwl_linear_dhidden  dhidden[r] = sum_j g_rj weight[j] over the row's kappa + 1 non-zero
+ *                       gradient columns (no GEMM), where g is the fused op's gradient with
+ *                       scale s_r = row_scale[r * rs_stride];
+ *   fwl_linear_coo      the (column, row) entries of g: row r's at offsets[r] (exclusive prefix
+ *                       sum of kappa[r] + [label outside the support]), key = column * 2N + 2r
+ *                       (+1 for a label entry), value g;
+ *   fwl_linear_dweight  dweight[j] = sum of g * hidden[row] over column j's entries, given the
+ *                       entries sorted by key (keys with a column outside [0, V) are skipped);
+ *                       rows of dweight without entries are not written (zero-fill them first).
+ * Every decision is the one fwl_forward_backward_typed takes on the same logits: H, losses and
+ * kappa are bit-identical to it.  Element types as enum fwl_dtype (logits, weight, hidden and the
+ * gradients share one). */
+size_t fwl_linear_state_bytes(int64_t N);
+int fwl_linear_support_cap(void);
+int fwl_linear_begin(void* state, int64_t N, hipStream_t stream);
+int fwl_linear_chunk(int dtype, const void* logits, int64_t N, int64_t Vc, int64_t ld, int64_t v0,
+                     int64_t V, const int64_t* targets, void* state, hipStream_t stream);
+int fwl_linear_finish(const void* state, const int64_t* targets, int64_t N, int64_t V, float* H,
+                      float* losses, int32_t* kappa, int32_t* support, int32_t* overflow,
+                      hipStream_t stream);
+int fwl_linear_dhidden(int dtype, const void* weight, int64_t V, int64_t d, const int64_t* targets,
+                       const int32_t* kappa, const int32_t* support, const float* row_scale,
+                       int64_t rs_stride, int64_t N, void* dhidden, hipStream_t stream);
+int fwl_linear_coo(const int64_t* targets, int64_t N, int64_t V, const int32_t* kappa,
+                   const int32_t* support, const int64_t* offsets, const float* row_scale,
+                   int64_t rs_stride, int64_t* keys, float* values, hipStream_t stream);
+int fwl_linear_dweight(int dtype, const void* hidden, int64_t N, int64_t V, int64_t d,
+                       const int64_t* keys, const float* values, int64_t P, void* dweight,
+                       hipStream_t stream);
+
 /* Process-wide dispatch switches, the GPU counterpart of the reference CPU path's set_params
  * (src/cpu/fw_cpu.cpp:758-763, used by its tests to force each branch).  Not thread-safe; meant
  * for tests and tuning.
