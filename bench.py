@@ -62,6 +62,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--copy-probe", action="store_true",
                     help="time a plain 1 GiB device copy instead (calibrates rocprof byte counters)")
+    ap.add_argument("--op", default="loss", choices=["loss", "linear"],
+                    help="loss: the FW loss on resident logits (the headline); linear: the LM head fused "
+                         "with the loss (familywise_linear_loss) against the unfused F.linear + loss")
+    ap.add_argument("--lm", default="8192,4096,128256,8192",
+                    help="--op linear: tokens N, hidden size d, vocabulary V, chunk columns")
     return ap.parse_args()
 
 
@@ -144,8 +149,85 @@ def copy_probe(args):
                       "ms": dt * 1e3, "gbps": 8 * n / dt / 1e9}), flush=True)
 
 
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}
+
+
+def bench_linear(args):
+    """One step = forward + backward (gradients of hidden and weight) of the FW loss of
+    hidden @ weight.T, mean reduction.  The fused op computes the logits one vocabulary chunk at a
+    time and derives both gradients from the sparse logit gradient; the unfused reference
+    materialises the logits and back-propagates through two more GEMMs."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+    import fwloss
+    N, d, V, chunk = (int(x) for x in args.lm.split(","))
+    dname = args.dtype if any(a.startswith("--dtype") for a in sys.argv) else "bf16"   # LM heads run in bf16
+    dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dname]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    h = torch.randn(N, d, device=dev, generator=g).to(dt).requires_grad_(True)
+    w = (torch.randn(V, d, device=dev, generator=g) * (3.0 / d ** 0.5)).to(dt).requires_grad_(True)
+    y = torch.randint(0, V, (N,), device=dev, generator=g)
+
+    def fused():
+        h.grad = None
+        w.grad = None
+        fwloss.familywise_linear_loss(h, w, y, "mean", chunk).backward()
+
+    def unfused():
+        h.grad = None
+        w.grad = None
+        fwloss.familywise_loss(F.linear(h, w), y, "mean").backward()
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps, e0.elapsed_time(e1) / steps
+    steps = min(args.steps, 20)
+    warm = min(args.warmup, 3)
+    wall_f, gpu_f = timed(fused, steps, warm)
+    res = fwloss.linear_forward(h, w, y, chunk)
+    n_over = int(res["overflow"].sum().item())
+    wall_u, gpu_u = (None, None)
+    if not args.no_two_op:
+        wall_u, gpu_u = timed(unfused, max(1, steps // 2), 1)
+    flops = 2.0 * N * V * d   # the logits GEMM: the only dense contraction of the fused step
+    tf = flops / (gpu_f * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "tokens/s, FW loss of an LM head (hidden @ weight.T), fwd+bwd, fused vocabulary chunks",
+        "value": N / wall_f, "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": wall_f * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": dname, "data": "synthetic",
+        "config": {"workload": f"LM head N={N} d={d} V={V} chunk={chunk} {dname}, labels uniform, mean reduction",
+                   "N": N, "d": d, "V": V, "chunk": chunk, "op": "familywise_linear_loss",
+                   "parallelism": "single GPU"},
+        "gpu_ms_per_step": gpu_f, "overflow_rows": n_over,
+        "unfused_ms_per_step": None if gpu_u is None else gpu_u,
+        "speedup_vs_unfused": None if gpu_u is None else gpu_u / gpu_f,
+        "roofline": {"bound": "mfma", "kernel": "whole step (logits GEMM per chunk + list merge + sparse grads)",
+                     "achieved": tf, "peak": MFMA_PEAK_TFLOPS[dname], "unit": "TFLOP/s",
+                     "frac": tf / MFMA_PEAK_TFLOPS[dname], "traffic": None, "flops": flops},
+    }), flush=True)
+
+
 def main():
     args = parse()
+    if args.op == "linear":
+        if args.gpus != 1:
+            print("bench.py: this build runs on one GPU only", file=sys.stderr)
+            sys.exit(2)
+        bench_linear(args)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the row-sharded multi-GPU design is described in DESIGN.md", file=sys.stderr)

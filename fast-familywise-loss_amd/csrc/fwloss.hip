@@ -29,6 +29,9 @@
 //                   tightened by fixed-point iterations on the list; a list that cannot be
 //                   tightened sends the row to the generic multi-pass path.
 //   fwl_mask_to_grad, fwl_cand_to_grad   the two-op backward of the drop-in interface.
+//   fwl_lin_*       the linear layer (LM head) fused with the loss: vocabulary chunks of logits
+//                   merged into per-row candidate lists, the threshold from the lists, and the
+//                   sparse gradients of hidden and weight.
 // The mean loss is reduced in fp64 in a fixed order: per-block partial sums, per-group sums by the
 // last block of each group of 32, then the last group finisher sums the group sums (ticket
 // counters in the caller's workspace, each reset by its last user).
