@@ -192,3 +192,30 @@ def test_chunk_order_independent(dev):
     for a, b in zip(*outs):
         assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a,
                            b.view(torch.int32) if b.dtype == torch.float32 else b)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_grads_unaligned_hidden_size(dev, dt):
+    """d whose rows are not whole 16-byte units: the element-wise gather and scatter paths."""
+    import fwloss
+    N, d, V, chunk = 90, 37, 2500, 999
+    h, w, y = make(dev, N, d, V, dt, seed=17)
+    hh = h.clone().requires_grad_(True)
+    ww = w.clone().requires_grad_(True)
+    fwloss.familywise_linear_loss(hh, ww, y, "sum", chunk).backward()
+    z = chunk_logits(h, w, chunk).float().cpu().numpy()
+    _, dh_ref, dw_ref = dense_grads(z, y.cpu().numpy(), h, w, np.ones(N))
+    close(hh.grad, dh_ref, TOL[dt])
+    close(ww.grad, dw_ref, TOL[dt])
+
+
+def test_only_hidden_needs_grad(dev):
+    import fwloss
+    N, d, V, chunk = 64, 32, 1000, 300
+    h, w, y = make(dev, N, d, V, "f32", seed=19)
+    hh = h.clone().requires_grad_(True)
+    fwloss.familywise_linear_loss(hh, w, y, "mean", chunk).backward()
+    z = chunk_logits(h, w, chunk).float().cpu().numpy()
+    _, dh_ref, _ = dense_grads(z, y.cpu().numpy(), h, w, np.full(N, 1.0 / N))
+    close(hh.grad, dh_ref, 1e-5)
+    assert w.grad is None

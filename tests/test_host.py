@@ -132,6 +132,47 @@ def test_typed_entry_point_argument_errors():
     assert L.fwl_scale_grad_typed(1, None, None, 0, 0, 16, None) == 0
 
 
+def test_linear_entry_point_argument_errors():
+    L = capi.lib()
+    assert L.fwl_linear_state_bytes(10) == 10 * (32 + 8 * L.fwl_linear_support_cap())
+    assert L.fwl_linear_state_bytes(0) == 0
+    assert L.fwl_linear_begin(None, 8, None) == 1
+    assert L.fwl_linear_begin(P(A16 + 8), 8, None) == 3          # the state needs 16-byte alignment
+    assert L.fwl_linear_begin(None, 0, None) == 0
+
+    def chunk(dtype=1, z=A16, N=8, Vc=16, ld=16, v0=0, V=64, y=A16, st=A16):
+        return L.fwl_linear_chunk(dtype, P(z), N, Vc, ld, v0, V, P(y), P(st), None)
+    assert chunk(dtype=3) == 1
+    assert chunk(ld=15) == 1                   # rows shorter than the chunk
+    assert chunk(v0=60) == 1                   # columns past V
+    assert chunk(v0=-1) == 1
+    assert chunk(z=None) == 1
+    assert chunk(y=A16 + 4) == 3
+    assert chunk(z=A16 + 1) == 3               # 16-bit logits need 2-byte alignment
+    assert chunk(N=0) == 0
+    assert L.fwl_linear_finish(P(A16), P(A16), 8, 0, P(A16), P(A16), P(A16), P(A16), P(A16), None) == 1
+    assert L.fwl_linear_finish(P(A16), P(A16), 8, 64, P(A16), None, P(A16), P(A16), P(A16), None) == 1
+    assert L.fwl_linear_finish(P(A16), P(A16), 8, 64, P(A16), P(A16), P(A16), P(A16 + 2), P(A16), None) == 3
+    assert L.fwl_linear_dhidden(1, P(A16), 64, 0, P(A16), P(A16), P(A16), P(A16), 0, 8, P(A16), None) == 1
+    assert L.fwl_linear_dhidden(1, P(A16), 64, 32, P(A16), P(A16), P(A16), P(A16), -1, 8, P(A16), None) == 1
+    assert L.fwl_linear_dhidden(4, P(A16), 64, 32, P(A16), P(A16), P(A16), P(A16), 0, 8, P(A16), None) == 1
+    assert L.fwl_linear_dhidden(1, P(A16 + 1), 64, 32, P(A16), P(A16), P(A16), P(A16), 0, 8, P(A16), None) == 3
+    assert L.fwl_linear_coo(P(A16), 8, 64, P(A16), P(A16), None, P(A16), 0, P(A16), P(A16), None) == 1
+    assert L.fwl_linear_coo(P(A16), 8, 64, P(A16), P(A16), P(A16), P(A16), 0, P(A16 + 4), P(A16), None) == 3
+    assert L.fwl_linear_dweight(1, P(A16), 8, 64, 32, None, P(A16), 5, P(A16), None) == 1
+    assert L.fwl_linear_dweight(1, P(A16), 8, 0, 32, P(A16), P(A16), 5, P(A16), None) == 1
+    assert L.fwl_linear_dweight(1, P(A16), 8, 64, 32, P(A16), P(A16), 0, P(A16), None) == 0
+
+
+def test_linear_loss_rejects_cpu_and_bad_arguments():
+    import fwloss
+    h, w, y = torch.zeros(4, 8), torch.zeros(10, 8), torch.zeros(4, dtype=torch.long)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        fwloss.familywise_linear_loss(h, w, y)
+    with pytest.raises(KeyError):
+        fwloss.familywise_linear_loss(h, w, y, reduction="max")
+
+
 def test_set_params_validation_and_round_trip():
     L = capi.lib()
     p, c = ctypes.c_int(-1), ctypes.c_int(-1)
