@@ -32,9 +32,10 @@
 //   fwl_lin_*       the linear layer (LM head) fused with the loss: vocabulary chunks of logits
 //                   merged into per-row candidate lists, the threshold from the lists, and the
 //                   sparse gradients of hidden and weight.
-// The mean loss is reduced in fp64 in a fixed order: per-block partial sums, per-group sums by the
-// last block of each group of 32, then the last group finisher sums the group sums (ticket
-// counters in the caller's workspace, each reset by its last user).
+// The mean loss is reduced in fp64 in a fixed order: per-block partial sums, then either the last
+// block sums them all (grids of up to 512 blocks) or per-group sums by the last block of each group
+// of 32 and the last group finisher sums the group sums (ticket counters in the caller's
+// workspace, each reset by its last user).
 //
 // Compile with -Xclang -target-feature -Xclang -packed-fp32-ops (see fwloss_build.py).
 #include <hip/hip_runtime.h>
@@ -195,6 +196,10 @@ constexpr int kStreamUnroll = 4;       // 128-bit loads per lane per streaming r
 constexpr int kRoundSlotsV1 = 16;      // 32-bit loads per lane per streaming round (unaligned rows)
 constexpr size_t kWsHeader = 256;      // the final ticket counter; then the mean's partial sums
 constexpr int kTicketGroup = 32;       // blocks per first-level ticket of the mean
+constexpr unsigned kOneTicketBlocks = 512;   // grids up to this size take a single ticket level
+                                             // (65536 x 1000, 512 blocks: 96.2 us against 96.9
+                                             // with two levels; 16384 x 100, 1280 blocks finishing
+                                             // together: 18.3 us against 10.0)
 constexpr int kTicketStride = 16;      // first-level tickets 64 bytes apart
 constexpr uint32_t kOffNone = 0x7FFFFFF0u;   // a buffer offset past every resource: access dropped
 
@@ -522,6 +527,31 @@ __device__ void mean_epilogue(double bsum, const Outs& o) {
   __shared__ int s_last;
   __shared__ double s_red[kBlock];
   if (o.mean == nullptr) return;
+  if (gridDim.x <= kOneTicketBlocks) {
+    // One ticket: the last block sums every partial (one device-scope round trip fewer than two
+    // levels; with more blocks finishing together the single counter serialises too many atomics)
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(o.partials + blockIdx.x, bsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wait_vmem();
+      s_last = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    double acc = 0.0;
+    for (unsigned i = threadIdx.x; i < gridDim.x; i += kBlock)
+      acc += __hip_atomic_load(o.partials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int s = kBlock / 2; s > 0; s >>= 1) {
+      if ((int)threadIdx.x < s) s_red[threadIdx.x] += s_red[threadIdx.x + s];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      *o.mean = (float)(s_red[0] / o.reduce_div);
+      __hip_atomic_store(o.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
   // Two ticket levels: the last block of each group of kTicketGroup blocks sums the group's
   // partials (in block order) and takes the final ticket; the last of those sums the group sums.
   // When many blocks finish together, no single counter serialises more than
