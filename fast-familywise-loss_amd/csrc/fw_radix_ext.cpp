@@ -188,10 +188,28 @@ at::Tensor fw_backward(at::Tensor logits, at::Tensor targets, at::Tensor H, at::
 
 // fw_forward_backward(logits, targets, scale=1/N, reduce_div=N) -> [H, losses, reduced, kappa, grad]
 // The fused hot path: one launch, logits read once, dense gradient written once.  Logits may be
-// float32, bfloat16 or float16; grad has the logits' dtype, H, losses and reduced are float32.
+// float32, bfloat16 or float16 (grad has the logits' dtype, H, losses and reduced are float32) or
+// float64 (every output fp64, as the reference CPU path computes them).
 std::vector<at::Tensor> fw_forward_backward(at::Tensor logits, at::Tensor targets, double scale,
                                             double reduce_div) {
   c10::DeviceGuard guard(logits.device());
+  if (logits.is_cuda() && logits.dim() == 2 && logits.scalar_type() == torch::kFloat64) {
+    // fp64 logits (the reference CPU path's other dtype): fp64 H, losses, reduced and grad
+    TORCH_CHECK(logits.size(1) >= 1, "logits must have K >= 1 classes");
+    check_rows(targets, logits, torch::kInt64, "targets");
+    at::Tensor z = logits.contiguous(), y = targets.contiguous();
+    const int64_t N = z.size(0), K = z.size(1);
+    if (scale < 0) scale = N > 0 ? 1.0 / (double)N : 1.0;
+    if (reduce_div < 0) reduce_div = (double)N;
+    const auto f64 = z.options();
+    at::Tensor H = torch::empty({N}, f64), losses = torch::empty({N}, f64), mean = torch::empty({}, f64);
+    at::Tensor kappa = torch::empty({N}, z.options().dtype(torch::kInt32)), grad = torch::empty({N, K}, f64);
+    check_status(fwl_forward_backward_f64(z.data_ptr<double>(), y.data_ptr<int64_t>(), N, K, scale, reduce_div,
+                                          H.data_ptr<double>(), losses.data_ptr<double>(), mean.data_ptr<double>(),
+                                          kappa.data_ptr<int32_t>(), grad.data_ptr<double>(), current_stream(z)),
+                 "fw_forward_backward");
+    return {H, losses, mean, kappa, grad};
+  }
   Common c = prepare(logits, targets, true);
   const int64_t N = c.logits.size(0), K = c.logits.size(1);
   if (scale < 0) scale = N > 0 ? 1.0 / (double)N : 1.0;
@@ -211,9 +229,18 @@ std::vector<at::Tensor> fw_forward_backward(at::Tensor logits, at::Tensor target
 at::Tensor fw_scale_grad(at::Tensor grad, at::Tensor grad_output) {
   TORCH_CHECK(grad.is_cuda() && grad.dim() == 2 && grad.is_contiguous(),
               "grad must be a contiguous CUDA tensor [N, K]");
-  const int dtype = fwl_dtype_of(grad);
   c10::DeviceGuard guard(grad.device());
   TORCH_CHECK(grad_output.device() == grad.device(), "grad_output must be on the device of grad");
+  if (grad.scalar_type() == torch::kFloat64) {
+    at::Tensor go = grad_output.to(torch::kFloat64).contiguous();
+    TORCH_CHECK(go.numel() == 1 || (go.dim() == 1 && go.size(0) == grad.size(0)),
+                "grad_output must be a scalar or have shape [N]");
+    check_status(fwl_scale_grad_f64(grad.data_ptr<double>(), go.data_ptr<double>(), go.numel() == 1 ? 0 : 1,
+                                    grad.size(0), grad.size(1), current_stream(grad)),
+                 "fw_scale_grad");
+    return grad;
+  }
+  const int dtype = fwl_dtype_of(grad);
   at::Tensor go = grad_output.to(torch::kFloat32).contiguous();
   int64_t stride = 0;
   if (go.numel() == 1) stride = 0;

@@ -75,9 +75,11 @@ class FWFunction(torch.autograd.Function):
 
 
 def familywise_loss(logits, target, reduction="mean"):
-    """FW loss of logits [N, C] (GPU; float32, bfloat16 or float16) and int64 targets [N];
-    reduction 'mean' | 'sum' | 'none'.  16-bit logits are widened to fp32 exactly; the loss and the
-    gradient are returned in the logits' dtype (the gradient rounded to nearest-even).
+    """FW loss of logits [N, C] (GPU; float32, float64, bfloat16 or float16) and int64 targets
+    [N]; reduction 'mean' | 'sum' | 'none'.  16-bit logits are widened to fp32 exactly; float64
+    logits are decided in fp64 (the reference CPU path's two dtypes, src/cpu/fw_cpu.cpp:697-703).
+    The loss and the gradient are returned in the logits' dtype (16-bit gradients rounded to
+    nearest-even).
 
     Same call shape as the reference's ``fwcpp.familywise_loss`` (src/cpu/fwcpp.py:18-19), which
     accepts 'sum' and 'mean'; 'none' returns the per-row losses (reference_impl.py:30-33).

@@ -33,6 +33,8 @@ SIGNATURES = {
     "fwl_scale_grad_typed": ([ctypes.c_int, _P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
     "fwl_set_params": ([ctypes.c_int, ctypes.c_int], ctypes.c_int),
     "fwl_get_params": ([ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+    "fwl_forward_backward_f64": ([_P, _P, _I64, _I64, _D, _D, _P, _P, _P, _P, _P, _P], ctypes.c_int),
+    "fwl_scale_grad_f64": ([_P, _P, _I64, _I64, _I64, _P], ctypes.c_int),
     "fwl_linear_state_bytes": ([_I64], ctypes.c_size_t),
     "fwl_linear_support_cap": ([], ctypes.c_int),
     "fwl_linear_begin": ([_P, _I64, _P], ctypes.c_int),

@@ -94,6 +94,20 @@ int fwl_forward_backward_typed(int dtype, const void* logits, const int64_t* tar
                                float* mean_loss, int32_t* kappa, void* grad, void* workspace,
                                size_t workspace_bytes, hipStream_t stream);
 
+/* fwl_forward_backward for float64 logits (the reference CPU path's second dtype,
+ * src/cpu/fw_cpu.cpp:697-703, run_generic<double>; the reference GPU ops take float32 only).
+ * Every decision is taken in fp64: tau from fixed-point iterations t <- H({z > t}) with sums in a
+ * fixed order; H[r] = tau (so z > H[r] is the support); losses, mean_loss and grad are fp64
+ * (grad[r,j] = z_j > tau ? scale / kappa : 0, minus scale at the label).  mean_loss needs losses.
+ * No workspace: the mean is reduced by a one-block kernel after the rows. */
+int fwl_forward_backward_f64(const double* logits, const int64_t* targets, int64_t N, int64_t C,
+                             double scale, double reduce_div, double* H, double* losses,
+                             double* mean_loss, int32_t* kappa, double* grad, hipStream_t stream);
+
+/* fwl_scale_grad for an fp64 gradient and fp64 factors (FWFunction::backward, fw_cpu.cpp:734-740). */
+int fwl_scale_grad_f64(double* grad, const double* grad_output, int64_t go_stride, int64_t N,
+                       int64_t C, hipStream_t stream);
+
 /* Forward with the support mask: selected[r,j] = (z_j > tau) as bytes 0/1 (torch.bool layout).
  * Replaces fw_radix_forward_small (src/cuda/fw_radix_argmax.cu:1381-1414; binding.cpp:11):
  * outputs [H, losses, mean_loss, kappa, selected_logits]. */

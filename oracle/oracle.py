@@ -83,6 +83,34 @@ def single_pass(z, y, scale=None, grad=True, nthreads=None, chunk=0, cap_factor=
     return out
 
 
+def definition_f64(z, y, scale=None):
+    """Definition oracle for float64 logits (numpy, fp64): per row sort descending, cumulative sums
+    in row order, tau = max_k (S_k - 1)/k (first maximiser; reference_impl.py:15-24), clamped below
+    the row maximum; kappa = |{z > tau}|, loss = (1 - z_y) + tau, grad = scale * ([z > tau] / kappa
+    - e_y) (fw_cpu.cpp:601-614; float64 logits run through fw_cpu.cpp:697-703).  Rows need a finite
+    maximum and targets in [0, C).  Returns dict(tau, loss, kappa, grad, mean)."""
+    z = np.ascontiguousarray(z, dtype=np.float64)
+    y = np.ascontiguousarray(y, dtype=np.int64)
+    N, C = z.shape
+    if scale is None:
+        scale = 1.0 / N if N else 1.0
+    v = -np.sort(-z, axis=1)
+    S = np.cumsum(v, axis=1)
+    f = (S - 1.0) / np.arange(1, C + 1, dtype=np.float64)
+    tau = f[np.arange(N), np.argmax(f, axis=1)] if N else np.zeros(0)
+    m = v[:, 0] if N else np.zeros(0)
+    hi = (tau >= m) & np.isfinite(m)
+    tau = np.where(hi, np.nextafter(m, -np.inf), tau)
+    sup = z > tau[:, None]
+    kappa = sup.sum(axis=1).astype(np.int32)
+    zy = z[np.arange(N), y]
+    loss = (1.0 - zy) + tau
+    inv = scale / kappa.astype(np.float64)
+    grad = np.where(sup, inv[:, None], 0.0)
+    grad[np.arange(N), y] -= scale
+    return dict(tau=tau, loss=loss, kappa=kappa, grad=grad, mean=loss.mean() if N else np.nan)
+
+
 def round_down(t):
     return np.float32(_lib().fwo_round_down(float(t)))
 

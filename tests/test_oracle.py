@@ -145,8 +145,10 @@ def test_single_pass_restatement_matches_definition():
     np.testing.assert_array_equal(s0["kappa"], d["kappa"])
 
 
-@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(HERE, "golden", "golden_*.npz"))),
-                         ids=lambda p: os.path.basename(p))
+F32_GOLDEN = sorted(p for p in glob.glob(os.path.join(HERE, "golden", "golden_*.npz")) if not p.endswith("_f64.npz"))
+
+
+@pytest.mark.parametrize("path", F32_GOLDEN, ids=lambda p: os.path.basename(p))
 def test_oracle_reproduces_reference_golden_vectors(path):
     g = np.load(path)
     z, y, scale = g["z"], g["y"], float(g["scale"])
@@ -178,6 +180,58 @@ def test_oracle_matches_compiled_reference():
         out = oracle.definition(z, y)
         np.testing.assert_array_equal(out["kappa"], k.numpy())
         np.testing.assert_allclose(out["loss64"], L.numpy(), rtol=1e-12, atol=1e-12)
+        np.testing.assert_array_equal(out["grad"], G.numpy())
+
+
+F64_CASES = ("gauss", "ties", "wide", "flat")
+
+
+@pytest.mark.parametrize("name", F64_CASES)
+def test_f64_oracle_reproduces_reference_golden_vectors(name):
+    """float64 logits: the numpy definition against the compiled reference's run_generic<double>
+    (fw_cpu.cpp:697-703): kappa and the gradient bit-identical, losses within 1e-15 relative (the
+    reference writes the loss as 1 + (thr - z_y) + (tau - thr), fw_cpu.cpp:614)."""
+    g = np.load(os.path.join(HERE, "golden", "golden_f64.npz"))
+    z, y, scale = g[f"{name}_z"], g[f"{name}_y"], float(g[f"{name}_scale"])
+    out = oracle.definition_f64(z, y, scale)
+    np.testing.assert_array_equal(out["kappa"], g[f"{name}_kappa"])
+    np.testing.assert_allclose(out["loss"], g[f"{name}_L"], rtol=1e-15, atol=1e-15)
+    G = np.zeros_like(z)
+    G[g[f"{name}_g_rows"], g[f"{name}_g_cols"]] = g[f"{name}_g_vals"]
+    np.testing.assert_array_equal(out["grad"], G)
+
+
+def test_f64_oracle_matches_exact_subset_brute_force():
+    """tau of the fp64 definition is within an ulp of the exact rational max over all subsets, kappa
+    is the exact support size and the loss is the fp64 formula (small rows, ties included)."""
+    rng = np.random.default_rng(64)
+    for row in random_small_rows(rng, 300):
+        row = row.astype(np.float64)
+        if rng.integers(0, 2):
+            row = row + rng.standard_normal(row.size) * 1e-9     # values that are not fp32
+        out = oracle.definition_f64(row[None, :], np.zeros(1, np.int64), 1.0)
+        tau = exact_tau(row)
+        t = out["tau"][0]
+        # fp64 prefix sums round once per term: a few ulps of the magnitudes involved
+        scale_ = Fraction(float(np.abs(row).max())) + abs(tau) + 1
+        assert abs(Fraction(float(t)) - tau) <= scale_ * row.size * Fraction(1, 2 ** 52)
+        assert out["kappa"][0] == sum(Fraction(float(x)) > tau for x in row)
+        assert out["loss"][0] == (1.0 - row[0]) + t
+
+
+def test_f64_oracle_matches_compiled_reference():
+    ref = oracle.load_ref()
+    if ref is None:
+        pytest.skip("oracle/_ref not built here (the reference sources are needed to build it)")
+    import torch
+    rng = np.random.default_rng(5)
+    for N, C in ((64, 1000), (16, 7), (8, 20000)):
+        z = rng.standard_normal((N, C)) * rng.uniform(0.1, 5.0)
+        y = rng.integers(0, C, N).astype(np.int64)
+        L, G, k = ref.fw_loss_grad(torch.from_numpy(z), torch.from_numpy(y), 1.0 / N, 2 ** 62, 100000, True)
+        out = oracle.definition_f64(z, y)
+        np.testing.assert_array_equal(out["kappa"], k.numpy())
+        np.testing.assert_allclose(out["loss"], L.numpy(), rtol=1e-15, atol=1e-15)
         np.testing.assert_array_equal(out["grad"], G.numpy())
 
 
