@@ -35,7 +35,7 @@ METRIC = "rows/sec and achieved HBM GB/s (% of peak), fwd+bwd, N=65536 C=1000 fp
 HBM_PEAK_GBS = 8000.0
 
 
-ELEM_BYTES = {"f32": 4, "bf16": 2, "f16": 2}
+ELEM_BYTES = {"f32": 4, "bf16": 2, "f16": 2, "f64": 8}
 
 
 def alg_bytes(N, C, elem=4):
@@ -54,7 +54,7 @@ def parse():
                     help="rows of the batch (default: the configuration's N; few rows of a long "
                          "configuration run the split-row kernels)")
     ap.add_argument("--sets", type=int, default=3, help="rotated input/output buffer sets")
-    ap.add_argument("--dtype", default="f32", choices=["f32", "bf16", "f16"],
+    ap.add_argument("--dtype", default="f32", choices=["f32", "bf16", "f16", "f64"],
                     help="element type of the logits and the gradient (decisions are fp32/fp64)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-two-op", action="store_true",
@@ -245,7 +245,7 @@ def main():
     z_np, y_np = fwloss_data.make(args.config, N=args.rows, seed=0)
     N, C = z_np.shape
     cfg_tag = args.config if args.rows is None else f"{args.config}_{N}rows"
-    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[args.dtype]
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16, "f64": torch.float64}[args.dtype]
     sets = []
     for s in range(args.sets):
         zt = torch.from_numpy(z_np).to(dev).to(tdt) if s == 0 else sets[0][0].roll(s, dims=0).contiguous()
@@ -304,7 +304,9 @@ def main():
 
     # the (dominant) kernel the automatic dispatch runs for this shape (16-byte aligned rows)
     unit = 16 // ELEM_BYTES[args.dtype]
-    if N <= 128 and C * ELEM_BYTES[args.dtype] >= 96 * 1024:
+    if args.dtype == "f64":
+        tag = "fwl_rows_f64"
+    elif N <= 128 and C * ELEM_BYTES[args.dtype] >= 96 * 1024:
         tag = "fwl_split_chunks"
     elif (args.dtype == "f32" and N >= 384 and C >= 32000) or (N >= 512 and C >= 65536):
         tag = "fwl_two_pass"      # fwl_block_rows (candidate lists) + fwl_support_to_grad

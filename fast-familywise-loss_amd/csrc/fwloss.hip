@@ -29,6 +29,8 @@
 //                   tightened by fixed-point iterations on the list; a list that cannot be
 //                   tightened sends the row to the generic multi-pass path.
 //   fwl_mask_to_grad, fwl_cand_to_grad   the two-op backward of the drop-in interface.
+//   fwl_rows_f64    float64 logits: one wavefront per row, an LDS candidate list, fixed-point
+//                   iterations in fp64, a second stream of the row for the gradient.
 //   fwl_lin_*       the linear layer (LM head) fused with the loss: vocabulary chunks of logits
 //                   merged into per-row candidate lists, the threshold from the lists, and the
 //                   sparse gradients of hidden and weight.
