@@ -308,12 +308,17 @@ def main():
         tag = "fwl_rows_f64"
     elif N <= 128 and C * ELEM_BYTES[args.dtype] >= 96 * 1024:
         tag = "fwl_split_chunks"
-    elif (args.dtype == "f32" and N >= 384 and C >= 32000) or (N >= 512 and C >= 65536):
-        tag = "fwl_two_pass"      # fwl_block_rows (candidate lists) + fwl_support_to_grad
-    elif C % unit == 0 and C // unit <= 64:
+    elif (args.dtype == "f32" and ((N >= 384 and C >= 32000) or (C >= 8192 and N * C >= 48 << 20))) or \
+            (args.dtype != "f32" and N >= 512 and C >= 65536):
+        tag = "fwl_two_pass"      # the candidate-list read pass + fwl_fill_zero + fwl_scatter_support
+    elif (C % unit == 0 and C // unit <= 64) or (C % unit != 0 and C <= 128):
         tag = "fwl_seg_rows"
+    elif C <= 2048:
+        tag = "fwl_wave_rows"
+    elif C <= 8192 or (args.dtype != "f32" and C <= 28672 and N >= 1024):
+        tag = "fwl_wave_stream_rows"
     else:
-        tag = "fwl_wave_rows" if C <= 2048 else ("fwl_wave_stream_rows" if C <= 8192 else "fwl_block_rows")
+        tag = "fwl_block_rows"
     traffic = traffic_for(tag, cfg_tag if args.dtype == "f32" else f"{cfg_tag}_{args.dtype}")
     result = {
         "metric": METRIC,

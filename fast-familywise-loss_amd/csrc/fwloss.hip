@@ -3362,21 +3362,35 @@ size_t mean_ws_bytes(int64_t N) {
 
 // Whether the fused op may run in two passes (the long-row block path) under switch `path`.
 // Measured on MI355X against one pass (fp32): 8192 x 32000 423 -> 400 us, 2048 x 131072 378 ->
-// 357 us, 520 x 128256 132 -> 118 us, 400 x 50257 50.5 -> 46.8 us; but 256 x 128256 67 -> 79 us,
-// 6553 x 10000 119 -> 129 us, 4096 x 16384 110 -> 115 us and 3000 x 20000 102 -> 106 us (the read
-// pass runs below the read rate there).  bf16: 2048 x 131072 218 -> 190 us, but 8192 x 32000
-// 228 -> 264 us (its read pass is issue-bound at that length).  Automatic dispatch: rows of
-// >= 32000 elements, >= 384 of them, in fp32; rows of >= 65536 elements, >= 512 of them, in 16
-// bits.  Forced paths 2 and 3 always (their tests exercise both passes in every element type).
+// 357 us, 520 x 128256 132 -> 118 us, 400 x 50257 50.5 -> 46.8 us; but 256 x 128256 67 -> 79 us.
+// With the fill-and-scatter write pass, large fp32 batches of shorter rows gain too (256 MB of
+// logits): 8192 x 8192 102.0 -> 95.6 us, 5592 x 12000 113.5 -> 96.6, 4096 x 16384 106.2 -> 93.5,
+// 2796 x 24000 119.7 -> 106.8; at 128 MB they are even, below it one pass wins (16-64 MB: 18-36 us
+// against 22-43).  bf16: 2048 x 131072 218 -> 190 us, but 8192 x 32000 228 -> 264 us (its read
+// pass is issue-bound at that length).  Automatic dispatch: fp32 rows of >= 32000 elements, >= 384
+// of them, or of >= 8192 elements in batches of >= 48M elements; 16-bit rows of >= 65536
+// elements, >= 512 of them.  Forced paths 2 and 3 always (their tests exercise both passes in
+// every element type).
 constexpr int64_t kTwoPassMinC = 32000;
 constexpr int64_t kTwoPassMinRows = 384;
+constexpr int64_t kTwoPassMinCBig = 8192;
+constexpr int64_t kTwoPassMinElemsBig = (int64_t)48 << 20;
 constexpr int64_t kTwoPassMinC16 = 65536;
 constexpr int64_t kTwoPassMinRows16 = 512;
 bool two_pass_rows(int64_t N, int64_t C, int64_t elem, int path) {
   if (path == 2 || path == 3) return true;
   if (path != 0) return false;
-  return elem == 4 ? (C >= kTwoPassMinC && N >= kTwoPassMinRows) : (C >= kTwoPassMinC16 && N >= kTwoPassMinRows16);
+  if (elem == 4)
+    return (C >= kTwoPassMinC && N >= kTwoPassMinRows) || (C >= kTwoPassMinCBig && N * C >= kTwoPassMinElemsBig);
+  return C >= kTwoPassMinC16 && N >= kTwoPassMinRows16;
 }
+
+// 16-bit rows a little beyond kMaxStreamC stream faster on one wavefront each than on one block
+// each once there are enough rows (bf16, one wavefront per row against one block per row):
+// 5592 x 12000 65.7 us against 98.1, 4096 x 16384 61.7 against 79.7, 1198 x 28000 43.1 against
+// 50.3; below about 1024 rows, or at 32000 elements, one block per row wins.
+constexpr int kMaxStreamC16 = 28672;
+constexpr int64_t kStreamMinRows16 = 1024;
 
 // the two passes' scratch: cut candidate lists (values, indices), kappa and H per row
 size_t two_pass_bytes(int64_t N) {
@@ -3458,7 +3472,12 @@ int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scal
     path = 2;
   }
   if (path == 0 && !aligned_rows && C <= 128) path = 6;   // short unaligned rows: 32-bit segments
-  if (path == 0) path = C <= max_wave_c ? 6 : (C <= kMaxStreamC ? 4 : 2);
+  if (path == 0) {
+    const bool two_pass = MODE == kGrad && two_pass_rows(N, C, kElemBytes<T>, 0) && aligned(o.grad, 4) &&
+                          ws != nullptr && aligned(ws, 8) && ws_bytes >= mean_ws_bytes(N) + two_pass_bytes(N);
+    const bool stream = C <= kMaxStreamC || (kElemBytes<T> == 2 && C <= kMaxStreamC16 && N >= kStreamMinRows16);
+    path = C <= max_wave_c ? 6 : (two_pass ? 2 : (stream ? 4 : 2));
+  }
   if ((path == 1 || path == 6) && C > max_wave_c) path = 4;
   if (path == 6 && dispatch_seg<T, MODE>(z, y, N, C, aligned_rows, o, s)) return launch_status();
   if (path == 1 || path == 6) {

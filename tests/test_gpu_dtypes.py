@@ -62,6 +62,16 @@ def test_dtype_shapes(ext, dev, name, C):
 
 
 @pytest.mark.parametrize("name", sorted(DTYPES))
+@pytest.mark.parametrize("N,C", [(1024, 8193), (1100, 12000), (1030, 28672), (1023, 20000), (1500, 28673)])
+def test_dtype_long_rows_streamed(ext, dev, name, N, C):
+    """16-bit rows of 8193-28672 elements stream on one wavefront each from 1024 rows on (one block
+    per row below that and beyond 28672); both sides of both boundaries."""
+    z16, y = case(C, N, N + C, DTYPES[name])
+    print(f"{name} N={N} C={C}", flush=True)
+    check(ext, dev, z16, y)
+
+
+@pytest.mark.parametrize("name", sorted(DTYPES))
 @pytest.mark.parametrize("path,cap", [(1, 512), (2, 512), (2, 64), (3, 512), (4, 512), (4, 64), (5, 512), (6, 512)])
 def test_dtype_forced_paths(ext, dev, reset_params16, name, path, cap):
     z16, y = case(1000, 200, 77, DTYPES[name])
