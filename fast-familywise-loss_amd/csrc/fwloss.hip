@@ -2577,7 +2577,7 @@ __device__ __forceinline__ int filter_f64(double* v, int n, double t, int lane) 
 }
 
 // EVEN (C even): 128-bit accesses of two doubles; odd C: 64-bit accesses.
-template <bool EVEN>
+template <bool EVEN, int R>
 __global__ __launch_bounds__(kBlock) void fwl_rows_f64(const double* __restrict__ z, const int64_t* __restrict__ tgt,
                                                        int64_t N, int C, double scale, double* __restrict__ H,
                                                        double* __restrict__ loss, int32_t* __restrict__ kappa,
@@ -2595,8 +2595,9 @@ __global__ __launch_bounds__(kBlock) void fwl_rows_f64(const double* __restrict_
     int n = 0;
     bool over = false;
     const int slots = EVEN ? C / 2 : C;   // 128-bit units, or single doubles
-    for (int u0 = 0; u0 < slots; u0 += kWave * kF64Round) {
-      double x[2 * kF64Round];
+    // R > 0: the whole row in R rounds held in registers (no second read for the gradient)
+    double xr[R > 0 ? R : 1][2 * kF64Round];
+    auto round = [&](int u0, double* x) {
 #pragma unroll
       for (int q = 0; q < kF64Round; ++q) {
         const int u = u0 + lane + kWave * q;
@@ -2634,6 +2635,15 @@ __global__ __launch_bounds__(kBlock) void fwl_rows_f64(const double* __restrict_
         // the current bound sends the row to the whole-row iterations
         if (n > kF64Cap / 2) n = filter_f64(cl, n, t, lane);
         if (n > kF64Cap / 2) over = true;
+      }
+    };
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int rd = 0; rd < R; ++rd) round(rd * kWave * kF64Round, xr[rd]);
+    } else {
+      for (int u0 = 0; u0 < slots; u0 += kWave * kF64Round) {
+        double x[2 * kF64Round];
+        round(u0, x);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -2680,6 +2690,31 @@ __global__ __launch_bounds__(kBlock) void fwl_rows_f64(const double* __restrict_
     }
     const double inv = scale / (double)kap;
     const rsrc_t out = make_rsrc(grad + r * C, row_bytes);
+    if constexpr (R > 0) {
+#pragma unroll
+      for (int rd = 0; rd < R; ++rd) {
+#pragma unroll
+        for (int q = 0; q < kF64Round; ++q) {
+          const int u = rd * kWave * kF64Round + lane + kWave * q;   // past the row: dropped
+          const double x0 = xr[rd][2 * q], x1 = xr[rd][2 * q + 1];
+          double g0 = x0 > tau ? inv : 0.0, g1 = x1 > tau ? inv : 0.0;
+          if constexpr (EVEN) {
+            if (yok && 2 * u == y) g0 -= scale;
+            if (yok && 2 * u + 1 == y) g1 -= scale;
+            const uint64_t b0 = (uint64_t)__double_as_longlong(g0), b1 = (uint64_t)__double_as_longlong(g1);
+            __builtin_amdgcn_raw_buffer_store_b128(
+                v4u{(uint32_t)b0, (uint32_t)(b0 >> 32), (uint32_t)b1, (uint32_t)(b1 >> 32)}, out, 16u * (uint32_t)u, 0,
+                kNonTemporal);
+          } else {
+            if (yok && u == y) g0 -= scale;
+            const uint64_t b0 = (uint64_t)__double_as_longlong(g0);
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{(uint32_t)b0, (uint32_t)(b0 >> 32)}, out, 8u * (uint32_t)u, 0,
+                                                  kNonTemporal);
+          }
+        }
+      }
+      continue;
+    }
     for (int u = lane; u - lane < slots; u += kWave) {
       if constexpr (EVEN) {
         const v4u w = __builtin_amdgcn_raw_buffer_load_b128(row, 16u * (uint32_t)u, 0, kNonTemporal);
@@ -3525,12 +3560,24 @@ int forward_f64(const double* z, const int64_t* y, int64_t N, int64_t C, double 
       !aligned(mean, 8) || !aligned(kappa, 4))
     return FWL_ERR_ALIGNMENT;
   if (N > 0) {
-    if (C % 2 == 0)
-      hipLaunchKernelGGL((fwl_rows_f64<true>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, y, N, (int)C, scale, H,
-                         losses, kappa, grad);
-    else
-      hipLaunchKernelGGL((fwl_rows_f64<false>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, y, N, (int)C, scale, H,
-                         losses, kappa, grad);
+    // rows of up to 4 rounds stay in registers (512 doubles per round with 128-bit units, 256 with
+    // 64-bit ones)
+    const int per_round = (C % 2 == 0 ? 2 : 1) * kWave * kF64Round;
+    const int rounds = (int)((C + per_round - 1) / per_round);
+    const dim3 g(blocks_wave(N)), b(kBlock);
+#define FWL_F64(E, R) hipLaunchKernelGGL((fwl_rows_f64<E, R>), g, b, 0, s, z, y, N, (int)C, scale, H, losses, kappa, grad)
+    if (C % 2 == 0) {
+      if (rounds <= 1) FWL_F64(true, 1);
+      else if (rounds <= 2) FWL_F64(true, 2);
+      else if (rounds <= 4) FWL_F64(true, 4);
+      else FWL_F64(true, 0);
+    } else {
+      if (rounds <= 1) FWL_F64(false, 1);
+      else if (rounds <= 2) FWL_F64(false, 2);
+      else if (rounds <= 4) FWL_F64(false, 4);
+      else FWL_F64(false, 0);
+    }
+#undef FWL_F64
   }
   if (mean != nullptr) hipLaunchKernelGGL(fwl_mean_f64, dim3(1), dim3(kBlock), 0, s, losses, N, reduce_div, mean);
   return launch_status();
