@@ -29,495 +29,16 @@
 //                   tightened by fixed-point iterations on the list; a list that cannot be
 //                   tightened sends the row to the generic multi-pass path.
 //   fwl_mask_to_grad, fwl_cand_to_grad   the two-op backward of the drop-in interface.
-//   fwl_rows_f64    float64 logits: one wavefront per row, an LDS candidate list, fixed-point
-//                   iterations in fp64, a second stream of the row for the gradient.
-//   fwl_lin_*       the linear layer (LM head) fused with the loss: vocabulary chunks of logits
-//                   merged into per-row candidate lists, the threshold from the lists, and the
-//                   sparse gradients of hidden and weight.
+// Other sources of the library: fwl_f64.hip (float64 logits), fwl_linear.hip (the LM head fused
+// with the loss), fwl_common.h (what they share).
 // The mean loss is reduced in fp64 in a fixed order: per-block partial sums, then either the last
 // block sums them all (grids of up to 512 blocks) or per-group sums by the last block of each group
 // of 32 and the last group finisher sums the group sums (ticket counters in the caller's
 // workspace, each reset by its last user).
 //
-// Compile with -Xclang -target-feature -Xclang -packed-fp32-ops (see fwloss_build.py).
-#include <hip/hip_runtime.h>
-
-#include <math.h>
-#include <stdint.h>
-
-#include <map>
-#include <type_traits>
-#include <mutex>
-#include <utility>
-
-#include "fwloss.h"
+#include "fwl_common.h"
 
 namespace {
-
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-typedef unsigned v2u __attribute__((ext_vector_type(2)));
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-// Raw buffer resources (GFX9 layout): the hardware range check drops stores and zero-fills loads
-// past `bytes`, so every lane can issue the same unconditional instruction.  Memory instructions
-// under lane-dependent branches would make the compiler's wait counting fall back to draining all
-// outstanding stores at the top of each row.
-constexpr int kRsrcFlags = 0x00020000;
-constexpr int kNonTemporal = 2;   // cache-policy bits of the buffer instructions: nt
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kRsrcFlags);
-}
-
-// Element types of the logits (and of the gradient of the fused op): float, or the 16-bit tags
-// below.  Values are widened to fp32 exactly when loaded; every decision is taken in fp32/fp64;
-// gradient values are computed in fp32 and rounded to nearest-even when stored.
-struct bf16_t {};   // bfloat16, stored as uint16
-struct f16_t {};    // IEEE binary16, stored as uint16
-template <typename T> constexpr int kElemBytes = 2;
-template <> constexpr int kElemBytes<float> = 4;
-template <typename T> using Storage = typename std::conditional<std::is_same<T, float>::value, float, uint16_t>::type;
-
-// elements per lane access: a 128-bit unit (VEC) or a single element
-template <typename T, bool VEC> constexpr int kUnit = VEC ? 16 / kElemBytes<T> : 1;
-
-template <typename T>
-__device__ __forceinline__ float widen16(uint32_t h) {
-  if constexpr (std::is_same<T, bf16_t>::value) return __uint_as_float(h << 16);
-  else return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-}
-
-template <typename T>
-__device__ __forceinline__ uint32_t narrow16(float f) {
-  if constexpr (std::is_same<T, bf16_t>::value) {
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;   // NaN stays NaN (quiet)
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;                     // round to nearest even
-  } else {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
-  }
-}
-
-// unit `u` of a row (elements kUnit*u ...) as fp32; offsets past the resource read 0
-template <typename T, bool VEC>
-__device__ __forceinline__ void load_unit(rsrc_t r, uint32_t u, float* out) {
-  if constexpr (VEC) {
-    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, 16u * u, 0, kNonTemporal);
-    if constexpr (std::is_same<T, float>::value) {
-      out[0] = __uint_as_float(v.x);
-      out[1] = __uint_as_float(v.y);
-      out[2] = __uint_as_float(v.z);
-      out[3] = __uint_as_float(v.w);
-    } else {
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        out[2 * i] = widen16<T>(w[i] & 0xFFFFu);
-        out[2 * i + 1] = widen16<T>(w[i] >> 16);
-      }
-    }
-  } else if constexpr (std::is_same<T, float>::value) {
-    out[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, 4u * u, 0, kNonTemporal));
-  } else {
-    out[0] = widen16<T>(__builtin_amdgcn_raw_buffer_load_b16(r, 2u * u, 0, kNonTemporal));
-  }
-}
-
-// store unit `u` (kUnit values, rounded to T); offsets past the resource are dropped
-template <typename T, bool VEC>
-__device__ __forceinline__ void store_unit(rsrc_t r, uint32_t u, const float* v) {
-  if constexpr (VEC) {
-    v4u w;
-    if constexpr (std::is_same<T, float>::value) {
-      w = v4u{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
-    } else {
-      w = v4u{narrow16<T>(v[0]) | (narrow16<T>(v[1]) << 16), narrow16<T>(v[2]) | (narrow16<T>(v[3]) << 16),
-              narrow16<T>(v[4]) | (narrow16<T>(v[5]) << 16), narrow16<T>(v[6]) | (narrow16<T>(v[7]) << 16)};
-    }
-    __builtin_amdgcn_raw_buffer_store_b128(w, r, 16u * u, 0, kNonTemporal);
-  } else if constexpr (std::is_same<T, float>::value) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, 4u * u, 0, kNonTemporal);
-  } else {
-    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)narrow16<T>(v[0]), r, 2u * u, 0, kNonTemporal);
-  }
-}
-
-// bit pattern of an fp32 value in element type T (16-bit types: in the low half)
-template <typename T>
-__device__ __forceinline__ uint32_t encode(float f) {
-  if constexpr (std::is_same<T, float>::value) return __float_as_uint(f);
-  else return narrow16<T>(f);
-}
-
-// store unit `u` from already-encoded element bit patterns
-// (POL: cache policy; the non-temporal hint suits streams that read and write, a pure write
-// stream runs faster without it)
-template <typename T, bool VEC, int POL = kNonTemporal>
-__device__ __forceinline__ void store_unit_bits(rsrc_t r, uint32_t u, const uint32_t* b) {
-  if constexpr (VEC) {
-    v4u w;
-    if constexpr (std::is_same<T, float>::value) w = v4u{b[0], b[1], b[2], b[3]};
-    else w = v4u{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
-    __builtin_amdgcn_raw_buffer_store_b128(w, r, 16u * u, 0, POL);
-  } else if constexpr (std::is_same<T, float>::value) {
-    __builtin_amdgcn_raw_buffer_store_b32(b[0], r, 4u * u, 0, POL);
-  } else {
-    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)b[0], r, 2u * u, 0, POL);
-  }
-}
-
-// a zero unit (all-zero bits are +0 in every element type)
-template <typename T, bool VEC>
-__device__ __forceinline__ void store_zero_unit(rsrc_t r, uint32_t u) {
-  if constexpr (VEC) __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, r, 16u * u, 0, kNonTemporal);
-  else if constexpr (std::is_same<T, float>::value) __builtin_amdgcn_raw_buffer_store_b32(0u, r, 4u * u, 0, kNonTemporal);
-  else __builtin_amdgcn_raw_buffer_store_b16((uint16_t)0, r, 2u * u, 0, kNonTemporal);
-}
-
-// scalar element access through plain pointers (element index j)
-template <typename T>
-__device__ __forceinline__ float load_elem(const void* base, int64_t j) {
-  if constexpr (std::is_same<T, float>::value) return static_cast<const float*>(base)[j];
-  else return widen16<T>(static_cast<const uint16_t*>(base)[j]);
-}
-template <typename T>
-__device__ __forceinline__ void store_elem(void* base, int64_t j, float v) {
-  if constexpr (std::is_same<T, float>::value) static_cast<float*>(base)[j] = v;
-  else static_cast<uint16_t*>(base)[j] = (uint16_t)narrow16<T>(v);
-}
-
-constexpr int kWave = 64;
-constexpr int kWavesPerBlock = 4;
-constexpr int kBlock = kWave * kWavesPerBlock;
-constexpr int kMaxWaveC = 2048;        // longest row held in registers by one wavefront (128-bit rows)
-constexpr int kMaxWaveC1 = 1024;       // the same for rows accessed 32 bits at a time
-constexpr int kMaxStreamC = 8192;      // longest row streamed by one wavefront (longer: one block per row)
-constexpr int kCapMax = 512;           // LDS candidate slots per wavefront in fwl_block_rows
-constexpr int kMaxBlocksWave = 2048;   // grid cap of fwl_wave_rows (4 rows in flight per block)
-constexpr int kMaxBlocksRow = 4096;    // grid cap of fwl_block_rows
-constexpr int kStreamUnroll = 4;       // 128-bit loads per lane per streaming round
-constexpr int kRoundSlotsV1 = 16;      // 32-bit loads per lane per streaming round (unaligned rows)
-constexpr size_t kWsHeader = 256;      // the final ticket counter; then the mean's partial sums
-constexpr int kTicketGroup = 32;       // blocks per first-level ticket of the mean
-constexpr unsigned kOneTicketBlocks = 512;   // grids up to this size take a single ticket level
-                                             // (65536 x 1000, 512 blocks: 96.2 us against 96.9
-                                             // with two levels; 16384 x 100, 1280 blocks finishing
-                                             // together: 18.3 us against 10.0)
-constexpr int kTicketStride = 16;      // first-level tickets 64 bytes apart
-constexpr uint32_t kOffNone = 0x7FFFFFF0u;   // a buffer offset past every resource: access dropped
-
-enum Mode : int { kGrad = 0, kMask = 1, kCand = 2 };
-
-struct Outs {
-  float* H;
-  float* loss;
-  int32_t* kappa;
-  float* mean;
-  void* grad;   // element type of the logits
-  uint8_t* mask;
-  float* cval;
-  int32_t* cidx;
-  int32_t* ccnt;
-  double scale;        // gradient scale (1/N for the mean reduction)
-  double reduce_div;   // mean = sum(losses) / reduce_div
-  float scale_f;
-  unsigned* ticket;     // final ticket
-  double* partials;     // one per block
-  double* gpartials;    // one per group of kTicketGroup blocks
-  unsigned* gtickets;   // one per group (kTicketStride apart)
-  int force_generic;
-  int cap;             // LDS candidate capacity per wavefront (<= kCapMax)
-  int cstride;         // candidate-list mode: row stride of cval/cidx (C for the drop-in op)
-  int ccap;            // candidate-list mode: entries kept per row (further ones are dropped)
-};
-
-// ------------------------------------------------------------------------------------------------
-// wavefront primitives (all lanes of the wavefront must be active when these are called)
-
-__device__ __forceinline__ int lane_id() {
-  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-}
-
-__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
-
-__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
-
-// number of set bits of b in lanes below this one
-__device__ __forceinline__ int rank_in(uint64_t b) {
-  return __builtin_amdgcn_mbcnt_hi((unsigned)(b >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)b, 0u));
-}
-
-// DPP controls (GFX9 encoding)
-constexpr int kQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
-constexpr int kQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
-constexpr int kRowRor8 = 0x128;       // row_ror:8  (lane ^ 8 inside a row of 16)
-constexpr int kRowMirror = 0x140;     // lane 15 - i inside a row of 16
-constexpr int kRowHalfMirror = 0x141; // lane 7 - i inside a half row of 8
-constexpr int kRowBcast15 = 0x142;    // lane 15 of each row to the next row
-constexpr int kRowBcast31 = 0x143;    // lane 31 to rows 2 and 3
-
-template <int CTRL>
-__device__ __forceinline__ int dpp_mov(int x) {
-  return __builtin_amdgcn_mov_dpp(x, CTRL, 0xF, 0xF, false);
-}
-
-// lanes whose DPP source is out of range (or whose row is masked off) read 0
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ int dpp_or0(int x) {
-  return __builtin_amdgcn_update_dpp(0, x, CTRL, ROW_MASK, 0xF, false);
-}
-
-template <int CTRL>
-__device__ __forceinline__ double dpp_mov_f64(double v) {
-  const int64_t b = __double_as_longlong(v);
-  const int lo = dpp_mov<CTRL>((int)b);
-  const int hi = dpp_mov<CTRL>((int)(b >> 32));
-  return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
-}
-
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ double dpp_or0_f64(double v) {
-  const int64_t b = __double_as_longlong(v);
-  const int lo = dpp_or0<CTRL, ROW_MASK>((int)b);
-  const int hi = dpp_or0<CTRL, ROW_MASK>((int)(b >> 32));
-  return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
-}
-
-__device__ __forceinline__ double readlane_f64(double v, int l) {
-  const int64_t b = __double_as_longlong(v);
-  const int lo = __builtin_amdgcn_readlane((int)b, l);
-  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
-  return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
-}
-
-// partner value of lane ^ M, without LDS: DPP inside rows of 16 lanes, the gfx950 permlane swaps
-// across rows (v_permlane16_swap / v_permlane32_swap with both operands x return, per lane, the
-// value of the other row / half in r[1] for the lower and r[0] for the upper one)
-template <int M>
-__device__ __forceinline__ float xor_lane(float v, int lane) {
-  const int x = __float_as_int(v);
-  if constexpr (M == 1) return __int_as_float(dpp_mov<kQuadXor1>(x));
-  else if constexpr (M == 2) return __int_as_float(dpp_mov<kQuadXor2>(x));
-  else if constexpr (M == 4) {
-    const int up = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0xF, false);   // row_shl:4
-    const int dn = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);   // row_shr:4
-    return __int_as_float((lane & 4) ? dn : up);
-  } else if constexpr (M == 8) return __int_as_float(dpp_mov<kRowRor8>(x));
-  else if constexpr (M == 16) {
-    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
-    return __int_as_float((lane & 16) ? r[0] : r[1]);
-  } else {
-    static_assert(M == 32, "xor distance");
-    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-    return __int_as_float((lane & 32) ? r[0] : r[1]);
-  }
-}
-
-// per-lane select with a wavefront-constant lane mask held in SGPRs (one v_cndmask)
-__device__ __forceinline__ float select_lanes(uint64_t mask, float if_set, float if_clear) {
-  float r;
-  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(if_clear), "v"(if_set), "s"(mask));
-  return r;
-}
-
-// maximum over the wavefront, returned in every lane (wavefront-uniform)
-__device__ __forceinline__ float wave_max_f32(float v) {
-  v = fmaxf(v, __int_as_float(dpp_mov<kQuadXor1>(__float_as_int(v))));
-  v = fmaxf(v, __int_as_float(dpp_mov<kQuadXor2>(__float_as_int(v))));
-  v = fmaxf(v, __int_as_float(dpp_mov<kRowHalfMirror>(__float_as_int(v))));
-  v = fmaxf(v, __int_as_float(dpp_mov<kRowMirror>(__float_as_int(v))));
-  const int x = __float_as_int(v);
-  const float a = __int_as_float(__builtin_amdgcn_readlane(x, 0));
-  const float b = __int_as_float(__builtin_amdgcn_readlane(x, 16));
-  const float c = __int_as_float(__builtin_amdgcn_readlane(x, 32));
-  const float d = __int_as_float(__builtin_amdgcn_readlane(x, 48));
-  return fmaxf(fmaxf(a, b), fmaxf(c, d));
-}
-
-// fp64 sum over the wavefront in a fixed order, returned in every lane
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  v += dpp_mov_f64<kQuadXor1>(v);
-  v += dpp_mov_f64<kQuadXor2>(v);
-  v += dpp_mov_f64<kRowHalfMirror>(v);
-  v += dpp_mov_f64<kRowMirror>(v);
-  return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
-}
-
-__device__ __forceinline__ double wave_max_f64(double v) {
-  v = fmax(v, dpp_mov_f64<kQuadXor1>(v));
-  v = fmax(v, dpp_mov_f64<kQuadXor2>(v));
-  v = fmax(v, dpp_mov_f64<kRowHalfMirror>(v));
-  v = fmax(v, dpp_mov_f64<kRowMirror>(v));
-  return fmax(fmax(readlane_f64(v, 0), readlane_f64(v, 16)), fmax(readlane_f64(v, 32), readlane_f64(v, 48)));
-}
-
-// one compare-exchange step of a bitonic network sorting groups of K lanes (descending where
-// lane & K == 0); the lanes keeping the maximum form a constant mask
-constexpr uint64_t keep_max_mask(int K, int J) {
-  uint64_t m = 0;
-  for (int i = 0; i < 64; ++i)
-    if (((i & J) == 0) == ((i & K) == 0)) m |= 1ull << i;
-  return m;
-}
-
-template <int K, int J>
-__device__ __forceinline__ float bitonic_step(float v, int lane) {
-  const float p = xor_lane<J>(v, lane);
-  return select_lanes(keep_max_mask(K, J), fmaxf(v, p), fminf(v, p));
-}
-
-template <int K>
-__device__ __forceinline__ float bitonic_merge(float v, int lane) {
-  if constexpr (K >= 64) v = bitonic_step<K, 32>(v, lane);
-  if constexpr (K >= 32) v = bitonic_step<K, 16>(v, lane);
-  if constexpr (K >= 16) v = bitonic_step<K, 8>(v, lane);
-  if constexpr (K >= 8) v = bitonic_step<K, 4>(v, lane);
-  if constexpr (K >= 4) v = bitonic_step<K, 2>(v, lane);
-  return bitonic_step<K, 1>(v, lane);
-}
-
-// Order-preserving integer key of a float that is not NaN: signed comparison of keys orders the
-// values (-0.0 just below +0.0).  The map is its own inverse.  Integer max/min need no NaN
-// quieting, so a compare-exchange is a DPP max, a DPP min and one select.
-__device__ __forceinline__ int fkey(float v) {
-  const int b = __float_as_int(v);
-  return b ^ ((b >> 31) & 0x7FFFFFFF);
-}
-__device__ __forceinline__ float fkey_inv(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7FFFFFFF)); }
-
-// partner of lane ^ M for integer values; lane ^ 4 takes two bank-masked DPP moves (banks 0 and 2
-// of each row, lanes with bit 2 clear, read lane + 4 = row_ror:12; banks 1 and 3 read lane - 4 =
-// row_ror:4)
-template <int M>
-__device__ __forceinline__ int xor_lane_i(int x, int lane) {
-  if constexpr (M == 1) return dpp_mov<kQuadXor1>(x);
-  else if constexpr (M == 2) return dpp_mov<kQuadXor2>(x);
-  else if constexpr (M == 4) {
-    const int a = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0x5, false);
-    return __builtin_amdgcn_update_dpp(a, x, 0x124, 0xF, 0xA, false);
-  } else if constexpr (M == 8) return dpp_mov<kRowRor8>(x);
-  else return __float_as_int(xor_lane<M>(__int_as_float(x), lane));
-}
-
-__device__ __forceinline__ int select_lanes_i(uint64_t mask, int if_set, int if_clear) {
-  int r;
-  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(if_clear), "v"(if_set), "s"(mask));
-  return r;
-}
-
-template <int K, int J>
-__device__ __forceinline__ int bitonic_step_i(int v, int lane) {
-  const int p = xor_lane_i<J>(v, lane);
-  return select_lanes_i(keep_max_mask(K, J), max(v, p), min(v, p));
-}
-
-template <int K>
-__device__ __forceinline__ int bitonic_merge_i(int v, int lane) {
-  if constexpr (K >= 64) v = bitonic_step_i<K, 32>(v, lane);
-  if constexpr (K >= 32) v = bitonic_step_i<K, 16>(v, lane);
-  if constexpr (K >= 16) v = bitonic_step_i<K, 8>(v, lane);
-  if constexpr (K >= 8) v = bitonic_step_i<K, 4>(v, lane);
-  if constexpr (K >= 4) v = bitonic_step_i<K, 2>(v, lane);
-  return bitonic_step_i<K, 1>(v, lane);
-}
-
-// sort the keys of lanes [0, T) descending (T = 16, 32 or 64)
-template <int T>
-__device__ __forceinline__ int sort_desc_i(int v, int lane) {
-  v = bitonic_merge_i<2>(v, lane);
-  v = bitonic_merge_i<4>(v, lane);
-  v = bitonic_merge_i<8>(v, lane);
-  v = bitonic_merge_i<16>(v, lane);
-  if constexpr (T >= 32) v = bitonic_merge_i<32>(v, lane);
-  if constexpr (T >= 64) v = bitonic_merge_i<64>(v, lane);
-  return v;
-}
-
-// DPP move whose lanes without a source (shifted in past the row edge) read 0
-template <int CTRL>
-__device__ __forceinline__ double dpp_zero_f64(double v) {
-  const int64_t b = __double_as_longlong(v);
-  const int lo = __builtin_amdgcn_mov_dpp((int)b, CTRL, 0xF, 0xF, true);
-  const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), CTRL, 0xF, 0xF, true);
-  return __longlong_as_double((int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo));
-}
-
-// inclusive prefix sum over lanes [0, T)
-template <int T>
-__device__ __forceinline__ double scan_f64(double v) {
-  v += dpp_zero_f64<0x111>(v);          // row_shr:1
-  v += dpp_zero_f64<0x112>(v);          // row_shr:2
-  v += dpp_zero_f64<0x114>(v);          // row_shr:4
-  v += dpp_zero_f64<0x118>(v);          // row_shr:8
-  if constexpr (T >= 32) v += dpp_or0_f64<kRowBcast15, 0xA>(v);   // rows 1, 3 += last lane of 0, 2
-  if constexpr (T >= 64) v += dpp_or0_f64<kRowBcast31, 0xC>(v);   // rows 2, 3 += lane 31
-  return v;
-}
-
-// largest float <= t (so that x > t <=> x > rd32(t) for every float x; fw_cpu.cpp:96-101)
-__device__ __forceinline__ float rd32(double t) {
-  float r = (float)t;
-  if ((double)r > t) {
-    unsigned b = __float_as_uint(r);
-    if (r > 0.0f) b -= 1u;
-    else if (r < 0.0f) b += 1u;
-    else b = 0x80000001u;
-    r = __uint_as_float(b);
-  }
-  return r;
-}
-
-// next float / double below a finite value
-__device__ __forceinline__ float prev_f32(float r) {
-  unsigned b = __float_as_uint(r);
-  if (r > 0.0f) b -= 1u;
-  else if (r < 0.0f) b += 1u;
-  else b = 0x80000001u;
-  return __uint_as_float(b);
-}
-__device__ __forceinline__ double prev_f64(double r) {
-  uint64_t b = (uint64_t)__double_as_longlong(r);
-  if (r > 0.0) b -= 1u;
-  else if (r < 0.0) b += 1u;
-  else b = 0x8000000000000001ull;
-  return __longlong_as_double((int64_t)b);
-}
-
-// largest float <= m - 1 (tau >= m - 1, so every support entry is > this bound).  For |m| >= 2^53
-// the fp64 subtraction loses the 1; the float below m is then the answer.
-__device__ __forceinline__ float bound_below_max(float m) {
-  const float t = rd32((double)m - 1.0);
-  return (t >= m && isfinite(m)) ? prev_f32(m) : t;
-}
-
-// tau < max always; fp64 rounding can only violate this when the 1 of S - 1 is lost (|z| >= 2^53)
-__device__ __forceinline__ double clamp_below_max(double tau, float m) {
-  return (tau >= (double)m && isfinite(m)) ? prev_f64((double)m) : tau;
-}
-
-// tau of a candidate set held one value per lane in lanes [0, n), 1 <= n <= T <= 64: sort
-// descending, S_k = fp64 prefix sums; tau = max_k (S_k - 1)/k (reference_impl.py:17-21).  The
-// maximising k is the support size: k z_(k) > S_k - 1 holds exactly for k = 1 .. kappa (the
-// sparsemax support condition; both sides are exact in fp64 whenever S_k is), so one division
-// gives tau = (S_kappa - 1)/kappa.  Rounding is monotone, so this is the largest of the rounded
-// (S_k - 1)/k.
-template <int T>
-__device__ __forceinline__ double select_tier(float c, int n, int lane) {
-  int key = fkey(lane < n ? c + 0.0f : -INFINITY);   // + 0.0f: -0.0 -> +0.0
-  key = sort_desc_i<T>(key, lane);
-  const float v = fkey_inv(key);
-  const double S = scan_f64<T>(lane < n ? (double)v : 0.0);
-  const uint64_t in = ballot(lane < n && (double)v * (double)(lane + 1) > S - 1.0);
-  int kap = 64 - (int)__builtin_clzll(in | 1ull);   // the highest k that satisfies it (>= 1)
-  kap = uniform(kap);
-  return (readlane_f64(S, kap - 1) - 1.0) / (double)kap;
-}
-
-__device__ __forceinline__ double select_small(float c, int n, int lane) {
-  if (n <= 16) return select_tier<16>(c, n, lane);
-  if (n <= 32) return select_tier<32>(c, n, lane);
-  return select_tier<64>(c, n, lane);
-}
 
 // ------------------------------------------------------------------------------------------------
 // mean of the per-row losses: block partial sums, the last block reduces them (fixed order)
@@ -632,21 +153,6 @@ __device__ __forceinline__ int slot_index(int i, int lane) {
   return U * (lane + kWave * (i / U)) + (i % U);
 }
 
-// sum/count over the first n entries of one wavefront's list, entries > thr
-__device__ __forceinline__ void list_sum_count(const float* bv, int n, float thr, int lane, double& s,
-                                               int& c) {
-  double acc = 0.0;
-  int cnt = 0;
-  for (int p0 = 0; p0 < n; p0 += kWave) {
-    const int p = p0 + lane;
-    const float v = p < n ? bv[p] : -INFINITY;
-    const bool k = v > thr;
-    acc += k ? (double)v : 0.0;
-    cnt += __popcll(ballot(k));
-  }
-  s = wave_sum_f64(acc);
-  c = cnt;
-}
 
 // element j of the register row (j wavefront-uniform, 0 <= j < C): the uniform slot index makes
 // the register array access an indexed register move (s_set_gpr_idx), then one lane read
@@ -671,47 +177,6 @@ __device__ __forceinline__ int wave_excl_scan_i32(int v, int& total) {
   return s - v;
 }
 
-// tau, kappa and (for n <= 64) the support bits of a candidate list cl[0, n) that holds every row
-// entry > t0 (t0 <= tau, e.g. the largest float <= max - 1) and whose largest entry is the row
-// maximum m.  Up to 64 entries: one per lane, sorted across the wavefront, fp64 prefix sums,
-// tau = max_k (S_k - 1)/k.  Longer lists: fixed-point iterations t <- H({z > t}) from t0 (each
-// iterate is <= tau and the set shrinks every step until it is {z > tau}).
-__device__ __forceinline__ void resolve_list(const float* cl, int n, float t0, float m, int lane, double& tau,
-                                             int& kappa, uint64_t& support) {
-  tau = NAN;
-  kappa = 0;
-  support = 0;
-  if (n > 0 && n <= kWave) {
-    const float c = lane < n ? cl[lane] : -INFINITY;
-    tau = clamp_below_max(select_small(c, n, lane), m);
-    support = ballot(lane < n && c > rd32(tau));
-    kappa = __popcll(support);
-  } else if (n > kWave) {
-    double t = (double)t0, s;
-    int c;
-    list_sum_count(cl, n, t0, lane, s, c);
-    for (int it = 0; it <= n + 1; ++it) {
-      const double tn = (s - 1.0) / (double)c;
-      double s2;
-      int c2;
-      list_sum_count(cl, n, rd32(tn), lane, s2, c2);
-      if (c2 == c || !(tn > t)) {
-        tau = tn;
-        kappa = c2;
-        break;
-      }
-      t = tn;
-      s = s2;
-      c = c2;
-    }
-    const double tc = clamp_below_max(tau, m);
-    if (tc != tau) {
-      double s3;
-      tau = tc;
-      list_sum_count(cl, n, rd32(tau), lane, s3, kappa);
-    }
-  }
-}
 
 struct RowResult {
   float H;
@@ -2498,667 +1963,11 @@ __global__ void fwl_empty_mean(float* mean, double reduce_div) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// fp64 logits (the reference CPU path's second dtype, src/cpu/fw_cpu.cpp:697-703): one wavefront per
-// row.  The row is streamed once for its candidates z > (running max) - 1, kept in LDS; tau comes
-// from fixed-point iterations t <- H({z > t}) on that list (Michelot), every sum in fp64 in a fixed
-// order; a second stream of the row writes the gradient.  Rows whose candidates do not fit in the
-// list run the same iterations over the whole row.
-
-constexpr int kF64Cap = 1024;    // LDS candidates per wavefront (a round adds at most 512)
-constexpr int kF64Round = 4;     // 128-bit units (two doubles) per lane per streaming round
-
-// largest double <= m - 1 (the subtraction's rounding error from TwoSum)
-__device__ __forceinline__ double bound_below_max_f64(double m) {
-  const double s = m - 1.0;
-  const double bp = s - m, ap = s - bp;
-  const double e = (m - ap) + (-1.0 - bp);   // m - 1 == s + e exactly
-  double t = e < 0.0 ? prev_f64(s) : s;
-  if (t >= m && isfinite(m)) t = prev_f64(m);   // |m| >= 2^53: the 1 is lost
-  return t;
-}
-
-__device__ __forceinline__ void sum_count_f64(const double* v, int n, double t, int lane, double& s, int& c) {
-  double acc = 0.0;
-  int cnt = 0;
-  for (int p0 = 0; p0 < n; p0 += kWave) {
-    const int p = p0 + lane;
-    const double x = p < n ? v[p] : -INFINITY;
-    const bool k = x > t;
-    acc += k ? x : 0.0;
-    cnt += __popcll(ballot(k));
-  }
-  s = wave_sum_f64(acc);
-  c = cnt;
-}
-
-// two doubles of a 128-bit unit, one of a 64-bit unit
-__device__ __forceinline__ double lo_f64(v4u w) { return __longlong_as_double((int64_t)(((uint64_t)w.y << 32) | w.x)); }
-__device__ __forceinline__ double hi_f64(v4u w) { return __longlong_as_double((int64_t)(((uint64_t)w.w << 32) | w.z)); }
-__device__ __forceinline__ double one_f64(v2u w) { return __longlong_as_double((int64_t)(((uint64_t)w.y << 32) | w.x)); }
-
-// sum and count of the row entries > t (a stream of the row; EVEN: 128-bit units of two doubles)
-template <bool EVEN>
-__device__ __forceinline__ void row_sum_count_f64(rsrc_t row, int C, double t, int lane, double& s, int& c) {
-  const int slots = EVEN ? C / 2 : C;
-  double acc = 0.0;
-  int cnt = 0;
-  for (int u = lane; u - lane < slots; u += kWave) {
-    double x0, x1 = -INFINITY;
-    if constexpr (EVEN) {
-      const v4u w = __builtin_amdgcn_raw_buffer_load_b128(row, 16u * (uint32_t)u, 0, kNonTemporal);
-      x0 = u < slots ? lo_f64(w) : -INFINITY;
-      x1 = u < slots ? hi_f64(w) : -INFINITY;
-    } else {
-      const v2u w = __builtin_amdgcn_raw_buffer_load_b64(row, 8u * (uint32_t)u, 0, kNonTemporal);
-      x0 = u < slots ? one_f64(w) : -INFINITY;
-    }
-    acc += x0 > t ? x0 : 0.0;
-    acc += x1 > t ? x1 : 0.0;
-    cnt += (x0 > t) + (x1 > t);
-  }
-  s = wave_sum_f64(acc);
-  c = (int)wave_sum_f64((double)cnt);
-}
-
-// Stable in-place compaction of an fp64 candidate list to its entries > t.
-__device__ __forceinline__ int filter_f64(double* v, int n, double t, int lane) {
-  int out = 0;
-  for (int p0 = 0; p0 < n; p0 += kWave) {
-    const int p = p0 + lane;
-    const double x = p < n ? v[p] : -INFINITY;
-    const bool keep = x > t;
-    const uint64_t b = ballot(keep);
-    __builtin_amdgcn_wave_barrier();
-    if (keep) v[out + rank_in(b)] = x;
-    out += __popcll(b);
-    __builtin_amdgcn_wave_barrier();
-  }
-  return out;
-}
-
-// EVEN (C even): 128-bit accesses of two doubles; odd C: 64-bit accesses.
-template <bool EVEN, int R>
-__global__ __launch_bounds__(kBlock) void fwl_rows_f64(const double* __restrict__ z, const int64_t* __restrict__ tgt,
-                                                       int64_t N, int C, double scale, double* __restrict__ H,
-                                                       double* __restrict__ loss, int32_t* __restrict__ kappa,
-                                                       double* __restrict__ grad) {
-  __shared__ double s_val[kWavesPerBlock][kF64Cap];
-  const int lane = lane_id();
-  const int wid = uniform((int)(threadIdx.x >> 6));
-  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
-  double* cl = s_val[wid];
-  const uint32_t row_bytes = (uint32_t)(8 * C);
-  for (int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid; r < N; r += stride) {
-    const rsrc_t row = make_rsrc(z + r * C, row_bytes);
-    // pass 1: candidates above the running bound
-    double m = -INFINITY, t = -INFINITY;
-    int n = 0;
-    bool over = false;
-    const int slots = EVEN ? C / 2 : C;   // 128-bit units, or single doubles
-    // R > 0: the whole row in R rounds held in registers (no second read for the gradient)
-    double xr[R > 0 ? R : 1][2 * kF64Round];
-    auto round = [&](int u0, double* x) {
-#pragma unroll
-      for (int q = 0; q < kF64Round; ++q) {
-        const int u = u0 + lane + kWave * q;
-        if constexpr (EVEN) {
-          const v4u w = __builtin_amdgcn_raw_buffer_load_b128(row, 16u * (uint32_t)u, 0, kNonTemporal);
-          x[2 * q] = u < slots ? lo_f64(w) : -INFINITY;
-          x[2 * q + 1] = u < slots ? hi_f64(w) : -INFINITY;
-        } else {
-          const v2u w = __builtin_amdgcn_raw_buffer_load_b64(row, 8u * (uint32_t)u, 0, kNonTemporal);
-          x[2 * q] = u < slots ? one_f64(w) : -INFINITY;
-          x[2 * q + 1] = -INFINITY;
-        }
-      }
-      double lm = x[0];
-#pragma unroll
-      for (int i = 1; i < 2 * kF64Round; ++i) lm = fmax(lm, x[i]);
-      const double wm = wave_max_f64(lm);
-      if (wm > m) {
-        m = wm;
-        t = bound_below_max_f64(m);
-      }
-      if (!over) {
-#pragma unroll
-        for (int i = 0; i < 2 * kF64Round; ++i) {
-          const bool c = x[i] > t;
-          const uint64_t b = ballot(c);
-          if (b != 0) {
-            const int at = n + rank_in(b);
-            if (c && at < kF64Cap) cl[at] = x[i];
-            n += __popcll(b);
-          }
-        }
-        __builtin_amdgcn_wave_barrier();
-        // at most kF64Cap / 2 entries before a round, so nothing is dropped; more than that above
-        // the current bound sends the row to the whole-row iterations
-        if (n > kF64Cap / 2) n = filter_f64(cl, n, t, lane);
-        if (n > kF64Cap / 2) over = true;
-      }
-    };
-    if constexpr (R > 0) {
-#pragma unroll
-      for (int rd = 0; rd < R; ++rd) round(rd * kWave * kF64Round, xr[rd]);
-    } else {
-      for (int u0 = 0; u0 < slots; u0 += kWave * kF64Round) {
-        double x[2 * kF64Round];
-        round(u0, x);
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-    if (!over) n = filter_f64(cl, n, t, lane);
-    // tau by t <- H({z > t}) from t <= tau: each iterate is <= tau and the set shrinks until it is
-    // the support (on the list, or on the whole row when the list overflowed)
-    double tau = NAN;
-    int kap = 0;
-    if (over || n > 0) {
-      double s;
-      int c;
-      if (over) row_sum_count_f64<EVEN>(row, C, t, lane, s, c);
-      else sum_count_f64(cl, n, t, lane, s, c);
-      for (int it = 0; it <= C + 1; ++it) {
-        const double tn = (s - 1.0) / (double)c;
-        double s2;
-        int c2;
-        if (over) row_sum_count_f64<EVEN>(row, C, tn, lane, s2, c2);
-        else sum_count_f64(cl, n, tn, lane, s2, c2);
-        if (c2 == c || !(tn > t) || c2 == 0) {
-          tau = tn;
-          kap = c2;
-          break;
-        }
-        t = tn;
-        s = s2;
-        c = c2;
-      }
-      if (tau >= m && isfinite(m)) {   // tau < max always (fp64 loses the 1 only for |z| >= 2^53)
-        tau = prev_f64(m);
-        double s3;
-        if (over) row_sum_count_f64<EVEN>(row, C, tau, lane, s3, kap);
-        else sum_count_f64(cl, n, tau, lane, s3, kap);
-      }
-    }
-    // outputs and pass 2: the gradient
-    const int64_t y = tgt[r];
-    const bool yok = y >= 0 && y < C;
-    const double zy = yok ? z[r * C + y] : NAN;
-    if (lane == 0) {
-      if (H) H[r] = tau;
-      if (loss) loss[r] = yok ? (1.0 - zy) + tau : NAN;
-      if (kappa) kappa[r] = kap;
-    }
-    const double inv = scale / (double)kap;
-    const rsrc_t out = make_rsrc(grad + r * C, row_bytes);
-    if constexpr (R > 0) {
-#pragma unroll
-      for (int rd = 0; rd < R; ++rd) {
-#pragma unroll
-        for (int q = 0; q < kF64Round; ++q) {
-          const int u = rd * kWave * kF64Round + lane + kWave * q;   // past the row: dropped
-          const double x0 = xr[rd][2 * q], x1 = xr[rd][2 * q + 1];
-          double g0 = x0 > tau ? inv : 0.0, g1 = x1 > tau ? inv : 0.0;
-          if constexpr (EVEN) {
-            if (yok && 2 * u == y) g0 -= scale;
-            if (yok && 2 * u + 1 == y) g1 -= scale;
-            const uint64_t b0 = (uint64_t)__double_as_longlong(g0), b1 = (uint64_t)__double_as_longlong(g1);
-            __builtin_amdgcn_raw_buffer_store_b128(
-                v4u{(uint32_t)b0, (uint32_t)(b0 >> 32), (uint32_t)b1, (uint32_t)(b1 >> 32)}, out, 16u * (uint32_t)u, 0,
-                kNonTemporal);
-          } else {
-            if (yok && u == y) g0 -= scale;
-            const uint64_t b0 = (uint64_t)__double_as_longlong(g0);
-            __builtin_amdgcn_raw_buffer_store_b64(v2u{(uint32_t)b0, (uint32_t)(b0 >> 32)}, out, 8u * (uint32_t)u, 0,
-                                                  kNonTemporal);
-          }
-        }
-      }
-      continue;
-    }
-    for (int u = lane; u - lane < slots; u += kWave) {
-      if constexpr (EVEN) {
-        const v4u w = __builtin_amdgcn_raw_buffer_load_b128(row, 16u * (uint32_t)u, 0, kNonTemporal);
-        const double x0 = lo_f64(w), x1 = hi_f64(w);
-        double g0 = x0 > tau ? inv : 0.0, g1 = x1 > tau ? inv : 0.0;
-        if (yok && 2 * u == y) g0 -= scale;
-        if (yok && 2 * u + 1 == y) g1 -= scale;
-        const uint64_t b0 = (uint64_t)__double_as_longlong(g0), b1 = (uint64_t)__double_as_longlong(g1);
-        __builtin_amdgcn_raw_buffer_store_b128(v4u{(uint32_t)b0, (uint32_t)(b0 >> 32), (uint32_t)b1, (uint32_t)(b1 >> 32)},
-                                               out, 16u * (uint32_t)u, 0, kNonTemporal);
-      } else {
-        const v2u w = __builtin_amdgcn_raw_buffer_load_b64(row, 8u * (uint32_t)u, 0, kNonTemporal);
-        const double x0 = one_f64(w);
-        double g0 = x0 > tau ? inv : 0.0;
-        if (yok && u == y) g0 -= scale;
-        const uint64_t b0 = (uint64_t)__double_as_longlong(g0);
-        __builtin_amdgcn_raw_buffer_store_b64(v2u{(uint32_t)b0, (uint32_t)(b0 >> 32)}, out, 8u * (uint32_t)u, 0,
-                                              kNonTemporal);
-      }
-    }
-  }
-}
-
-// mean = sum(losses) / reduce_div in a fixed order (one block)
-__global__ __launch_bounds__(kBlock) void fwl_mean_f64(const double* __restrict__ loss, int64_t N, double reduce_div,
-                                                       double* __restrict__ mean) {
-  __shared__ double s_red[kBlock];
-  double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < N; i += kBlock) acc += loss[i];
-  s_red[threadIdx.x] = acc;
-  __syncthreads();
-  for (int s = kBlock / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) s_red[threadIdx.x] += s_red[threadIdx.x + s];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) *mean = s_red[0] / reduce_div;
-}
-
-// grad[r, :] *= grad_output[r * go_stride] (fp64) for rows whose factor is not 1
-__global__ __launch_bounds__(kBlock) void fwl_scale_rows_f64(double* __restrict__ grad, const double* __restrict__ go,
-                                                             int64_t go_stride, int64_t N, int C) {
-  const int lane = lane_id();
-  const int wid = uniform((int)(threadIdx.x >> 6));
-  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
-  for (int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid; r < N; r += stride) {
-    const double s = go[r * go_stride];
-    if (s == 1.0) continue;
-    for (int j = lane; j < C; j += kWave) grad[r * C + j] *= s;
-  }
-}
-
-// ------------------------------------------------------------------------------------------------
-// The linear layer that produces the logits, fused with the loss: logits = hidden @ weight^T
-// arrive one vocabulary chunk at a time ([N, Vc] for columns v0 .. v0 + Vc - 1), and no [N, V]
-// logits tensor ever exists.  Per row a state in device memory carries, from chunk to chunk, the
-// running maximum m, a lower bound t <= tau (max(m - 1, H(list)) rounded down) and the list of
-// every entry seen so far that is > t (value and column).  Every support entry of the full row is
-// > t at every step, so after the last chunk the list holds the support and the row maximum, and
-// the threshold is resolved on it exactly as for a materialised row.  Rows whose list outgrows
-// kLinCap entries above the bound (or a chunk's kLinLds), and rows without a finite maximum, are
-// flagged; the caller runs them through the materialised path.
-//
-// The gradient of the loss with respect to the logits has kappa + 1 non-zeros per row, so the
-// backward needs no GEMM: dhidden[n] = sum_j g_nj weight[j] (a gather of kappa + 1 weight rows)
-// and dweight[j] = sum_n g_nj hidden[n] (one pass over (column, row) entries sorted by column).
-
-constexpr int kLinCap = 256;           // list entries a row keeps between chunks
-constexpr int kLinLds = 1024;          // LDS list entries per wavefront while a chunk streams
-constexpr int kLinRound = 2;           // 128-bit units per lane per streaming round
-constexpr int kLinHeader = 32;         // bytes of a row's state header
-constexpr int64_t kLinRowBytes = kLinHeader + 8 * kLinCap;
-constexpr int kLinOverflow = 1;        // header flag: the row takes the materialised path
-
-struct LinHead {
-  float m;      // running maximum
-  float t;      // lower bound of tau: every support entry is > t
-  int n;        // list entries
-  float zy;     // the label's logit (NaN until its chunk arrives)
-  int flags;
-  int pad[3];
-};
-
-__device__ __forceinline__ LinHead* lin_head(char* state, int64_t r) {
-  return reinterpret_cast<LinHead*>(state + r * kLinRowBytes);
-}
-__device__ __forceinline__ float* lin_vals(char* state, int64_t r) {
-  return reinterpret_cast<float*>(state + r * kLinRowBytes + kLinHeader);
-}
-__device__ __forceinline__ int* lin_cols(char* state, int64_t r) {
-  return reinterpret_cast<int*>(state + r * kLinRowBytes + kLinHeader) + kLinCap;
-}
-
-__global__ __launch_bounds__(kBlock) void fwl_lin_begin(char* __restrict__ state, int64_t N) {
-  const int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (r >= N) return;
-  LinHead* h = lin_head(state, r);
-  h->m = -INFINITY;
-  h->t = -INFINITY;
-  h->n = 0;
-  h->zy = NAN;
-  h->flags = 0;
-}
-
-// Stable in-place compaction of one wavefront's LDS list to its entries > t; returns the count.
-__device__ __forceinline__ int lin_filter(float* cl, int* ci, int n, float t, int lane) {
-  int out = 0;
-  for (int p0 = 0; p0 < n; p0 += kWave) {
-    const int p = p0 + lane;
-    const float v = p < n ? cl[p] : -INFINITY;
-    const int c = p < n ? ci[p] : 0;
-    const bool keep = v > t;
-    const uint64_t b = ballot(keep);
-    __builtin_amdgcn_wave_barrier();   // the batch is read before any of it is overwritten
-    if (keep) {
-      const int at = out + rank_in(b);
-      cl[at] = v;
-      ci[at] = c;
-    }
-    out += __popcll(b);
-    __builtin_amdgcn_wave_barrier();
-  }
-  return out;
-}
-
-// Appends the values x[0, K) of this lane (columns col[i]) that are > t; entries past the LDS
-// capacity are counted but not kept.
-template <int K>
-__device__ __forceinline__ int lin_append(float* cl, int* ci, int n, const float* x, const int* col, float t,
-                                          int lane) {
-#pragma unroll
-  for (int i = 0; i < K; ++i) {
-    const bool c = x[i] > t;
-    const uint64_t b = ballot(c);
-    if (b != 0) {
-      const int at = n + rank_in(b);
-      if (c && at < kLinLds) {
-        cl[at] = x[i];
-        ci[at] = col[i];
-      }
-      n += __popcll(b);
-    }
-  }
-  return n;
-}
-
-// One vocabulary chunk: one wavefront per row streams the row's Vc logits once.
-template <typename T, bool VEC>
-__global__ __launch_bounds__(kBlock) void fwl_lin_chunk(const void* __restrict__ zc, int64_t N, int Vc, int64_t ld,
-                                                        int64_t v0, const int64_t* __restrict__ tgt,
-                                                        char* __restrict__ state) {
-  constexpr int U = kUnit<T, VEC>;
-  constexpr int K = kLinRound * U;
-  __shared__ float s_val[kWavesPerBlock][kLinLds];
-  __shared__ int s_col[kWavesPerBlock][kLinLds];
-  const int lane = lane_id();
-  const int wid = uniform((int)(threadIdx.x >> 6));
-  const int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  if (r >= N) return;   // wavefront-uniform; this kernel has no block barrier
-  LinHead* hd = lin_head(state, r);
-  const int flags = uniform(hd->flags);
-  if (flags & kLinOverflow) return;
-  float m = hd->m, t = hd->t;
-  const int nprev = uniform(hd->n);
-  float* cl = s_val[wid];
-  int* ci = s_col[wid];
-  const rsrc_t row = make_rsrc(static_cast<const char*>(zc) + r * ld * kElemBytes<T>, (uint32_t)(Vc * kElemBytes<T>));
-  const int units = (Vc + U - 1) / U;
-  int n = 0;
-  bool lost = false;
-  for (int u0 = 0; u0 < units; u0 += kWave * kLinRound) {
-    float x[K];
-    int col[K];
-#pragma unroll
-    for (int q = 0; q < kLinRound; ++q) load_unit<T, VEC>(row, (uint32_t)(u0 + lane + kWave * q), x + U * q);
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      const int e = U * (u0 + lane + kWave * (i / U)) + i % U;
-      col[i] = (int)v0 + e;
-      if (e >= Vc) x[i] = -INFINITY;   // past the row (loaded as 0)
-    }
-    float lm = x[0];
-#pragma unroll
-    for (int i = 1; i < K; ++i) lm = fmaxf(lm, x[i]);
-    const float wm = wave_max_f32(lm);
-    if (wm > m) {
-      m = wm;
-      const float tb = bound_below_max(m);
-      if (tb > t) t = tb;
-    }
-    n = lin_append<K>(cl, ci, n, x, col, t, lane);
-    if (n > kLinLds) {
-      lost = true;
-      break;
-    }
-    __builtin_amdgcn_wave_barrier();
-    if (n > kLinLds / 2) n = lin_filter(cl, ci, n, t, lane);
-  }
-  // the previous chunks' entries that are still above the bound
-  if (!lost) {
-    const float* pv = lin_vals(state, r);
-    const int* pc = lin_cols(state, r);
-    for (int p0 = 0; p0 < nprev; p0 += kWave) {
-      const int p = p0 + lane;
-      float v = p < nprev ? pv[p] : -INFINITY;
-      int c = p < nprev ? pc[p] : 0;
-      n = lin_append<1>(cl, ci, n, &v, &c, t, lane);
-    }
-    if (n > kLinLds) lost = true;
-  }
-  __builtin_amdgcn_wave_barrier();
-  if (!lost) n = lin_filter(cl, ci, n, t, lane);
-  // too long for the state: tighten the bound with t <- H({z > t}) (each value is <= tau)
-  for (int it = 0; !lost && n > kLinCap && it < 32; ++it) {
-    double s;
-    int c;
-    list_sum_count(cl, n, t, lane, s, c);
-    const float tn = rd32((s - 1.0) / (double)c);
-    if (!(tn > t)) break;
-    t = tn;
-    n = lin_filter(cl, ci, n, t, lane);
-  }
-  if (n > kLinCap) lost = true;
-  __builtin_amdgcn_wave_barrier();
-  if (!lost) {
-    float* pv = lin_vals(state, r);
-    int* pc = lin_cols(state, r);
-    for (int p = lane; p < n; p += kWave) {
-      pv[p] = cl[p];
-      pc[p] = ci[p];
-    }
-  }
-  const int64_t y = tgt[r];
-  const bool here = y >= v0 && y < v0 + Vc;
-  const float zy = here ? load_elem<T>(zc, r * ld + (y - v0)) : 0.0f;
-  if (lane == 0) {
-    hd->m = m;
-    hd->t = t;
-    hd->n = lost ? 0 : n;
-    hd->flags = flags | (lost ? kLinOverflow : 0);
-    if (here) hd->zy = zy;
-  }
-}
-
-// After the last chunk: tau, kappa, H and the loss of every row from its list, and the support's
-// columns (in list order).  Flagged rows and rows without a finite maximum get overflow[r] = 1.
-__global__ __launch_bounds__(kBlock) void fwl_lin_finish(const char* __restrict__ state, const int64_t* __restrict__ tgt,
-                                                         int64_t N, int64_t V, float* __restrict__ H,
-                                                         float* __restrict__ loss, int32_t* __restrict__ kappa,
-                                                         int32_t* __restrict__ sup, int32_t* __restrict__ overflow) {
-  __shared__ float s_val[kWavesPerBlock][kLinCap];
-  const int lane = lane_id();
-  const int wid = uniform((int)(threadIdx.x >> 6));
-  const int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  if (r >= N) return;
-  char* st = const_cast<char*>(state);
-  const LinHead* hd = lin_head(st, r);
-  const int n = uniform(hd->n);
-  const float m = hd->m, t0 = hd->t, zy = hd->zy;
-  const bool bad = (uniform(hd->flags) & kLinOverflow) || n == 0 || !isfinite(m);
-  if (bad) {
-    if (lane == 0) {
-      overflow[r] = 1;
-      H[r] = NAN;
-      loss[r] = NAN;
-      kappa[r] = 0;
-    }
-    return;
-  }
-  const float* pv = lin_vals(st, r);
-  const int* pc = lin_cols(st, r);
-  float* cl = s_val[wid];
-  for (int p = lane; p < n; p += kWave) cl[p] = pv[p];
-  __builtin_amdgcn_wave_barrier();
-  double tau;
-  int kap;
-  uint64_t support;
-  resolve_list(cl, n, t0, m, lane, tau, kap, support);
-  const float Hf = rd32(tau);
-  int out = 0;
-  for (int p0 = 0; p0 < n; p0 += kWave) {
-    const int p = p0 + lane;
-    const bool keep = p < n && cl[p] > Hf;
-    const uint64_t b = ballot(keep);
-    if (keep) sup[r * kLinCap + out + rank_in(b)] = pc[p];
-    out += __popcll(b);
-  }
-  const int64_t y = tgt[r];
-  if (lane == 0) {
-    overflow[r] = 0;
-    H[r] = Hf;
-    loss[r] = (y >= 0 && y < V) ? (float)((1.0 - (double)zy) + tau) : NAN;
-    kappa[r] = kap;
-  }
-}
-
-// The gradient values of row r, as the fused op writes them (scale s = row_scale[r * stride]):
-// inv = (float)(s / kappa) on the support, minus (float)s at the label.
-struct LinRowGrad {
-  float inv, lab;   // value at a support column that is not the label; value at the label
-  bool lab_alone;   // the label is outside the support (its own entry)
-};
-
-__device__ __forceinline__ LinRowGrad lin_row_grad(const int32_t* sup, int64_t r, int kap, int64_t y, int64_t V,
-                                                   double s, int lane) {
-  LinRowGrad g;
-  g.inv = (float)(s / (double)kap);
-  const float sf = (float)s;
-  bool in = false;
-  if (y >= 0 && y < V) {
-    for (int p0 = 0; p0 < kap; p0 += kWave) {
-      const int p = p0 + lane;
-      in |= ballot(p < kap && sup[r * kLinCap + p] == (int)y) != 0;
-    }
-    g.lab = in ? g.inv - sf : 0.0f - sf;
-    g.lab_alone = !in;
-  } else {
-    g.lab = 0.0f;
-    g.lab_alone = false;
-  }
-  return g;
-}
-
-// dhidden[r] = sum over the row's non-zero gradient columns j of g_rj * weight[j], accumulated in
-// fp32 in support order (the label last when it is outside the support).  One wavefront per row;
-// flagged rows (kappa 0) are left to the caller.
-template <typename T, bool VEC>
-__global__ __launch_bounds__(kBlock) void fwl_lin_dhidden(const void* __restrict__ W, int64_t V, int d,
-                                                          const int64_t* __restrict__ tgt,
-                                                          const int32_t* __restrict__ kappa,
-                                                          const int32_t* __restrict__ sup,
-                                                          const float* __restrict__ rscale, int64_t rs_stride,
-                                                          int64_t N, void* __restrict__ dh) {
-  constexpr int U = kUnit<T, VEC>;
-  const int lane = lane_id();
-  const int wid = uniform((int)(threadIdx.x >> 6));
-  const int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  if (r >= N) return;
-  const int kap = uniform(kappa[r]);
-  if (kap <= 0) return;
-  const int64_t y = tgt[r];
-  const LinRowGrad g = lin_row_grad(sup, r, kap, y, V, (double)rscale[r * rs_stride], lane);
-  const uint32_t row_bytes = (uint32_t)(d * kElemBytes<T>);
-  const rsrc_t out = make_rsrc(static_cast<char*>(dh) + r * (int64_t)d * kElemBytes<T>, row_bytes);
-  const int units = (d + U - 1) / U;
-  for (int u = lane; u - lane < units; u += kWave) {
-    float acc[U];
-#pragma unroll
-    for (int e = 0; e < U; ++e) acc[e] = 0.0f;
-    for (int p = 0; p < kap; ++p) {
-      const int j = uniform(sup[r * kLinCap + p]);
-      if (j < 0 || (int64_t)j >= V) continue;   // not a column of weight (never produced by the chunks)
-      const float gj = (int64_t)j == y ? g.lab : g.inv;
-      float w[U];
-      load_unit<T, VEC>(make_rsrc(static_cast<const char*>(W) + (int64_t)j * d * kElemBytes<T>, row_bytes), (uint32_t)u, w);
-#pragma unroll
-      for (int e = 0; e < U; ++e) acc[e] = fmaf(gj, w[e], acc[e]);
-    }
-    if (g.lab_alone) {
-      float w[U];
-      load_unit<T, VEC>(make_rsrc(static_cast<const char*>(W) + y * d * kElemBytes<T>, row_bytes), (uint32_t)u, w);
-#pragma unroll
-      for (int e = 0; e < U; ++e) acc[e] = fmaf(g.lab, w[e], acc[e]);
-    }
-    store_unit<T, VEC>(out, (uint32_t)u, acc);
-  }
-}
-
-// (column, row) entries of the gradient, one per support column and one per label outside the
-// support: key = column * 2N + 2 * row (+ 1 for a label entry), value g.  Row r's entries start
-// at offsets[r] (exclusive prefix sum of kappa[r] + [label outside the support]).
-__global__ __launch_bounds__(kBlock) void fwl_lin_coo(const int64_t* __restrict__ tgt, int64_t N, int64_t V,
-                                                      const int32_t* __restrict__ kappa,
-                                                      const int32_t* __restrict__ sup,
-                                                      const int64_t* __restrict__ offsets,
-                                                      const float* __restrict__ rscale, int64_t rs_stride,
-                                                      int64_t* __restrict__ keys, float* __restrict__ vals) {
-  const int lane = lane_id();
-  const int wid = uniform((int)(threadIdx.x >> 6));
-  const int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  if (r >= N) return;
-  const int kap = uniform(kappa[r]);
-  if (kap <= 0) return;
-  const int64_t y = tgt[r];
-  const LinRowGrad g = lin_row_grad(sup, r, kap, y, V, (double)rscale[r * rs_stride], lane);
-  const int64_t o = offsets[r];
-  for (int p = lane; p < kap; p += kWave) {
-    int64_t j = sup[r * kLinCap + p];
-    if (j < 0 || j >= V) j = V;   // not a column of weight: a key that dweight skips
-    keys[o + p] = j * 2 * N + 2 * r;
-    vals[o + p] = j == y ? g.lab : g.inv;
-  }
-  if (g.lab_alone && lane == 0) {
-    keys[o + kap] = y * 2 * N + 2 * r + 1;
-    vals[o + kap] = g.lab;
-  }
-}
-
-// dweight[j] = sum of g * hidden[row] over column j's entries, in key order (keys sorted).  One
-// wavefront per entry; the wavefront at the first entry of a column does the column.
-template <typename T, bool VEC>
-__global__ __launch_bounds__(kBlock) void fwl_lin_dweight(const void* __restrict__ hid, int64_t N, int64_t V, int d,
-                                                          const int64_t* __restrict__ keys,
-                                                          const float* __restrict__ vals, int64_t P,
-                                                          void* __restrict__ dW) {
-  constexpr int U = kUnit<T, VEC>;
-  const int lane = lane_id();
-  const int wid = uniform((int)(threadIdx.x >> 6));
-  const int64_t p0 = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  if (p0 >= P) return;
-  const int64_t twoN = 2 * N;
-  const int64_t j = keys[p0] / twoN;
-  if (j < 0 || j >= V) return;   // not a column of weight
-  if (p0 > 0 && keys[p0 - 1] / twoN == j) return;
-  int64_t p1 = p0 + 1;
-  while (p1 < P && keys[p1] / twoN == j) ++p1;
-  const uint32_t row_bytes = (uint32_t)(d * kElemBytes<T>);
-  const rsrc_t out = make_rsrc(static_cast<char*>(dW) + j * d * kElemBytes<T>, row_bytes);
-  const int units = (d + U - 1) / U;
-  for (int u = lane; u - lane < units; u += kWave) {
-    float acc[U];
-#pragma unroll
-    for (int e = 0; e < U; ++e) acc[e] = 0.0f;
-    for (int64_t p = p0; p < p1; ++p) {
-      const int64_t n = (keys[p] % twoN) / 2;   // keys >= 0: 0 <= n < N
-      const float gv = vals[p];
-      float h[U];
-      load_unit<T, VEC>(make_rsrc(static_cast<const char*>(hid) + n * d * kElemBytes<T>, row_bytes), (uint32_t)u, h);
-#pragma unroll
-      for (int e = 0; e < U; ++e) acc[e] = fmaf(gv, h[e], acc[e]);
-    }
-    store_unit<T, VEC>(out, (uint32_t)u, acc);
-  }
-}
-
-// ------------------------------------------------------------------------------------------------
 // host side
 
 int g_path = 0;
 int g_cap = kCapMax;
 
-int blocks_wave(int64_t N) {
-  const int64_t b = (N + kWavesPerBlock - 1) / kWavesPerBlock;
-  return (int)(b < kMaxBlocksWave ? (b > 0 ? b : 1) : kMaxBlocksWave);
-}
 int blocks_row(int64_t N) { return (int)(N < kMaxBlocksRow ? (N > 0 ? N : 1) : kMaxBlocksRow); }
 
 // Blocks of `kernel` that fit on the current device at once (cached per device and kernel).
@@ -3224,9 +2033,7 @@ int wave_grid(int64_t N, int64_t row_bytes, int resident) {
   return (int)(g > min_blocks ? g : min_blocks);
 }
 
-bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-int launch_status() { return hipGetLastError() == hipSuccess ? FWL_OK : FWL_ERR_LAUNCH; }
 
 template <typename T, int MODE, int NV, bool V4>
 void launch_wave(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
@@ -3458,8 +2265,6 @@ void launch_split(const void* z, const int64_t* y, int64_t N, int C, const Outs&
 
 // rows are addressed through buffer resources with 32-bit byte ranges and offsets (one round
 // past the row end included), hence the bound on C
-constexpr int64_t kMaxC = (int64_t)1 << 29;
-bool bad_shape(int64_t N, int64_t C) { return N < 0 || C < 1 || C > kMaxC; }
 
 // shared forward driver; `out_v4_ok` says whether the mode's dense output allows 128-bit access
 template <typename T, int MODE>
@@ -3547,96 +2352,6 @@ int scale_grad(void* grad, const float* grad_output, int64_t go_stride, int64_t 
                        go_stride, N, Ci);
   return launch_status();
 }
-
-
-// ---- fp64 logits (host side)
-
-int forward_f64(const double* z, const int64_t* y, int64_t N, int64_t C, double scale, double reduce_div, double* H,
-                double* losses, double* mean, int32_t* kappa, double* grad, hipStream_t s) {
-  if (bad_shape(N, C) || (N > 0 && (z == nullptr || y == nullptr || grad == nullptr)) ||
-      (mean != nullptr && N > 0 && losses == nullptr))
-    return FWL_ERR_INVALID_ARG;
-  if (!aligned(z, 8) || !aligned(y, 8) || !aligned(grad, 8) || !aligned(H, 8) || !aligned(losses, 8) ||
-      !aligned(mean, 8) || !aligned(kappa, 4))
-    return FWL_ERR_ALIGNMENT;
-  if (N > 0) {
-    // rows of up to 4 rounds stay in registers (512 doubles per round with 128-bit units, 256 with
-    // 64-bit ones)
-    const int per_round = (C % 2 == 0 ? 2 : 1) * kWave * kF64Round;
-    const int rounds = (int)((C + per_round - 1) / per_round);
-    const dim3 g(blocks_wave(N)), b(kBlock);
-#define FWL_F64(E, R) hipLaunchKernelGGL((fwl_rows_f64<E, R>), g, b, 0, s, z, y, N, (int)C, scale, H, losses, kappa, grad)
-    if (C % 2 == 0) {
-      if (rounds <= 1) FWL_F64(true, 1);
-      else if (rounds <= 2) FWL_F64(true, 2);
-      else if (rounds <= 4) FWL_F64(true, 4);
-      else FWL_F64(true, 0);
-    } else {
-      if (rounds <= 1) FWL_F64(false, 1);
-      else if (rounds <= 2) FWL_F64(false, 2);
-      else if (rounds <= 4) FWL_F64(false, 4);
-      else FWL_F64(false, 0);
-    }
-#undef FWL_F64
-  }
-  if (mean != nullptr) hipLaunchKernelGGL(fwl_mean_f64, dim3(1), dim3(kBlock), 0, s, losses, N, reduce_div, mean);
-  return launch_status();
-}
-
-// ---- the linear layer fused with the loss (host side)
-
-template <typename T>
-bool lin_vec_ok(const void* a, const void* b, int64_t d) {
-  return (d * kElemBytes<T>) % 16 == 0 && aligned(a, 16) && aligned(b, 16);
-}
-
-template <typename T>
-int lin_chunk(const void* zc, int64_t N, int64_t Vc, int64_t ld, int64_t v0, const int64_t* y, void* state,
-              hipStream_t s) {
-  if (!aligned(zc, kElemBytes<T>)) return FWL_ERR_ALIGNMENT;
-  const int64_t blocks = (N + kWavesPerBlock - 1) / kWavesPerBlock;
-  if ((Vc % kUnit<T, true>) == 0 && (ld % kUnit<T, true>) == 0 && aligned(zc, 16))
-    hipLaunchKernelGGL((fwl_lin_chunk<T, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s, zc, N, (int)Vc, ld, v0, y,
-                       static_cast<char*>(state));
-  else
-    hipLaunchKernelGGL((fwl_lin_chunk<T, false>), dim3((unsigned)blocks), dim3(kBlock), 0, s, zc, N, (int)Vc, ld, v0,
-                       y, static_cast<char*>(state));
-  return launch_status();
-}
-
-template <typename T>
-int lin_dhidden(const void* W, int64_t V, int64_t d, const int64_t* y, const int32_t* kappa, const int32_t* sup,
-                const float* rs, int64_t rs_stride, int64_t N, void* dh, hipStream_t s) {
-  if (!aligned(W, kElemBytes<T>) || !aligned(dh, kElemBytes<T>)) return FWL_ERR_ALIGNMENT;
-  const int64_t blocks = (N + kWavesPerBlock - 1) / kWavesPerBlock;
-  if (lin_vec_ok<T>(W, dh, d))
-    hipLaunchKernelGGL((fwl_lin_dhidden<T, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s, W, V, (int)d, y, kappa,
-                       sup, rs, rs_stride, N, dh);
-  else
-    hipLaunchKernelGGL((fwl_lin_dhidden<T, false>), dim3((unsigned)blocks), dim3(kBlock), 0, s, W, V, (int)d, y,
-                       kappa, sup, rs, rs_stride, N, dh);
-  return launch_status();
-}
-
-template <typename T>
-int lin_dweight(const void* hid, int64_t N, int64_t V, int64_t d, const int64_t* keys, const float* vals, int64_t P,
-                void* dW, hipStream_t s) {
-  if (!aligned(hid, kElemBytes<T>) || !aligned(dW, kElemBytes<T>)) return FWL_ERR_ALIGNMENT;
-  const int64_t blocks = (P + kWavesPerBlock - 1) / kWavesPerBlock;
-  if (lin_vec_ok<T>(hid, dW, d))
-    hipLaunchKernelGGL((fwl_lin_dweight<T, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s, hid, N, V, (int)d,
-                       keys, vals, P, dW);
-  else
-    hipLaunchKernelGGL((fwl_lin_dweight<T, false>), dim3((unsigned)blocks), dim3(kBlock), 0, s, hid, N, V, (int)d,
-                       keys, vals, P, dW);
-  return launch_status();
-}
-
-// the linear entry points' dimension limits: rows of the state addressed in 64 bits, columns and
-// hidden sizes in 32 bits, and grids within 2^31 blocks
-constexpr int64_t kLinMaxV = (int64_t)1 << 30;
-constexpr int64_t kLinMaxD = (int64_t)1 << 26;
-bool lin_bad_rows(int64_t N) { return N < 0 || N > ((int64_t)1 << 31); }
 
 }  // namespace
 
@@ -3825,114 +2540,5 @@ int fwl_get_params(int* path, int* cand_cap) {
   return FWL_OK;
 }
 
-
-int fwl_forward_backward_f64(const double* logits, const int64_t* targets, int64_t N, int64_t C, double scale,
-                             double reduce_div, double* H, double* losses, double* mean_loss, int32_t* kappa,
-                             double* grad, hipStream_t stream) {
-  return forward_f64(logits, targets, N, C, scale, reduce_div, H, losses, mean_loss, kappa, grad, stream);
-}
-
-int fwl_scale_grad_f64(double* grad, const double* grad_output, int64_t go_stride, int64_t N, int64_t C,
-                       hipStream_t stream) {
-  if (bad_shape(N, C) || go_stride < 0 || (N > 0 && (grad == nullptr || grad_output == nullptr)))
-    return FWL_ERR_INVALID_ARG;
-  if (!aligned(grad, 8) || !aligned(grad_output, 8)) return FWL_ERR_ALIGNMENT;
-  if (N == 0) return FWL_OK;
-  hipLaunchKernelGGL(fwl_scale_rows_f64, dim3(blocks_wave(N)), dim3(kBlock), 0, stream, grad, grad_output, go_stride, N,
-                     (int)C);
-  return launch_status();
-}
-
-size_t fwl_linear_state_bytes(int64_t N) { return N > 0 ? (size_t)N * (size_t)kLinRowBytes : 0; }
-
-int fwl_linear_support_cap(void) { return kLinCap; }
-
-int fwl_linear_begin(void* state, int64_t N, hipStream_t stream) {
-  if (lin_bad_rows(N) || (N > 0 && state == nullptr)) return FWL_ERR_INVALID_ARG;
-  if (!aligned(state, 16)) return FWL_ERR_ALIGNMENT;
-  if (N == 0) return FWL_OK;
-  hipLaunchKernelGGL(fwl_lin_begin, dim3((unsigned)((N + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream,
-                     static_cast<char*>(state), N);
-  return launch_status();
-}
-
-int fwl_linear_chunk(int dtype, const void* logits, int64_t N, int64_t Vc, int64_t ld, int64_t v0, int64_t V,
-                     const int64_t* targets, void* state, hipStream_t stream) {
-  if (lin_bad_rows(N) || Vc < 1 || Vc > kMaxC || ld < Vc || v0 < 0 || V > kLinMaxV || v0 + Vc > V ||
-      (N > 0 && (logits == nullptr || targets == nullptr || state == nullptr)))
-    return FWL_ERR_INVALID_ARG;
-  if (!aligned(targets, 8) || !aligned(state, 16)) return FWL_ERR_ALIGNMENT;
-  if (N == 0) return FWL_OK;
-  switch (dtype) {
-    case FWL_FLOAT32: return lin_chunk<float>(logits, N, Vc, ld, v0, targets, state, stream);
-    case FWL_BFLOAT16: return lin_chunk<bf16_t>(logits, N, Vc, ld, v0, targets, state, stream);
-    case FWL_FLOAT16: return lin_chunk<f16_t>(logits, N, Vc, ld, v0, targets, state, stream);
-    default: return FWL_ERR_INVALID_ARG;
-  }
-}
-
-int fwl_linear_finish(const void* state, const int64_t* targets, int64_t N, int64_t V, float* H, float* losses,
-                      int32_t* kappa, int32_t* support, int32_t* overflow, hipStream_t stream) {
-  if (lin_bad_rows(N) || V < 1 || V > kLinMaxV ||
-      (N > 0 && (state == nullptr || targets == nullptr || H == nullptr || losses == nullptr || kappa == nullptr ||
-                 support == nullptr || overflow == nullptr)))
-    return FWL_ERR_INVALID_ARG;
-  if (!aligned(state, 16) || !aligned(targets, 8) || !aligned(H, 4) || !aligned(losses, 4) || !aligned(kappa, 4) ||
-      !aligned(support, 4) || !aligned(overflow, 4))
-    return FWL_ERR_ALIGNMENT;
-  if (N == 0) return FWL_OK;
-  hipLaunchKernelGGL(fwl_lin_finish, dim3((unsigned)((N + kWavesPerBlock - 1) / kWavesPerBlock)), dim3(kBlock), 0,
-                     stream, static_cast<const char*>(state), targets, N, V, H, losses, kappa, support, overflow);
-  return launch_status();
-}
-
-int fwl_linear_dhidden(int dtype, const void* weight, int64_t V, int64_t d, const int64_t* targets,
-                       const int32_t* kappa, const int32_t* support, const float* row_scale, int64_t rs_stride,
-                       int64_t N, void* dhidden, hipStream_t stream) {
-  if (lin_bad_rows(N) || V < 1 || V > kLinMaxV || d < 1 || d > kLinMaxD || rs_stride < 0 ||
-      (N > 0 && (weight == nullptr || targets == nullptr || kappa == nullptr || support == nullptr ||
-                 row_scale == nullptr || dhidden == nullptr)))
-    return FWL_ERR_INVALID_ARG;
-  if (!aligned(targets, 8) || !aligned(kappa, 4) || !aligned(support, 4) || !aligned(row_scale, 4))
-    return FWL_ERR_ALIGNMENT;
-  if (N == 0) return FWL_OK;
-  switch (dtype) {
-    case FWL_FLOAT32: return lin_dhidden<float>(weight, V, d, targets, kappa, support, row_scale, rs_stride, N, dhidden, stream);
-    case FWL_BFLOAT16: return lin_dhidden<bf16_t>(weight, V, d, targets, kappa, support, row_scale, rs_stride, N, dhidden, stream);
-    case FWL_FLOAT16: return lin_dhidden<f16_t>(weight, V, d, targets, kappa, support, row_scale, rs_stride, N, dhidden, stream);
-    default: return FWL_ERR_INVALID_ARG;
-  }
-}
-
-int fwl_linear_coo(const int64_t* targets, int64_t N, int64_t V, const int32_t* kappa, const int32_t* support,
-                   const int64_t* offsets, const float* row_scale, int64_t rs_stride, int64_t* keys, float* values,
-                   hipStream_t stream) {
-  if (lin_bad_rows(N) || V < 1 || V > kLinMaxV || rs_stride < 0 ||
-      (N > 0 && (targets == nullptr || kappa == nullptr || support == nullptr || offsets == nullptr ||
-                 row_scale == nullptr || keys == nullptr || values == nullptr)))
-    return FWL_ERR_INVALID_ARG;
-  if (!aligned(targets, 8) || !aligned(offsets, 8) || !aligned(keys, 8) || !aligned(kappa, 4) || !aligned(support, 4) ||
-      !aligned(row_scale, 4) || !aligned(values, 4))
-    return FWL_ERR_ALIGNMENT;
-  if (N == 0) return FWL_OK;
-  hipLaunchKernelGGL(fwl_lin_coo, dim3((unsigned)((N + kWavesPerBlock - 1) / kWavesPerBlock)), dim3(kBlock), 0, stream,
-                     targets, N, V, kappa, support, offsets, row_scale, rs_stride, keys, values);
-  return launch_status();
-}
-
-int fwl_linear_dweight(int dtype, const void* hidden, int64_t N, int64_t V, int64_t d, const int64_t* keys,
-                       const float* values, int64_t P, void* dweight, hipStream_t stream) {
-  if (lin_bad_rows(N) || V < 1 || V > kLinMaxV || d < 1 || d > kLinMaxD || P < 0 || P > ((int64_t)1 << 32) ||
-      (P > 0 && (hidden == nullptr || keys == nullptr || values == nullptr || dweight == nullptr)))
-    return FWL_ERR_INVALID_ARG;
-  if (!aligned(keys, 8) || !aligned(values, 4)) return FWL_ERR_ALIGNMENT;
-  if (P == 0) return FWL_OK;
-  switch (dtype) {
-    case FWL_FLOAT32: return lin_dweight<float>(hidden, N, V, d, keys, values, P, dweight, stream);
-    case FWL_BFLOAT16: return lin_dweight<bf16_t>(hidden, N, V, d, keys, values, P, dweight, stream);
-    case FWL_FLOAT16: return lin_dweight<f16_t>(hidden, N, V, d, keys, values, P, dweight, stream);
-    default: return FWL_ERR_INVALID_ARG;
-  }
-}
 
 }  // extern "C"

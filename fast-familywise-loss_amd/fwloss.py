@@ -152,7 +152,7 @@ class FWLinearFunction(torch.autograd.Function):
             out = losses
         else:
             total = losses.double().sum()
-            out = (total / N if (reduction == "mean" and N) else total).float()
+            out = (total / N if reduction == "mean" else total).float()   # an empty mean is NaN
         ctx.save_for_backward(hidden.detach(), weight.detach(), target, res["kappa_sparse"], res["support"])
         ctx.dense = res["dense"]
         ctx.reduction = reduction
@@ -172,12 +172,13 @@ class FWLinearFunction(torch.autograd.Function):
             rs = go.reshape(-1)
         dh, dw = _ext.fw_linear_grads(h, w, y, kappa, support, rs, want_dh, want_dw)
         if ctx.dense is not None:
+            # rows solved on their materialised logits: dense logit gradients, in the weight's dtype
             rows, gr = ctx.dense
-            g = gr.float() * (rs if rs.numel() == 1 else rs[rows]).reshape(-1, 1)
+            g = (gr.float() * (rs if rs.numel() == 1 else rs[rows]).reshape(-1, 1)).to(w.dtype)
             if want_dh:
-                dh[rows] += (g @ w.float()).to(dh.dtype)
+                dh.index_add_(0, rows, g @ w)
             if want_dw:
-                dw += (g.t() @ h[rows].float()).to(dw.dtype)
+                dw.addmm_(g.t().contiguous(), h[rows])
         return (dh if want_dh else None), (dw if want_dw else None), None, None, None
 
 

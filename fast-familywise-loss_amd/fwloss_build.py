@@ -1,6 +1,6 @@
 """Build driver for the native parts of the package (in-tree, no JIT cache).
 
-* ``libfwloss.so``      -- HIP kernels + C ABI (csrc/fwloss.hip, include/fwloss.h), hipcc for gfx950.
+* ``libfwloss.so``      -- HIP kernels + C ABI (csrc/*.hip, include/fwloss.h), hipcc for gfx950.
 * ``fw_radix_cuda*.so`` -- the PyTorch extension (csrc/fw_radix_ext.cpp), host C++ only, linked
                           against libfwloss.so with an $ORIGIN rpath.
 
@@ -41,11 +41,27 @@ def ext_path():
     return os.path.join(PKG, "fw_radix_cuda" + suffix)
 
 
+HIP_SOURCES = ["fwloss.hip", "fwl_f64.hip", "fwl_linear.hip"]   # share csrc/fwl_common.h
+
+
 def build_lib():
+    """Compile every HIP source to an object (in parallel), then link libfwloss.so."""
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    objs, procs = [], []
+    for src in HIP_SOURCES:
+        obj = os.path.join(CSRC, src.replace(".hip", ".o"))
+        cmd = [hipcc] + HIP_FLAGS + ["-c", f"-I{INCLUDE}", os.path.join(CSRC, src), "-o", obj]
+        print("+ " + " ".join(cmd), flush=True)
+        procs.append(subprocess.Popen(cmd))
+        objs.append(obj)
+    failed = [src for src, p in zip(HIP_SOURCES, procs) if p.wait() != 0]
+    if failed:
+        raise subprocess.CalledProcessError(1, f"hipcc {' '.join(failed)}")
     tmp = LIB + ".tmp"
-    _run([os.path.join(ROCM, "bin", "hipcc")] + HIP_FLAGS + ["-shared", f"-I{INCLUDE}",
-         os.path.join(CSRC, "fwloss.hip"), "-o", tmp])
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC"] + objs + ["-o", tmp])
     os.replace(tmp, LIB)
+    for obj in objs:
+        os.remove(obj)
     return LIB
 
 

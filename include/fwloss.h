@@ -64,10 +64,11 @@ const char* fwl_status_string(int status);
 /* Bytes of device workspace the forward entry points need for an [N, C] problem: 256 bytes, one
  * fp64 per block of the largest grid (>= 4096 blocks), 72 bytes per group of 32 blocks, then the
  * larger of: 524 bytes per (row, chunk) for at most 128 rows of >= 24576 elements (the split
- * rows), and 520 bytes per row for >= 384 rows of >= 32000 elements (the fused op in two
- * passes).  The answer follows the current fwl_set_params switches (forcing path 7 needs the
- * chunk scratch, forcing path 2 or 3 the two-pass scratch, for rows of any length).  A smaller
- * workspace is accepted where no mean is requested: the one-pass kernels then run. */
+ * rows), and 520 bytes per row for >= 384 rows of >= 32000 elements or for batches of >= 48M
+ * elements in rows of >= 8192 (the fused op in two passes).  The answer follows the current
+ * fwl_set_params switches (forcing path 7 needs the chunk scratch, forcing path 2 or 3 the
+ * two-pass scratch, for rows of any length).  A smaller workspace is accepted where no mean is
+ * requested: the one-pass kernels then run. */
 size_t fwl_workspace_bytes(int64_t N, int64_t C);
 
 /* Fused forward + backward: the whole hot path in one launch, reading logits once and writing the

@@ -195,8 +195,8 @@ def test_workspace_sizes():
     """The split-row scratch is counted exactly where the split kernels may run: few rows (<= 128)
     of at least 96 KiB (24576 fp32 elements; the size covers every element type), or rows of any
     length when path 7 is forced; the two-pass scratch where the fused op may run in two passes
-    (>= 384 rows of >= 32000 elements, or path 2/3 forced).  The two share one region (the larger
-    is counted)."""
+    (>= 384 rows of >= 32000 elements, rows of >= 8192 elements in batches of >= 48M elements, or
+    path 2/3 forced).  The two share one region (the larger is counted)."""
     L = capi.lib()
     p, c = ctypes.c_int(-1), ctypes.c_int(-1)
     L.fwl_get_params(ctypes.byref(p), ctypes.byref(c))
@@ -206,15 +206,19 @@ def test_workspace_sizes():
         base = L.fwl_workspace_bytes(4096, 1000)
         assert base >= 256 + 8 * 4096
         assert L.fwl_workspace_bytes(16, 1000) == base           # short rows: no scratch
-        assert L.fwl_workspace_bytes(65536, 8192) == base
+        assert L.fwl_workspace_bytes(65536, 8191) == base
         assert L.fwl_workspace_bytes(0, 131072) == base
-        # >= 384 rows of >= 32000 elements (the fp32 rule, which covers the 16-bit one) run the
-        # fused op in two passes: per row 64 support values and indices, kappa and H
+        # >= 384 rows of >= 32000 elements, or batches of >= 48M elements in rows of >= 8192 (the
+        # fp32 rules, which cover the 16-bit one) run the fused op in two passes: per row 64
+        # support values and indices, kappa and H
         row = 64 * 8 + 4 + 4
         assert L.fwl_workspace_bytes(2048, 131072) - base == 2048 * row
         assert L.fwl_workspace_bytes(384, 32000) - base == 384 * row
         assert L.fwl_workspace_bytes(383, 32000) == base
-        assert L.fwl_workspace_bytes(65536, 31999) == base
+        assert L.fwl_workspace_bytes(6144, 8192) - base == 6144 * row     # 48M elements
+        assert L.fwl_workspace_bytes(6143, 8192) == base
+        assert L.fwl_workspace_bytes(65536, 8192) - base == 65536 * row
+        assert L.fwl_workspace_bytes(1024, 31999) == base
         assert L.fwl_workspace_bytes(129, 24576) == base
         assert L.fwl_workspace_bytes(128, 24575) == base
         # (row, chunk) items: about 1024 in all, chunks of at least 4096 elements, <= 256 per row;
