@@ -191,7 +191,6 @@ struct Outs {
   float scale_f;
   unsigned* ticket;     // final ticket
   double* partials;     // one per block
-  double* gpartials;    // one per group of kTicketGroup blocks
   unsigned* gtickets;   // one per group (kTicketStride apart)
   int force_generic;
   int cap;             // LDS candidate capacity per wavefront (<= kCapMax)

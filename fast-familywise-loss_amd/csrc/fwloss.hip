@@ -31,9 +31,9 @@
 //   fwl_mask_to_grad, fwl_cand_to_grad   the two-op backward of the drop-in interface.
 // Other sources of the library: fwl_f64.hip (float64 logits), fwl_linear.hip (the LM head fused
 // with the loss), fwl_common.h (what they share).
-// The mean loss is reduced in fp64 in a fixed order: per-block partial sums, then either the last
-// block sums them all (grids of up to 512 blocks) or per-group sums by the last block of each group
-// of 32 and the last group finisher sums the group sums (ticket counters in the caller's
+// The mean loss is reduced in fp64 in a fixed order: per-block partial sums, summed in block order
+// by the last block to finish, found by one ticket (grids of up to 512 blocks) or by a ticket per
+// group of 32 blocks whose last finishers share a second ticket (ticket counters in the caller's
 // workspace, each reset by its last user).
 //
 #include "fwl_common.h"
@@ -76,10 +76,9 @@ __device__ void mean_epilogue(double bsum, const Outs& o) {
     }
     return;
   }
-  // Two ticket levels: the last block of each group of kTicketGroup blocks sums the group's
-  // partials (in block order) and takes the final ticket; the last of those sums the group sums.
-  // When many blocks finish together, no single counter serialises more than
-  // max(kTicketGroup, groups) atomics.
+  // Two ticket levels: the last block of each group of kTicketGroup blocks takes the final ticket;
+  // the last of those sums every block's partial (in block order).  When many blocks finish
+  // together, no single counter serialises more than max(kTicketGroup, groups) atomics.
   const unsigned nb = gridDim.x;
   const unsigned g = blockIdx.x / kTicketGroup;
   const unsigned ng = (nb + kTicketGroup - 1) / kTicketGroup;
@@ -100,16 +99,10 @@ __device__ void mean_epilogue(double bsum, const Outs& o) {
     t = (unsigned)__builtin_amdgcn_readfirstlane((int)t);
     int last = 0;
     if (t == gsize - 1) {
-      // the group's partials, one per lane, summed in a fixed order
-      const double v = lane < (int)gsize
-                           ? __hip_atomic_load(o.partials + g0 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                           : 0.0;
-      const double gs = wave_sum_f64(v);
+      // every partial of the group is published (each before its block's group ticket)
       unsigned t2 = 0;
       if (lane == 0) {
-        __hip_atomic_store(o.gpartials + g, gs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(gt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wait_vmem();
         t2 = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       last = (unsigned)__builtin_amdgcn_readfirstlane((int)t2) == ng - 1;
@@ -119,8 +112,8 @@ __device__ void mean_epilogue(double bsum, const Outs& o) {
   __syncthreads();
   if (!s_last) return;
   double acc = 0.0;
-  for (unsigned i = threadIdx.x; i < ng; i += kBlock)
-    acc += __hip_atomic_load(o.gpartials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (unsigned i = threadIdx.x; i < nb; i += kBlock)
+    acc += __hip_atomic_load(o.partials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   s_red[threadIdx.x] = acc;
   __syncthreads();
   for (int s = kBlock / 2; s > 0; s >>= 1) {
@@ -2199,7 +2192,7 @@ int64_t partial_slots(int64_t N) {
 size_t mean_ws_bytes(int64_t N) {
   const size_t P = (size_t)partial_slots(N);
   const size_t G = (P + kTicketGroup - 1) / kTicketGroup;
-  return kWsHeader + sizeof(double) * P + sizeof(double) * G + sizeof(unsigned) * kTicketStride * G;
+  return kWsHeader + sizeof(double) * P + sizeof(unsigned) * kTicketStride * G;
 }
 
 // Whether the fused op may run in two passes (the long-row block path) under switch `path`.
@@ -2281,12 +2274,10 @@ int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scal
   if (o.mean != nullptr) {
     if (ws == nullptr || ws_bytes < fwl_workspace_bytes(N, C64) || !aligned(ws, 8)) return FWL_ERR_WORKSPACE;
     const size_t P = (size_t)partial_slots(N);
-    const size_t G = (P + kTicketGroup - 1) / kTicketGroup;
     char* wb = static_cast<char*>(ws);
     o.ticket = reinterpret_cast<unsigned*>(wb);
     o.partials = reinterpret_cast<double*>(wb + kWsHeader);
-    o.gpartials = reinterpret_cast<double*>(wb + kWsHeader + sizeof(double) * P);
-    o.gtickets = reinterpret_cast<unsigned*>(wb + kWsHeader + sizeof(double) * (P + G));
+    o.gtickets = reinterpret_cast<unsigned*>(wb + kWsHeader + sizeof(double) * P);
   }
   if (N == 0) {
     if (o.mean != nullptr) hipLaunchKernelGGL(fwl_empty_mean, dim3(1), dim3(1), 0, s, o.mean, reduce_div);

@@ -62,7 +62,7 @@ enum fwl_dtype {
 const char* fwl_status_string(int status);
 
 /* Bytes of device workspace the forward entry points need for an [N, C] problem: 256 bytes, one
- * fp64 per block of the largest grid (>= 4096 blocks), 72 bytes per group of 32 blocks, then the
+ * fp64 per block of the largest grid (>= 4096 blocks), 64 bytes per group of 32 blocks, then the
  * larger of: 524 bytes per (row, chunk) for at most 128 rows of >= 24576 elements (the split
  * rows), and 520 bytes per row for >= 384 rows of >= 32000 elements or for batches of >= 48M
  * elements in rows of >= 8192 (the fused op in two passes).  The answer follows the current

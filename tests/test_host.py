@@ -62,10 +62,10 @@ def test_workspace_bytes():
     assert base >= 256 + 8 * 4096
     assert L.fwl_workspace_bytes(65536, 1000) == base
     # grows with N once the row-per-wave grid exceeds the fixed caps: per block one fp64 partial,
-    # per group of 32 blocks one fp64 group sum and one 64-byte ticket slot
+    # per group of 32 blocks one 64-byte ticket slot
     big = L.fwl_workspace_bytes(1 << 22, 10)
     blocks = (1 << 22) // 256
-    assert big == 256 + 8 * blocks + (8 + 64) * (blocks // 32)
+    assert big == 256 + 8 * blocks + 64 * (blocks // 32)
     assert L.fwl_workspace_bytes(1 << 22, 10) >= L.fwl_workspace_bytes((1 << 22) - 1, 10)
 
 
