@@ -219,3 +219,32 @@ def test_only_hidden_needs_grad(dev):
     _, dh_ref, _ = dense_grads(z, y.cpu().numpy(), h, w, np.full(N, 1.0 / N))
     close(hh.grad, dh_ref, 1e-5)
     assert w.grad is None
+
+
+@pytest.mark.parametrize("spread", [0.5, 3.0, 12.0])
+def test_lm_head_scale_against_unfused(dev, spread):
+    """An LM-head shape (4096 tokens, d = 512, V = 50000, bf16) at flat, moderate and peaky logit
+    spreads, against the unfused layer + familywise_loss with autograd's dense backward: the same
+    loss (to the fp32 sum order) and gradients within bf16 rounding."""
+    import fwloss
+    N, d, V, chunk = 4096, 512, 50000, 8192
+    g = torch.Generator(device=dev).manual_seed(int(spread * 10))
+    h = torch.randn(N, d, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(V, d, device=dev, generator=g) * (spread / d ** 0.5)).to(torch.bfloat16)
+    y = torch.randint(0, V, (N,), device=dev, generator=g)
+    print(f"lm head spread={spread}", flush=True)
+    h1, w1 = h.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    l1 = fwloss.familywise_linear_loss(h1, w1, y, "mean", chunk)
+    l1.backward()
+    res = fwloss.linear_forward(h, w, y, chunk)
+    z = chunk_logits(h, w, chunk)
+    H, losses, _, kappa, _ = fwloss.fw_forward_backward(z, y)
+    assert torch.equal(res["kappa"], kappa)
+    assert torch.equal(res["H"].view(torch.int32), H.view(torch.int32))
+    assert torch.equal(res["losses"].view(torch.int32), losses.view(torch.int32))
+    h2, w2 = h.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    l2 = fwloss.familywise_loss(torch.cat([F.linear(h2, w2[v0:v0 + chunk]) for v0 in range(0, V, chunk)], 1), y)
+    l2.backward()
+    assert abs(l1.float().item() - l2.float().item()) <= 1e-2 * max(1.0, abs(l2.float().item()))
+    close(h1.grad, h2.grad.double().cpu().numpy(), 2e-2)
+    close(w1.grad, w2.grad.double().cpu().numpy(), 2e-2)
