@@ -160,3 +160,31 @@ def test_fw_loss_grad_float64(ext, dev):
     assert L.dtype == torch.float64 and G.dtype == torch.float64 and k.dtype == torch.int64
     np.testing.assert_allclose(L.cpu().numpy(), ref["loss"], rtol=1e-14)
     np.testing.assert_array_equal(G.cpu().numpy(), ref["grad"])
+
+
+@pytest.mark.parametrize("C", [1000, 5001])
+def test_graph_capture_replays(ext, dev, C):
+    """The float64 path allocates nothing and records no memset: a captured call replays to the
+    eager result, with eager work between the replays (register rows and streamed rows)."""
+    rng = np.random.default_rng(C)
+    z = torch.from_numpy(rng.standard_normal((300, C))).to(dev)
+    y = torch.from_numpy(rng.integers(0, C, 300).astype(np.int64)).to(dev)
+    eager = ext.fw_forward_backward(z, y)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ext.fw_forward_backward(z, y)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ext.fw_forward_backward(z, y)
+    print(f"f64 graph replays C={C}", flush=True)
+    for it in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(out, eager):
+            assert torch.equal(a, b), f"replay {it} differs from the eager result"
+        _ = ext.fw_forward_backward(z, y)
+        torch.cuda.synchronize()
