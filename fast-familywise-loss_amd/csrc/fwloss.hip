@@ -906,12 +906,19 @@ template <int W, typename T, bool VEC>
 __device__ __forceinline__ bool scan_round(Round<T, VEC>& a, int round, int C, int wid, int lane, float* bv,
                                            int* bi, int cap, int& n, float& m, float& t) {
   constexpr int S = Round<T, VEC>::kSlots;
+  constexpr int kRoundElems = kUnit<T, VEC> * kWave * W * Round<T, VEC>::kPer;
   float lm = -INFINITY;
+  if ((round + 1) * kRoundElems <= C) {
+    // a round inside the row: nothing to mask
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    const int j = round_slot_index<W, T, VEC>(round, i, wid, lane);
-    a.x[i] = j < C ? a.x[i] : -INFINITY;
-    lm = fmaxf(lm, a.x[i]);
+    for (int i = 0; i < S; ++i) lm = fmaxf(lm, a.x[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int j = round_slot_index<W, T, VEC>(round, i, wid, lane);
+      a.x[i] = j < C ? a.x[i] : -INFINITY;
+      lm = fmaxf(lm, a.x[i]);
+    }
   }
   m = fmaxf(m, wave_max_f32(lm));
   t = fmaxf(t, bound_below_max(m));
