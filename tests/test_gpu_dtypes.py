@@ -62,6 +62,26 @@ def test_dtype_shapes(ext, dev, name, C):
 
 
 @pytest.mark.parametrize("name", sorted(DTYPES))
+@pytest.mark.parametrize("N,C", [(300, 130), (300, 1002), (300, 2046), (300, 2050), (200, 3002), (96, 8194),
+                                 (1030, 12002), (96, 30002), (16, 50002), (600, 65538)])
+def test_dtype_even_rows(ext, dev, name, N, C):
+    """16-bit rows of even length that are not whole 128-bit units run 128-bit accesses with the
+    per-dword range check (register rows, streamed rows, one block per row, split rows, two
+    passes)."""
+    z16, y = case(C, N, N * 7 + C, DTYPES[name])
+    print(f"{name} even N={N} C={C}", flush=True)
+    check(ext, dev, z16, y)
+
+
+@pytest.mark.parametrize("name", sorted(DTYPES))
+@pytest.mark.parametrize("path", [1, 2, 4, 7])
+def test_dtype_even_rows_forced(ext, dev, reset_params16, name, path):
+    z16, y = case(3002, 64, 3002 + path, DTYPES[name])
+    ext.set_params(path, 512)
+    check(ext, dev, z16, y)
+
+
+@pytest.mark.parametrize("name", sorted(DTYPES))
 @pytest.mark.parametrize("N,C", [(1024, 8193), (1100, 12000), (1030, 28672), (1023, 20000), (1500, 28673)])
 def test_dtype_long_rows_streamed(ext, dev, name, N, C):
     """16-bit rows of 8193-28672 elements stream on one wavefront each from 1024 rows on (one block
