@@ -31,8 +31,8 @@
 //   fwl_mask_to_grad, fwl_cand_to_grad   the two-op backward of the drop-in interface.
 // Other sources of the library: fwl_f64.hip (float64 logits), fwl_linear.hip (the LM head fused
 // with the loss), fwl_common.h (what they share).
-// The mean loss is reduced in fp64 in a fixed order: per-block partial sums, summed in block order
-// by the last block to finish, found by one ticket (grids of up to 512 blocks) or by a ticket per
+// The mean loss is reduced in fp64 in a fixed order: per-block partial sums, summed in a fixed
+// lane-strided order by the last block to finish, found by one ticket (grids of up to 512 blocks) or by a ticket per
 // group of 32 blocks whose last finishers share a second ticket (ticket counters in the caller's
 // workspace, each reset by its last user).
 //
@@ -47,45 +47,53 @@ namespace {
 // Unlike a device-scope fence this does not write back the L2 cache.
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Sum of the grid's nb block partials, by wavefront 0 of the last block, in a fixed order: lane l
+// adds partials l, l + 64, l + 128, ... in turn, then a butterfly over the lanes (x + y == y + x,
+// so every lane ends with the same bits).  The loads are issued kSumBatch per lane at a time so
+// that their device-scope round trips overlap.
+constexpr int kSumBatch = 8;
+__device__ double sum_partials(const double* p, unsigned nb, unsigned lane) {
+  double acc = 0.0;
+  for (unsigned base = 0; base < nb; base += kWave * kSumBatch) {
+    double v[kSumBatch];
+#pragma unroll
+    for (int k = 0; k < kSumBatch; ++k) {
+      const unsigned i = base + lane + kWave * k;
+      v[k] = i < nb ? __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0;
+    }
+#pragma unroll
+    for (int k = 0; k < kSumBatch; ++k) acc += v[k];
+  }
+#pragma unroll
+  for (int m = kWave / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  return acc;
+}
+
+// Called by every thread of a block with the block's loss sum (thread 0's value is used), after the
+// block's last barrier: wavefront 0 publishes the partial and takes a ticket; the last block's
+// wavefront 0 sums every partial and writes the mean.
 __device__ void mean_epilogue(double bsum, const Outs& o) {
-  __shared__ int s_last;
-  __shared__ double s_red[kBlock];
-  if (o.mean == nullptr) return;
-  if (gridDim.x <= kOneTicketBlocks) {
+  if (o.mean == nullptr || threadIdx.x >= kWave) return;
+  const unsigned lane = threadIdx.x;
+  const unsigned nb = gridDim.x;
+  if (nb <= kOneTicketBlocks) {
     // One ticket: the last block sums every partial (one device-scope round trip fewer than two
     // levels; with more blocks finishing together the single counter serialises too many atomics)
-    if (threadIdx.x == 0) {
+    unsigned t = 0;
+    if (lane == 0) {
       __hip_atomic_store(o.partials + blockIdx.x, bsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       wait_vmem();
-      s_last = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+      t = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __syncthreads();
-    if (!s_last) return;
-    double acc = 0.0;
-    for (unsigned i = threadIdx.x; i < gridDim.x; i += kBlock)
-      acc += __hip_atomic_load(o.partials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_red[threadIdx.x] = acc;
-    __syncthreads();
-    for (int s = kBlock / 2; s > 0; s >>= 1) {
-      if ((int)threadIdx.x < s) s_red[threadIdx.x] += s_red[threadIdx.x + s];
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-      *o.mean = (float)(s_red[0] / o.reduce_div);
-      __hip_atomic_store(o.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return;
-  }
-  // Two ticket levels: the last block of each group of kTicketGroup blocks takes the final ticket;
-  // the last of those sums every block's partial (in block order).  When many blocks finish
-  // together, no single counter serialises more than max(kTicketGroup, groups) atomics.
-  const unsigned nb = gridDim.x;
-  const unsigned g = blockIdx.x / kTicketGroup;
-  const unsigned ng = (nb + kTicketGroup - 1) / kTicketGroup;
-  const unsigned g0 = g * kTicketGroup;
-  const unsigned gsize = nb - g0 < (unsigned)kTicketGroup ? nb - g0 : (unsigned)kTicketGroup;
-  if (threadIdx.x < kWave) {   // wavefront 0
-    const int lane = (int)threadIdx.x;
+    if ((unsigned)__builtin_amdgcn_readfirstlane((int)t) != nb - 1) return;
+  } else {
+    // Two ticket levels: the last block of each group of kTicketGroup blocks takes the final
+    // ticket; the last of those sums every block's partial.  When many blocks finish together, no
+    // single counter serialises more than max(kTicketGroup, groups) atomics.
+    const unsigned g = blockIdx.x / kTicketGroup;
+    const unsigned ng = (nb + kTicketGroup - 1) / kTicketGroup;
+    const unsigned g0 = g * kTicketGroup;
+    const unsigned gsize = nb - g0 < (unsigned)kTicketGroup ? nb - g0 : (unsigned)kTicketGroup;
     unsigned* gt = o.gtickets + (size_t)g * kTicketStride;
     unsigned t = 0;
     if (lane == 0) {
@@ -96,32 +104,18 @@ __device__ void mean_epilogue(double bsum, const Outs& o) {
       wait_vmem();
       t = __hip_atomic_fetch_add(gt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    t = (unsigned)__builtin_amdgcn_readfirstlane((int)t);
-    int last = 0;
-    if (t == gsize - 1) {
-      // every partial of the group is published (each before its block's group ticket)
-      unsigned t2 = 0;
-      if (lane == 0) {
-        __hip_atomic_store(gt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        t2 = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      last = (unsigned)__builtin_amdgcn_readfirstlane((int)t2) == ng - 1;
+    if ((unsigned)__builtin_amdgcn_readfirstlane((int)t) != gsize - 1) return;
+    // every partial of the group is published (each before its block's group ticket)
+    unsigned t2 = 0;
+    if (lane == 0) {
+      __hip_atomic_store(gt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      t2 = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (lane == 0) s_last = last;
+    if ((unsigned)__builtin_amdgcn_readfirstlane((int)t2) != ng - 1) return;
   }
-  __syncthreads();
-  if (!s_last) return;
-  double acc = 0.0;
-  for (unsigned i = threadIdx.x; i < nb; i += kBlock)
-    acc += __hip_atomic_load(o.partials + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  s_red[threadIdx.x] = acc;
-  __syncthreads();
-  for (int s = kBlock / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) s_red[threadIdx.x] += s_red[threadIdx.x + s];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    *o.mean = (float)(s_red[0] / o.reduce_div);
+  const double total = sum_partials(o.partials, nb, lane);
+  if (lane == 0) {
+    *o.mean = (float)(total / o.reduce_div);
     __hip_atomic_store(o.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }

@@ -376,6 +376,25 @@ def test_deterministic(ext, dev):
     assert a["mean"] == b["mean"]
 
 
+@pytest.mark.parametrize("N,C", [(1 << 20, 16), (300000, 100), (1500, 1000), (700, 3000)])
+def test_mean_over_many_blocks(ext, dev, N, C):
+    """The mean of grids from a few hundred blocks to several thousand (one and two ticket levels;
+    several batches of partial loads in the last block): equal to the fp64 mean of the per-row
+    losses, and bit-identical on a repeated call (tickets reset, fixed summation order)."""
+    rng = np.random.default_rng(N + C)
+    z = rng.standard_normal((N, C), dtype=np.float32)
+    y = rng.integers(0, C, N, dtype=np.int64)
+    zt, yt = to_dev(dev, z, y)
+    out = []
+    for rdiv in (float(N), 1.0, float(N)):
+        H, loss, mean, kappa, grad = ext.fw_forward_backward(zt, yt, 1.0 / N, rdiv)
+        torch.cuda.synchronize()
+        ref = loss.double().sum().item() / rdiv
+        assert abs(mean.item() - ref) <= 1e-6 * max(1.0, abs(ref)), (rdiv, mean.item(), ref)
+        out.append(mean.item())
+    assert out[0] == out[2]
+
+
 # ---------------------------------------------------------------- full-size configurations
 
 def _row_properties(zt, yt, H, loss, kappa, grad, scale):
