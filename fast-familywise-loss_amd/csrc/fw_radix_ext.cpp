@@ -386,7 +386,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("row_scale"), py::arg("want_dh") = true, py::arg("want_dw") = true);
   m.def("fw_scale_grad", &fw_scale_grad, "In-place grad *= grad_output (device-side skip when 1)");
   m.def("set_params", &set_params, "Dispatch switches: path (0 auto, 1 wave registers, 2 block stream, 3 block generic, "
-        "4 wave stream, 5 wave generic, 6 short-row segments, 7 split rows), cand_cap",
+        "4 wave stream, 5 wave generic, 6 short-row segments, 7 split rows, 8 = 1 without line-aligned windows), cand_cap",
         py::arg("path"), py::arg("cand_cap") = 512);
   m.def("get_params", &get_params);
 }

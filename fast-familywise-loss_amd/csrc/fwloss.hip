@@ -133,6 +133,21 @@ __device__ __forceinline__ void load_row(rsrc_t row, int lane, float* x) {
 }
 
 
+// Line-aligned window of a 16-byte aligned fp32 row: the resource starts at the row's first
+// 128-byte line boundary, `a` units (0..7) before the row, so every 1024-byte load of the
+// wavefront covers exactly 8 lines (a row start inside a line makes it 9).  Lanes of the first
+// load that fall in front of the row take an offset past the resource (they read 0, like lanes
+// past the row's end); nothing outside the row is read.
+__device__ __forceinline__ uint32_t window_unit(int k, int lane, int a) {
+  return k == 0 && lane < a ? (kOffNone >> 4) : (uint32_t)(lane + kWave * k);
+}
+
+template <int NV>
+__device__ __forceinline__ void load_row_window(rsrc_t row, int lane, int a, float* x) {
+#pragma unroll
+  for (int k = 0; k < NV; ++k) load_unit<float, true>(row, window_unit(k, lane, a), x + 4 * k);
+}
+
 // element index of register slot i of this lane
 template <typename T, bool VEC>
 __device__ __forceinline__ int slot_index(int i, int lane) {
@@ -143,11 +158,12 @@ __device__ __forceinline__ int slot_index(int i, int lane) {
 
 // element j of the register row (j wavefront-uniform, 0 <= j < C): the uniform slot index makes
 // the register array access an indexed register move (s_set_gpr_idx), then one lane read
+// (shift: units of the row's line-aligned window in front of its first element)
 template <typename T, int NV, bool VEC>
-__device__ __forceinline__ float element_at(const float* x, int j) {
+__device__ __forceinline__ float element_at(const float* x, int j, int shift = 0) {
   constexpr int U = kUnit<T, VEC>;
-  const int slot = uniform(U * ((j / U) >> 6) + (j % U));
-  const int owner = uniform((j / U) & 63);
+  const int slot = uniform(U * ((j / U + shift) >> 6) + (j % U));
+  const int owner = uniform((j / U + shift) & 63);
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[slot]), owner));
 }
 
@@ -189,17 +205,31 @@ __device__ __forceinline__ void row_bias(int C, int lane, float* bias) {
 // One row: x holds it (E values per lane).  Once its candidates are in the LDS list, the loads of
 // the next row (resource `next`, zero-size if there is none) are issued into xn, so they are in
 // flight during the selection and the stores of this row; x stays for the outputs.
-template <typename T, int MODE, int NV, bool V4>
+// AW: x and xn hold line-aligned windows (load_row_window), the current row `a` units into its
+// window and the next row `an` units into its own; the gradient row shares the logits row's
+// offset within its line.
+template <typename T, int MODE, int NV, bool V4, bool AW>
 __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t y64, int C, int lane,
                                                  float* x, float* xn, const float* bias, float* cl, int* ci_lds,
-                                                 const Outs& o) {
+                                                 const Outs& o, int a, int an) {
   constexpr int U = kUnit<T, V4>;
   constexpr int E = U * NV;
   static_assert(std::is_same<T, float>::value || MODE != kMask, "16-bit logits: no mask output");
+  static_assert(!AW || (std::is_same<T, float>::value && V4 && MODE == kGrad), "windows: fp32 gradient rows");
   const bool yok = y64 >= 0 && y64 < C;
   const int yr = yok ? (int)y64 : -1;
+  if constexpr (AW) {
+    // the row's units are a .. a + C/4 - 1 of the window
 #pragma unroll
-  for (int i = 0; i < E; ++i) x[i] += bias[i];
+    for (int k = 0; k < NV; ++k) {
+      const float b = (uint32_t)(lane + kWave * k - a) < (uint32_t)(C / 4) ? -0.0f : -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * k + e] += b;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < E; ++i) x[i] += bias[i];
+  }
 
   // row maximum and the first lower bound max - 1 (rounded down: every support entry passes)
   float lm = x[0];
@@ -224,9 +254,10 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
       n += __popcll(b);
     }
   }
-  const float zy = yok ? element_at<T, NV, V4>(x, yr) : NAN;
+  const float zy = yok ? element_at<T, NV, V4>(x, yr, AW ? a : 0) : NAN;
   __builtin_amdgcn_wave_barrier();
-  load_row<T, NV, V4>(next, lane, xn);
+  if constexpr (AW) load_row_window<NV>(next, lane, an, xn);
+  else load_row<T, NV, V4>(next, lane, xn);
 
   double tau;
   int kappa;
@@ -237,9 +268,10 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
 
   const float inv = (float)(o.scale / (double)kappa);
   if constexpr (MODE == kGrad) {
-    const rsrc_t out = make_rsrc(static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>,
-                                 (uint32_t)(kElemBytes<T> * C));
-    const int qy = yr / U, ky = yr >= 0 ? qy >> 6 : -1, ly = qy & 63, ey = yr % U;
+    const int sh = AW ? a : 0;
+    const rsrc_t out = make_rsrc(static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T> - 16 * sh,
+                                 (uint32_t)(kElemBytes<T> * C + 16 * sh));
+    const int qy = yr / U + sh, ky = yr >= 0 ? qy >> 6 : -1, ly = qy & 63, ey = yr % U;
     // the four values a gradient element can take, encoded once per row
     const uint32_t b_inv = encode<T>(inv), b_lab_in = encode<T>(inv - o.scale_f);
     const uint32_t b_lab_out = encode<T>(0.0f - o.scale_f);
@@ -252,7 +284,7 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
 #pragma unroll
         for (int e = 0; e < U; ++e) g[e] = e == ey ? (x[U * k + e] > Hf ? b_lab_in : b_lab_out) : g[e];
       }
-      store_unit_bits<T, V4>(out, (uint32_t)(lane + kWave * k), g);
+      store_unit_bits<T, V4>(out, AW ? window_unit(k, lane, a) : (uint32_t)(lane + kWave * k), g);
     }
   } else if constexpr (MODE == kMask) {
     const rsrc_t out = make_rsrc(o.mask + r * (int64_t)C, (uint32_t)C);
@@ -316,7 +348,10 @@ __device__ __forceinline__ void mirror_row_stores(int lane) {
 // A wavefront handles rows w + k*stride, k < nrows <= 64.  Their labels arrive in one gather load
 // before the first row, and their H, loss and kappa stay in registers (row k in lane k) until the
 // last row, so the only memory instructions inside the row loop are the row loads and stores.
-template <typename T, int MODE, int NV, bool V4>
+// AW: rows read and written through line-aligned windows (load_row_window); the host takes it
+// for 16-byte aligned fp32 gradient rows whose logits and gradient share their offsets within a
+// 128-byte line, when the widest window still fits NV units per lane.
+template <typename T, int MODE, int NV, bool V4, bool AW>
 __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__ z,
                                                         const int64_t* __restrict__ tgt, int64_t N,
                                                         int C, Outs o) {
@@ -332,8 +367,16 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
   const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;   // this wavefront's rows: w + k*stride
   const int nrows = w < N ? (int)((N - 1 - w) / stride + 1) : 0;   // <= kRowsPerWave (host grid)
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
+  // units of row k's window in front of the row (0 without windows)
+  auto row_shift = [&](int k) {
+    if constexpr (!AW) return 0;
+    const uintptr_t p = reinterpret_cast<uintptr_t>(z) + (uintptr_t)((w + (int64_t)k * stride) * C * kElemBytes<T>);
+    return k < nrows ? uniform((int)((p >> 4) & 7)) : 0;
+  };
   auto row_rsrc = [&](int k) {
-    return k < nrows ? make_rsrc(static_cast<const char*>(z) + (w + (int64_t)k * stride) * C * kElemBytes<T>, row_bytes)
+    const int sh = row_shift(k);
+    return k < nrows ? make_rsrc(static_cast<const char*>(z) + (w + (int64_t)k * stride) * C * kElemBytes<T> - 16 * sh,
+                                 row_bytes + 16u * (uint32_t)sh)
                      : make_rsrc(z, 0u);
   };
   const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
@@ -341,12 +384,13 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
   int my_kappa = 0;
   double lsum = 0.0;
   float xa[E], xb[E], bias[E];
-  row_bias<T, NV, V4>(C, lane, bias);
+  if constexpr (!AW) row_bias<T, NV, V4>(C, lane, bias);
   auto row = [&](int k, float* x, float* xn) {
     const int64_t y = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
                       (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
-    const RowResult res = process_row<T, MODE, NV, V4>(w + (int64_t)k * stride, row_rsrc(k + 1), y, C, lane, x, xn,
-                                                    bias, s_list[wid], s_idx[wid], o);
+    const RowResult res = process_row<T, MODE, NV, V4, AW>(w + (int64_t)k * stride, row_rsrc(k + 1), y, C, lane, x,
+                                                        xn, bias, s_list[wid], s_idx[wid], o, row_shift(k),
+                                                        row_shift(k + 1));
     lsum += (double)res.loss;
     if (lane == k) {
       my_H = res.H;
@@ -355,7 +399,8 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
     }
   };
   if (nrows > 0) {
-    load_row<T, NV, V4>(row_rsrc(0), lane, xa);
+    if constexpr (AW) load_row_window<NV>(row_rsrc(0), lane, row_shift(0), xa);
+    else load_row<T, NV, V4>(row_rsrc(0), lane, xa);
     __builtin_amdgcn_sched_barrier(0);   // keep the mirror stores after the loads
     mirror_row_stores<T, MODE, NV, V4>(lane);
     __builtin_amdgcn_sched_barrier(0);
@@ -1961,6 +2006,7 @@ __global__ void fwl_empty_mean(float* mean, double reduce_div) {
 
 int g_path = 0;
 int g_cap = kCapMax;
+bool g_no_window = false;   // path 8: path 1 without line-aligned windows
 
 int blocks_row(int64_t N) { return (int)(N < kMaxBlocksRow ? (N > 0 ? N : 1) : kMaxBlocksRow); }
 
@@ -2029,11 +2075,42 @@ int wave_grid(int64_t N, int64_t row_bytes, int resident) {
 
 
 
-template <typename T, int MODE, int NV, bool V4>
+template <typename T, int MODE, int NV, bool V4, bool AW = false>
 void launch_wave(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
-  const void* k = reinterpret_cast<const void*>(&fwl_wave_rows<T, MODE, NV, V4>);
+  const void* k = reinterpret_cast<const void*>(&fwl_wave_rows<T, MODE, NV, V4, AW>);
   const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
-  hipLaunchKernelGGL((fwl_wave_rows<T, MODE, NV, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+  hipLaunchKernelGGL((fwl_wave_rows<T, MODE, NV, V4, AW>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+}
+
+// Largest window shift (units of 16 bytes, 0..7) over the rows of a launch that may read and
+// write fp32 rows through line-aligned windows, or -1 where windows do not apply: rows of
+// 16-byte multiples from 16-byte aligned logits and gradient that share their offset within a
+// 128-byte line, and not every row already line aligned.  Row starts repeat mod 128 every 8 rows.
+int window_shift_max(const void* z, const void* g, int64_t N, int C) {
+  const uintptr_t zp = reinterpret_cast<uintptr_t>(z), gp = reinterpret_cast<uintptr_t>(g);
+  if (g == nullptr || C % 4 != 0 || zp % 16 != 0 || gp % 16 != 0 || (zp - gp) % 128 != 0) return -1;
+  int mx = 0;
+  for (int64_t r = 0; r < 8 && r < N; ++r) {
+    const int a = (int)(((zp + (uintptr_t)(r * 4 * C)) >> 4) & 7);
+    mx = a > mx ? a : mx;
+  }
+  return mx > 0 ? mx : -1;
+}
+
+// register tier of a row of `units` 128-bit units per lane: NV = 1, 2, 3, 4, 5, 6 or 8
+inline int wave_tier(int units) {
+  return units <= 384 ? (units + 63) / 64 : 8;
+}
+
+template <typename T, int MODE, int NV>
+void launch_wave_v4(const void* z, const int64_t* y, int64_t N, int C, bool aw, const Outs& o, hipStream_t s) {
+  if constexpr (std::is_same<T, float>::value && MODE == kGrad) {
+    if (aw) {
+      launch_wave<T, MODE, NV, true, true>(z, y, N, C, o, s);
+      return;
+    }
+  }
+  launch_wave<T, MODE, NV, true>(z, y, N, C, o, s);
 }
 
 // register rows: NV units per lane, the smallest power of two that covers the row (E <= 32)
@@ -2044,14 +2121,20 @@ void dispatch_wave(const void* z, const int64_t* y, int64_t N, int C, bool v4, c
     // per-lane work grows with NV whatever the row length: tiers at every 64 units up to 6
     constexpr int U = kUnit<T, true>;
     const int units = (C + U - 1) / U;
-    if (units <= 64) launch_wave<T, MODE, 1, true>(z, y, N, C, o, s);
-    else if (units <= 128) launch_wave<T, MODE, 2, true>(z, y, N, C, o, s);
-    else if (units <= 192) launch_wave<T, MODE, 3, true>(z, y, N, C, o, s);
-    else if (units <= 256) launch_wave<T, MODE, 4, true>(z, y, N, C, o, s);
+    // line-aligned windows where the widest one stays in the row's own tier (fp32 gradient rows)
+    bool aw = false;
+    if constexpr (std::is_same<T, float>::value && MODE == kGrad) {
+      const int sh = window_shift_max(z, o.grad, N, C);
+      aw = sh > 0 && wave_tier(units + sh) == wave_tier(units) && !g_no_window;
+    }
+    if (units <= 64) launch_wave_v4<T, MODE, 1>(z, y, N, C, aw, o, s);
+    else if (units <= 128) launch_wave_v4<T, MODE, 2>(z, y, N, C, aw, o, s);
+    else if (units <= 192) launch_wave_v4<T, MODE, 3>(z, y, N, C, aw, o, s);
+    else if (units <= 256) launch_wave_v4<T, MODE, 4>(z, y, N, C, aw, o, s);
     else if constexpr (U == 4) {
-      if (units <= 320) launch_wave<T, MODE, 5, true>(z, y, N, C, o, s);
-      else if (units <= 384) launch_wave<T, MODE, 6, true>(z, y, N, C, o, s);
-      else launch_wave<T, MODE, 8, true>(z, y, N, C, o, s);
+      if (units <= 320) launch_wave_v4<T, MODE, 5>(z, y, N, C, aw, o, s);
+      else if (units <= 384) launch_wave_v4<T, MODE, 6>(z, y, N, C, aw, o, s);
+      else launch_wave_v4<T, MODE, 8>(z, y, N, C, aw, o, s);
     }
   } else {
     if (C <= 64) launch_wave<T, MODE, 1, false>(z, y, N, C, o, s);
@@ -2297,7 +2380,7 @@ int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scal
   const bool even16 = kElemBytes<T> == 2 && MODE == kGrad && C % 2 == 0 && C > 256 && aligned(z, 4) &&
                       aligned(o.grad, 4);
   const bool v4 = aligned_rows || (std::is_same<T, float>::value && MODE != kMask) || even16;
-  int path = g_path;
+  int path = g_path == 8 ? 1 : g_path;
   // measured on MI355X: registers win up to 2048 for 128-bit rows, up to 1024 for rows accessed
   // one element at a time; one streaming wavefront per row up to 8192; one block per row beyond
   const int max_wave_c = v4 ? kMaxWaveC : kMaxWaveC1;
@@ -2528,8 +2611,9 @@ int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_
 }
 
 int fwl_set_params(int path, int cand_cap) {
-  if (path < 0 || path > 7 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
+  if (path < 0 || path > 8 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
   g_path = path;
+  g_no_window = path == 8;
   g_cap = cand_cap;
   return FWL_OK;
 }

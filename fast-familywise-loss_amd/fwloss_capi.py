@@ -99,16 +99,19 @@ class Workspace:
         return self.buf
 
 
-def forward_backward(z, y, scale=None, reduce_div=None, ws=None):
-    """Fused op through the C ABI.  Returns dict(H, loss, mean, kappa, grad)."""
+def forward_backward(z, y, scale=None, reduce_div=None, ws=None, grad=None):
+    """Fused op through the C ABI.  Returns dict(H, loss, mean, kappa, grad); `grad` may supply the
+    gradient buffer (a contiguous [N, C] float32 tensor, e.g. a view at any offset)."""
     N, C = z.shape
     scale = (1.0 / N if N else 1.0) if scale is None else scale
     reduce_div = float(N) if reduce_div is None else reduce_div
     ws = ws or Workspace(z.device)
     buf = ws.get(N, C)
+    if grad is not None and (tuple(grad.shape) != (N, C) or grad.dtype != torch.float32 or not grad.is_contiguous()):
+        raise ValueError("grad must be a contiguous float32 [N, C] tensor")
     out = dict(H=torch.empty(N, device=z.device), loss=torch.empty(N, device=z.device),
                mean=torch.empty((), device=z.device), kappa=torch.empty(N, dtype=torch.int32, device=z.device),
-               grad=torch.empty_like(z))
+               grad=torch.empty_like(z) if grad is None else grad)
     rc = lib().fwl_forward_backward(_ptr(z), _ptr(y), N, C, scale, reduce_div, _ptr(out["H"]), _ptr(out["loss"]),
                                     _ptr(out["mean"]), _ptr(out["kappa"]), _ptr(out["grad"]), _ptr(buf),
                                     buf.numel(), _stream())

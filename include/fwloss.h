@@ -214,7 +214,10 @@ int fwl_linear_dweight(int dtype, const void* hidden, int64_t N, int64_t V, int6
  *              7 = split rows: one block per (row, chunk of >= 4096 elements) streams the chunk
  *              and keeps its own support, then one block per row resolves their union (at most
  *              128 rows, and a workspace of fwl_workspace_bytes(N, C) taken with path 7 set;
- *              otherwise path 2 runs).
+ *              otherwise path 2 runs),
+ *              8 = path 1 without line-aligned windows (path 1 reads and writes 16-byte aligned
+ *              fp32 gradient rows through windows that start on the row's first 128-byte line
+ *              boundary, where the logits and gradient share their offsets within a line).
  *   cand_cap:  LDS candidate capacity per wavefront of paths 2 and 4, in [64, 512] (512 =
  *              default); smaller values make rows overflow into the generic solve sooner.
  * Returns FWL_ERR_INVALID_ARG for values out of range. */

@@ -357,6 +357,40 @@ def test_misaligned_and_strided_inputs(ext, dev):
     assert_parity(fused(ext, zt2, yt), oracle.definition(z2, yt.cpu().numpy()), z2)
 
 
+@pytest.mark.parametrize("N,C,off", [(300, 1000, 0), (300, 996, 4), (5, 996, 4), (300, 1000, 4), (300, 480, 4),
+                                      (300, 2000, 0), (300, 1996, 12), (300, 64, 4), (300, 500, 8)])
+def test_line_aligned_windows(ext, dev, reset_params, N, C, off):
+    """Register rows read and written through line-aligned windows (path 1) against the oracle and
+    bit-for-bit against path 8 (no windows), with logits and gradient both starting `off` floats
+    into a 128-byte line; labels include both row ends; the floats around the gradient rows stay
+    untouched.  (996, 4) and (1996, 12) take every shift 0..7; (1000, 4) and (500, 8) need a wider
+    tier and run without windows."""
+    rng = np.random.default_rng(N + C + off)
+    pad = 64
+    zbuf = torch.from_numpy(rng.standard_normal(N * C + pad).astype(np.float32)).to(dev)
+    zt = zbuf[off:off + N * C].view(N, C)
+    y = rng.integers(0, C, N)
+    y[:4] = [0, C - 1, C - 1, 0][:min(4, N)]
+    yt = torch.from_numpy(y).to(dev)
+    z = zt.cpu().numpy()
+    ref = oracle.definition(z, y)
+    outs = []
+    for path in (1, 8):
+        ext.set_params(path, 512)
+        gbuf = torch.full((N * C + pad,), 7.0, device=dev)
+        out = fwloss_capi.forward_backward(zt, yt, grad=gbuf[off:off + N * C].view(N, C))
+        torch.cuda.synchronize()
+        g = gbuf.cpu().numpy()
+        assert np.all(g[:off] == 7.0) and np.all(g[off + N * C:] == 7.0)
+        res = {k: v.cpu().numpy() for k, v in out.items()}
+        np.testing.assert_array_equal(res["kappa"], ref["kappa"])
+        assert bits_equal(res["H"], ref["H"]) and bits_equal(res["loss"], ref["loss"])
+        assert bits_equal(res["grad"], ref["grad"])
+        outs.append(res)
+    for k in ("H", "loss", "kappa", "grad", "mean"):
+        assert bits_equal(outs[0][k], outs[1][k]), k
+
+
 def test_empty_batch(ext, dev):
     zt = torch.empty((0, 10), device=dev)
     yt = torch.empty((0,), dtype=torch.int64, device=dev)

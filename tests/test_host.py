@@ -179,7 +179,8 @@ def test_set_params_validation_and_round_trip():
     assert L.fwl_get_params(ctypes.byref(p), ctypes.byref(c)) == 0
     saved = (p.value, c.value)
     try:
-        assert L.fwl_set_params(8, 512) == 1
+        assert L.fwl_set_params(9, 512) == 1
+        assert L.fwl_set_params(8, 512) == 0
         assert L.fwl_set_params(7, 512) == 0
         assert L.fwl_set_params(-1, 512) == 1
         assert L.fwl_set_params(2, 63) == 1
@@ -253,7 +254,7 @@ def test_extension_rejects_cpu_and_bad_inputs():
     with pytest.raises(KeyError):   # what the reference's dict lookup raises (src/cpu/fwcpp.py:19)
         fwloss.familywise_loss(z, y, reduction="max")
     with pytest.raises(RuntimeError):
-        fwloss.set_params(8, 512)
+        fwloss.set_params(9, 512)
     assert tuple(fwloss.get_params()) == (0, 512)
     libs = fwloss.native_libraries()
     assert any(p.endswith("libfwloss.so") for p in libs) and any("fw_radix_cuda" in p for p in libs)
