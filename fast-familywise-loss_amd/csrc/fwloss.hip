@@ -133,19 +133,19 @@ __device__ __forceinline__ void load_row(rsrc_t row, int lane, float* x) {
 }
 
 
-// Line-aligned window of a 16-byte aligned fp32 row: the resource starts at the row's first
-// 128-byte line boundary, `a` units (0..7) before the row, so every 1024-byte load of the
-// wavefront covers exactly 8 lines (a row start inside a line makes it 9).  Lanes of the first
-// load that fall in front of the row take an offset past the resource (they read 0, like lanes
-// past the row's end); nothing outside the row is read.
+// Line-aligned window of a row of 16-byte units from a 16-byte aligned start: the resource starts
+// at the row's first 128-byte line boundary, `a` units (0..7) before the row, so every 1024-byte
+// load of the wavefront covers exactly 8 lines (a row start inside a line makes it 9).  Lanes of
+// the first load that fall in front of the row take an offset past the resource (they read 0,
+// like lanes past the row's end); nothing outside the row is read.  a = 0 is plain addressing.
 __device__ __forceinline__ uint32_t window_unit(int k, int lane, int a) {
   return k == 0 && lane < a ? (kOffNone >> 4) : (uint32_t)(lane + kWave * k);
 }
 
-template <int NV>
+template <typename T, int NV>
 __device__ __forceinline__ void load_row_window(rsrc_t row, int lane, int a, float* x) {
 #pragma unroll
-  for (int k = 0; k < NV; ++k) load_unit<float, true>(row, window_unit(k, lane, a), x + 4 * k);
+  for (int k = 0; k < NV; ++k) load_unit<T, true>(row, window_unit(k, lane, a), x + kUnit<T, true> * k);
 }
 
 // element index of register slot i of this lane
@@ -219,12 +219,12 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
   const bool yok = y64 >= 0 && y64 < C;
   const int yr = yok ? (int)y64 : -1;
   if constexpr (AW) {
-    // the row's units are a .. a + C/4 - 1 of the window
+    // the row's units are a .. a + C/U - 1 of the window
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const float b = (uint32_t)(lane + kWave * k - a) < (uint32_t)(C / 4) ? -0.0f : -INFINITY;
+      const float b = (uint32_t)(lane + kWave * k - a) < (uint32_t)(C / U) ? -0.0f : -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[4 * k + e] += b;
+      for (int e = 0; e < U; ++e) x[U * k + e] += b;
     }
   } else {
 #pragma unroll
@@ -256,7 +256,7 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
   }
   const float zy = yok ? element_at<T, NV, V4>(x, yr, AW ? a : 0) : NAN;
   __builtin_amdgcn_wave_barrier();
-  if constexpr (AW) load_row_window<NV>(next, lane, an, xn);
+  if constexpr (AW) load_row_window<T, NV>(next, lane, an, xn);
   else load_row<T, NV, V4>(next, lane, xn);
 
   double tau;
@@ -348,9 +348,12 @@ __device__ __forceinline__ void mirror_row_stores(int lane) {
 // A wavefront handles rows w + k*stride, k < nrows <= 64.  Their labels arrive in one gather load
 // before the first row, and their H, loss and kappa stay in registers (row k in lane k) until the
 // last row, so the only memory instructions inside the row loop are the row loads and stores.
-// AW: rows read and written through line-aligned windows (load_row_window); the host takes it
-// for 16-byte aligned fp32 gradient rows whose logits and gradient share their offsets within a
-// 128-byte line, when the widest window still fits NV units per lane.
+// AW: rows read and written through line-aligned windows (load_row_window); the host takes it for
+// fp32 gradient rows of 16-byte multiples from 16-byte aligned logits and gradient that share their
+// offsets within a 128-byte line.  A row whose window would not fit NV units per lane keeps plain
+// addressing (shift 0).  16-bit rows keep plain addressing throughout: their kernel is issue-bound,
+// and the per-row window arithmetic measured 4% slower there (bf16 65536 x 1000: 59.5 against
+// 57.2 us; 65536 x 2000: 105.9 against 102.1).
 template <typename T, int MODE, int NV, bool V4, bool AW>
 __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__ z,
                                                         const int64_t* __restrict__ tgt, int64_t N,
@@ -367,11 +370,14 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
   const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;   // this wavefront's rows: w + k*stride
   const int nrows = w < N ? (int)((N - 1 - w) / stride + 1) : 0;   // <= kRowsPerWave (host grid)
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
-  // units of row k's window in front of the row (0 without windows)
+  // units of row k's window in front of the row (0 without windows, or where the window would
+  // not fit the lanes' NV units)
+  const int fit = kWave * NV - (C + kUnit<T, V4> - 1) / kUnit<T, V4>;
   auto row_shift = [&](int k) {
     if constexpr (!AW) return 0;
     const uintptr_t p = reinterpret_cast<uintptr_t>(z) + (uintptr_t)((w + (int64_t)k * stride) * C * kElemBytes<T>);
-    return k < nrows ? uniform((int)((p >> 4) & 7)) : 0;
+    const int a = (int)((p >> 4) & 7);
+    return k < nrows && a <= fit ? uniform(a) : 0;
   };
   auto row_rsrc = [&](int k) {
     const int sh = row_shift(k);
@@ -399,7 +405,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
     }
   };
   if (nrows > 0) {
-    if constexpr (AW) load_row_window<NV>(row_rsrc(0), lane, row_shift(0), xa);
+    if constexpr (AW) load_row_window<T, NV>(row_rsrc(0), lane, row_shift(0), xa);
     else load_row<T, NV, V4>(row_rsrc(0), lane, xa);
     __builtin_amdgcn_sched_barrier(0);   // keep the mirror stores after the loads
     mirror_row_stores<T, MODE, NV, V4>(lane);
@@ -2082,19 +2088,19 @@ void launch_wave(const void* z, const int64_t* y, int64_t N, int C, const Outs& 
   hipLaunchKernelGGL((fwl_wave_rows<T, MODE, NV, V4, AW>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
 }
 
-// Largest window shift (units of 16 bytes, 0..7) over the rows of a launch that may read and
-// write fp32 rows through line-aligned windows, or -1 where windows do not apply: rows of
-// 16-byte multiples from 16-byte aligned logits and gradient that share their offset within a
-// 128-byte line, and not every row already line aligned.  Row starts repeat mod 128 every 8 rows.
-int window_shift_max(const void* z, const void* g, int64_t N, int C) {
+// Whether line-aligned windows apply to a launch of the register-row kernel with `spare` unused
+// 16-byte units per lane row (64*NV minus the row's units): rows of 16-byte multiples from
+// 16-byte aligned logits and gradient that share their offset within a 128-byte line, with at
+// least one row starting inside a line whose window fits (shift <= spare).  Row starts repeat mod
+// 128 every 8 rows.
+bool windows_apply(const void* z, const void* g, int64_t N, int64_t row_bytes, int spare) {
   const uintptr_t zp = reinterpret_cast<uintptr_t>(z), gp = reinterpret_cast<uintptr_t>(g);
-  if (g == nullptr || C % 4 != 0 || zp % 16 != 0 || gp % 16 != 0 || (zp - gp) % 128 != 0) return -1;
-  int mx = 0;
+  if (g == nullptr || row_bytes % 16 != 0 || zp % 16 != 0 || gp % 16 != 0 || (zp - gp) % 128 != 0) return false;
   for (int64_t r = 0; r < 8 && r < N; ++r) {
-    const int a = (int)(((zp + (uintptr_t)(r * 4 * C)) >> 4) & 7);
-    mx = a > mx ? a : mx;
+    const int a = (int)(((zp + (uintptr_t)(r * row_bytes)) >> 4) & 7);
+    if (a > 0 && a <= spare) return true;
   }
-  return mx > 0 ? mx : -1;
+  return false;
 }
 
 // register tier of a row of `units` 128-bit units per lane: NV = 1, 2, 3, 4, 5, 6 or 8
@@ -2121,12 +2127,10 @@ void dispatch_wave(const void* z, const int64_t* y, int64_t N, int C, bool v4, c
     // per-lane work grows with NV whatever the row length: tiers at every 64 units up to 6
     constexpr int U = kUnit<T, true>;
     const int units = (C + U - 1) / U;
-    // line-aligned windows where the widest one stays in the row's own tier (fp32 gradient rows)
+    // line-aligned windows for the fp32 gradient rows whose window fits the row's own tier
     bool aw = false;
-    if constexpr (std::is_same<T, float>::value && MODE == kGrad) {
-      const int sh = window_shift_max(z, o.grad, N, C);
-      aw = sh > 0 && wave_tier(units + sh) == wave_tier(units) && !g_no_window;
-    }
+    if constexpr (std::is_same<T, float>::value && MODE == kGrad)
+      aw = !g_no_window && windows_apply(z, o.grad, N, (int64_t)C * kElemBytes<T>, kWave * wave_tier(units) - units);
     if (units <= 64) launch_wave_v4<T, MODE, 1>(z, y, N, C, aw, o, s);
     else if (units <= 128) launch_wave_v4<T, MODE, 2>(z, y, N, C, aw, o, s);
     else if (units <= 192) launch_wave_v4<T, MODE, 3>(z, y, N, C, aw, o, s);

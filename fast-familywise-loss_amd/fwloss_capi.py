@@ -122,16 +122,19 @@ def forward_backward(z, y, scale=None, reduce_div=None, ws=None, grad=None):
 DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}   # enum fwl_dtype
 
 
-def forward_backward_typed(z, y, scale=None, reduce_div=None, ws=None):
-    """fwl_forward_backward_typed for float32/bfloat16/float16 logits; grad has the logits' dtype."""
+def forward_backward_typed(z, y, scale=None, reduce_div=None, ws=None, grad=None):
+    """fwl_forward_backward_typed for float32/bfloat16/float16 logits; grad has the logits' dtype
+    (`grad` may supply it: a contiguous [N, C] tensor of that dtype, e.g. a view at any offset)."""
     N, C = z.shape
     scale = (1.0 / N if N else 1.0) if scale is None else scale
     reduce_div = float(N) if reduce_div is None else reduce_div
     ws = ws or Workspace(z.device)
     buf = ws.get(N, C)
+    if grad is not None and (tuple(grad.shape) != (N, C) or grad.dtype != z.dtype or not grad.is_contiguous()):
+        raise ValueError("grad must be a contiguous [N, C] tensor of the logits' dtype")
     out = dict(H=torch.empty(N, device=z.device), loss=torch.empty(N, device=z.device),
                mean=torch.empty((), device=z.device), kappa=torch.empty(N, dtype=torch.int32, device=z.device),
-               grad=torch.empty_like(z))
+               grad=torch.empty_like(z) if grad is None else grad)
     rc = lib().fwl_forward_backward_typed(DTYPES[z.dtype], _ptr(z), _ptr(y), N, C, scale, reduce_div, _ptr(out["H"]),
                                           _ptr(out["loss"]), _ptr(out["mean"]), _ptr(out["kappa"]), _ptr(out["grad"]),
                                           _ptr(buf), buf.numel(), _stream())

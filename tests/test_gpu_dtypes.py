@@ -215,3 +215,35 @@ def test_c_abi_typed(ext, dev):
 def reset_params16(ext):
     yield
     ext.set_params(0, 512)
+
+
+@pytest.mark.parametrize("name", sorted(DTYPES))
+@pytest.mark.parametrize("C,off", [(1000, 0), (1000, 8), (504, 24), (2000, 0), (8, 0)])
+def test_dtype_offset_rows(ext, dev, name, C, off):
+    """16-bit rows of 128-bit units starting `off` elements into a 128-byte line (logits and
+    gradient alike), through path 1 and path 8 (16-bit rows keep plain addressing on both): the
+    oracle's values bit-for-bit, and the elements around the gradient rows stay untouched."""
+    N, pad = 300, 64
+    z16, y = case(C, N, C + off, DTYPES[name])
+    y[:2] = [0, C - 1]
+    zbuf = torch.zeros(N * C + pad, dtype=z16.dtype, device=dev)
+    zbuf[off:off + N * C] = z16.reshape(-1).to(dev)
+    zt = zbuf[off:off + N * C].view(N, C)
+    yt = torch.from_numpy(y).to(dev)
+    ref, g16 = expected(z16, y, 1.0 / N)
+    grads = []
+    try:
+        for path in (1, 8):
+            ext.set_params(path, 512)
+            gbuf = torch.full((N * C + pad,), 3.0, dtype=z16.dtype, device=dev)
+            out = fwloss_capi.forward_backward_typed(zt, yt, grad=gbuf[off:off + N * C].view(N, C))
+            torch.cuda.synchronize()
+            g = gbuf.cpu()
+            assert bool((g[:off] == 3.0).all()) and bool((g[off + N * C:] == 3.0).all())
+            np.testing.assert_array_equal(out["kappa"].cpu().numpy(), ref["kappa"])
+            np.testing.assert_array_equal(out["H"].cpu().numpy().view(np.uint32), ref["H"].view(np.uint32))
+            np.testing.assert_array_equal(out["loss"].cpu().numpy().view(np.uint32), ref["loss"].view(np.uint32))
+            grads.append(out["grad"].cpu())
+            assert torch.equal(grads[-1].view(torch.int16), g16.view(torch.int16))
+    finally:
+        ext.set_params(0, 512)

@@ -358,13 +358,14 @@ def test_misaligned_and_strided_inputs(ext, dev):
 
 
 @pytest.mark.parametrize("N,C,off", [(300, 1000, 0), (300, 996, 4), (5, 996, 4), (300, 1000, 4), (300, 480, 4),
-                                      (300, 2000, 0), (300, 1996, 12), (300, 64, 4), (300, 500, 8)])
+                                      (300, 2000, 0), (300, 1996, 12), (300, 64, 4), (300, 500, 8), (300, 1020, 0),
+                                      (300, 252, 0)])
 def test_line_aligned_windows(ext, dev, reset_params, N, C, off):
     """Register rows read and written through line-aligned windows (path 1) against the oracle and
     bit-for-bit against path 8 (no windows), with logits and gradient both starting `off` floats
     into a 128-byte line; labels include both row ends; the floats around the gradient rows stay
-    untouched.  (996, 4) and (1996, 12) take every shift 0..7; (1000, 4) and (500, 8) need a wider
-    tier and run without windows."""
+    untouched.  (996, 4) and (1996, 12) take every shift 0..7; in (1000, 4), (500, 8), (1020, 0)
+    and (252, 0) only the rows whose window fits the tier take one, the others plain addressing."""
     rng = np.random.default_rng(N + C + off)
     pad = 64
     zbuf = torch.from_numpy(rng.standard_normal(N * C + pad).astype(np.float32)).to(dev)
