@@ -392,6 +392,35 @@ def test_line_aligned_windows(ext, dev, reset_params, N, C, off):
         assert bits_equal(outs[0][k], outs[1][k]), k
 
 
+@pytest.mark.parametrize("N,C,off", [(300, 1000, 0), (300, 996, 4), (300, 1020, 0), (300, 64, 4), (5, 1000, 0)])
+def test_offset_mask_rows(ext, dev, reset_params, N, C, off):
+    """The drop-in mask forward (fw_forward_small) on register rows (paths 1 and 8; mask rows keep
+    plain addressing on both), logits starting `off` floats into a 128-byte line: the support mask,
+    H, losses, kappa and the gradient from the mask against the oracle, and the two paths
+    bit-for-bit."""
+    rng = np.random.default_rng(N + 7 * C + off)
+    zbuf = torch.from_numpy(rng.standard_normal(N * C + 64).astype(np.float32)).to(dev)
+    zt = zbuf[off:off + N * C].view(N, C)
+    y = rng.integers(0, C, N)
+    y[:2] = [0, C - 1][:min(2, N)]
+    yt = torch.from_numpy(y).to(dev)
+    z = zt.cpu().numpy()
+    ref = oracle.definition(z, y)
+    outs = []
+    for path in (1, 8):
+        ext.set_params(path, 512)
+        H, losses, mean, kappa, sel = ext.fw_forward_small(zt, yt)
+        grad = ext.fw_backward_small(yt, sel, kappa)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(sel.cpu().numpy(), z > ref["tau"][:, None])
+        out = dict(H=H.cpu().numpy(), loss=losses.cpu().numpy(), mean=float(mean.cpu()), kappa=kappa.cpu().numpy(),
+                   grad=grad.cpu().numpy())
+        assert_parity(out, ref, z)
+        outs.append(out)
+    for k in ("H", "loss", "kappa", "grad"):
+        assert bits_equal(outs[0][k], outs[1][k]), k
+
+
 def test_empty_batch(ext, dev):
     zt = torch.empty((0, 10), device=dev)
     yt = torch.empty((0,), dtype=torch.int64, device=dev)
