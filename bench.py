@@ -31,7 +31,14 @@ for _p in (PKG, ORACLE):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
-METRIC = "rows/sec and achieved HBM GB/s (% of peak), fwd+bwd, N=65536 C=1000 fp32"
+DTYPE_NAME = {"f32": "fp32", "bf16": "bf16", "f16": "fp16", "f64": "fp64"}
+
+
+def metric_for(N, C, dtype, dist=None):
+    """The metric of the workload actually run: BASELINE.json's metric string for the headline, the
+    same wording with this run's shape, dtype and input distribution otherwise."""
+    m = f"rows/sec and achieved HBM GB/s (% of peak), fwd+bwd, N={N} C={C} {DTYPE_NAME[dtype]}"
+    return m if dist is None else f"{m}, {dist}"
 HBM_PEAK_GBS = 8000.0
 
 
@@ -50,6 +57,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--dist", default=None, choices=["gauss", "laplace", "mixture"],
+                    help="logits from the reference harness's distributions (data_io.py:8-83) at the "
+                         "configuration's shape instead of the configuration's own recipe")
+    ap.add_argument("--sigma", type=float, default=1.0, help="--dist: the distributions' sigma")
     ap.add_argument("--rows", type=int, default=None,
                     help="rows of the batch (default: the configuration's N; few rows of a long "
                          "configuration run the split-row kernels)")
@@ -70,15 +81,18 @@ def parse():
     return ap.parse_args()
 
 
-def traffic_for(kernel_tag, cfg):
-    """HBM bytes per launch of the fused kernel, from the rocprofv3 summary committed under profiles/
-    (FETCH_SIZE and WRITE_SIZE passes, each scaled by what the counter reads for a plain copy)."""
+def profile_for(kernel_tag, cfg):
+    """(HBM bytes per launch, average kernel duration in ns) of the fused kernel from the rocprofv3
+    summary committed under profiles/ (FETCH_SIZE and WRITE_SIZE passes, each scaled by what the
+    counter reads for a plain copy; the kernel-trace average), or None where not profiled."""
     path = os.path.join(ROOT, "profiles", f"{kernel_tag}_{cfg}.md")
     if not os.path.isfile(path):
-        return None
+        return None, None
     with open(path) as f:
-        m = re.search(r"^hbm_bytes_per_launch: (\d+)$", f.read(), re.M)
-    return int(m.group(1)) if m else None
+        text = f.read()
+    m = re.search(r"^hbm_bytes_per_launch: (\d+)$", text, re.M)
+    d = re.search(r"^avg_duration_ns: (\d+)$", text, re.M)
+    return (int(m.group(1)) if m else None), (int(d.group(1)) if d else None)
 
 
 def _median_time(call, seconds, min_calls):
@@ -99,7 +113,15 @@ def cpu_baseline(z_np, y_np, seconds):
     import torch
     import oracle
     N, C = z_np.shape
-    threads = torch.get_num_threads()
+    # every CPU of the process's affinity mask, within the CPU share the host grants this job
+    # (OMP_NUM_THREADS, where the host sets it); both counts are reported
+    affinity = len(os.sched_getaffinity(0))
+    threads = affinity
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
     ref = oracle.load_ref()
     nthreads = [threads]
     if ref is not None:
@@ -123,8 +145,8 @@ def cpu_baseline(z_np, y_np, seconds):
     try:
         med1, times1 = _median_time(call, seconds / 3, 3)
     finally:
-        torch.set_num_threads(threads)
-    return {"value": N / med, "unit": "rows/s", "cores": threads, "kind": kind,
+        torch.set_num_threads(prev_threads)
+    return {"value": N / med, "unit": "rows/s", "cores": threads, "affinity_cpus": affinity, "kind": kind,
             "sample": f"{label}: full {N}x{C} batch, loss + dense gradient per call, median of {len(times)} "
                       f"calls ({sum(times):.1f} s of CPU work), {threads} threads",
             "ms_per_call": med * 1e3, "gbps": alg_bytes(N, C) / med / 1e9,
@@ -242,9 +264,17 @@ def main():
         return
 
     dev = torch.device("cuda:0")
-    z_np, y_np = fwloss_data.make(args.config, N=args.rows, seed=0)
+    if args.dist is None:
+        z_np, y_np = fwloss_data.make(args.config, N=args.rows, seed=0)
+        recipe = f"{args.config} recipe (fwloss_data.make)"
+    else:
+        shape = fwloss_data.CONFIGS[args.config]
+        z_np, y_np = fwloss_data.make_dist(args.dist, args.rows or shape["N"], shape["C"], args.sigma, seed=0)
+        recipe = f"{args.dist} sigma={args.sigma:g} (fwloss_data.make_dist, data_io.py:8-83)"
     N, C = z_np.shape
     cfg_tag = args.config if args.rows is None else f"{args.config}_{N}rows"
+    if args.dist is not None:
+        cfg_tag += f"_{args.dist}{args.sigma:g}"
     tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16, "f64": torch.float64}[args.dtype]
     sets = []
     for s in range(args.sets):
@@ -319,9 +349,9 @@ def main():
         tag = "fwl_wave_stream_rows"
     else:
         tag = "fwl_block_rows"
-    traffic = traffic_for(tag, cfg_tag if args.dtype == "f32" else f"{cfg_tag}_{args.dtype}")
+    traffic, prof_ns = profile_for(tag, cfg_tag if args.dtype == "f32" else f"{cfg_tag}_{args.dtype}")
     result = {
-        "metric": METRIC,
+        "metric": metric_for(N, C, args.dtype, None if args.dist is None else recipe),
         "value": N * args.steps / wall,
         "unit": "rows/s",
         "n_gpus": 1,
@@ -334,15 +364,18 @@ def main():
         "dtype": args.dtype,
         "data": "synthetic",
         "config": {"workload": f"{cfg_tag} fused FW loss forward+backward, N={N} C={C} {args.dtype} logits "
-                               "(fwloss_data.make), labels uniform int64, buffers rotated over "
+                               f"({recipe}), labels uniform int64, buffers rotated over "
                                f"{args.sets} sets", "N": N, "C": C, "op": "fw_forward_backward",
+                   "dist": args.dist or args.config, "sigma": args.sigma if args.dist else None,
                    "parallelism": "single GPU"},
         "gbps": nbytes / (ms_per_step * 1e-3) / 1e9,
         "hbm_frac": nbytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "kernel_ms": kern_ms,
         "two_op_ms_per_step": two_op_ms,
         "roofline": {"bound": "hbm", "kernel": tag, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "alg_bytes": nbytes},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "alg_bytes": nbytes,
+                     # the same fraction from the committed kernel-trace average (profiles/)
+                     "frac_profiled": None if prof_ns is None else nbytes / prof_ns / HBM_PEAK_GBS},
     }
     if not args.no_cpu_baseline and args.dtype == "f32":
         result["cpu_baseline"] = cpu_baseline(z_np, y_np, args.cpu_seconds)

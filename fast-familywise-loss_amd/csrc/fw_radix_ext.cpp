@@ -7,7 +7,8 @@
 // Differences from the reference host code (src/cuda/fw_radix_argmax.cu:1381-1609), all additive:
 //   * targets, kappas, masks and candidate tensors are validated (the reference checks only the
 //     logits of the forwards, :1383-1386, :1419-1421);
-//   * non-contiguous inputs are made contiguous instead of being read with the wrong strides;
+//   * non-contiguous inputs are made contiguous instead of being read with the wrong strides (the
+//     fused op reads rows of logits in place at any row stride);
 //   * launches go on the current stream instead of the legacy default stream;
 //   * any K is accepted by every op (the reference's small kernel has no bound check above
 //     K = 10000, :1405-1408).
@@ -18,6 +19,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "fwloss.h"
 
@@ -31,22 +33,24 @@ void check_status(int rc, const char* op) {
   TORCH_CHECK(rc == FWL_OK, op, ": ", fwl_status_string(rc));
 }
 
-// One zero-initialised workspace per (device, stream).  The kernels leave it zeroed again, and
-// work on one stream is ordered, so calls never share a workspace concurrently.
+// One workspace per (device, stream): calls on one stream are ordered, so they never use a
+// workspace concurrently, and the library keeps no state in it from one call to the next.  A
+// workspace that has to grow is replaced, but the superseded ones stay allocated until the process
+// ends: a HIP graph captured on the stream keeps the device address it captured, and its replays
+// must not write into memory the caching allocator has handed to another tensor since.  Growth is
+// geometric, so the superseded ones add up to less than the current one.
 at::Tensor workspace(const at::Tensor& like, size_t bytes) {
   static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, at::Tensor> cache;
+  static std::map<std::pair<int, hipStream_t>, std::vector<at::Tensor>> cache;
   const auto key = std::make_pair((int)like.get_device(), current_stream(like));
   std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find(key);
-  if (it == cache.end() || (size_t)it->second.numel() < bytes) {
-    const size_t grow = bytes < 65536 ? 65536 : bytes;
-    at::Tensor ws = at::zeros({(int64_t)grow}, like.options().dtype(at::kByte));
-    if (it == cache.end()) cache.emplace(key, ws);
-    else it->second = ws;
-    return ws;
+  std::vector<at::Tensor>& held = cache[key];
+  if (held.empty() || (size_t)held.back().numel() < bytes) {
+    size_t grow = bytes < 65536 ? 65536 : bytes;
+    if (!held.empty() && grow < 2 * (size_t)held.back().numel()) grow = 2 * (size_t)held.back().numel();
+    held.push_back(at::empty({(int64_t)grow}, like.options().dtype(at::kByte)));
   }
-  return it->second;
+  return held.back();
 }
 
 void check_logits(const at::Tensor& logits) {
@@ -186,12 +190,17 @@ at::Tensor fw_backward(at::Tensor logits, at::Tensor targets, at::Tensor H, at::
   return grad;
 }
 
-// fw_forward_backward(logits, targets, scale=1/N, reduce_div=N) -> [H, losses, reduced, kappa, grad]
+// fw_forward_backward(logits, targets, scale=1/N, reduce_div=N, path=-1, cand_cap=-1, losses64=False)
+//   -> [H, losses, reduced, kappa, grad] (+ [losses64] when asked)
 // The fused hot path: one launch, logits read once, dense gradient written once.  Logits may be
 // float32, bfloat16 or float16 (grad has the logits' dtype, H, losses and reduced are float32) or
-// float64 (every output fp64, as the reference CPU path computes them).
-std::vector<at::Tensor> fw_forward_backward(at::Tensor logits, at::Tensor targets, double scale,
-                                            double reduce_div) {
+// float64 (every output fp64, as the reference CPU path computes them).  Rows of logits may lie any
+// distance apart (a column slice such as logits[:, 1:] is read in place; grad is contiguous).
+// path/cand_cap >= 0 set this call's dispatch switches (fwl_options); -1 keeps set_params's.
+// losses64: also the fp64 per-row losses, the dtype of the reference's fw_loss_grad
+// (src/cpu/fw_cpu.cpp:750-757).
+std::vector<at::Tensor> fw_forward_backward(at::Tensor logits, at::Tensor targets, double scale, double reduce_div,
+                                            int64_t path, int64_t cand_cap, bool losses64) {
   c10::DeviceGuard guard(logits.device());
   if (logits.is_cuda() && logits.dim() == 2 && logits.scalar_type() == torch::kFloat64) {
     // fp64 logits (the reference CPU path's other dtype): fp64 H, losses, reduced and grad
@@ -208,20 +217,49 @@ std::vector<at::Tensor> fw_forward_backward(at::Tensor logits, at::Tensor target
                                           H.data_ptr<double>(), losses.data_ptr<double>(), mean.data_ptr<double>(),
                                           kappa.data_ptr<int32_t>(), grad.data_ptr<double>(), current_stream(z)),
                  "fw_forward_backward");
+    if (losses64) return {H, losses, mean, kappa, grad, losses};
     return {H, losses, mean, kappa, grad};
   }
-  Common c = prepare(logits, targets, true);
-  const int64_t N = c.logits.size(0), K = c.logits.size(1);
+  TORCH_CHECK(logits.is_cuda(), "logits must be a CUDA tensor");
+  TORCH_CHECK(logits.dim() == 2, "logits must have shape [N, K]");
+  const int dtype = fwl_dtype_of(logits);
+  TORCH_CHECK(logits.size(1) >= 1, "logits must have K >= 1 classes");
+  check_rows(targets, logits, torch::kInt64, "targets");
+  // rows in place when their elements are adjacent; anything else is copied
+  at::Tensor z = logits;
+  if (z.size(0) > 1 ? !(z.stride(1) == 1 && z.stride(0) >= z.size(1)) : z.stride(1) != 1) z = z.contiguous();
+  const int64_t N = z.size(0), K = z.size(1);
+  const int64_t ld = N > 1 ? z.stride(0) : K;
+  at::Tensor y = targets.contiguous();
   if (scale < 0) scale = N > 0 ? 1.0 / (double)N : 1.0;
   if (reduce_div < 0) reduce_div = (double)N;
-  at::Tensor grad = torch::empty({N, K}, c.logits.options());
-  const int rc = fwl_forward_backward_typed(
-      fwl_dtype_of(c.logits), c.logits.data_ptr(), c.targets.data_ptr<int64_t>(), N, K, scale, reduce_div,
-      c.H.data_ptr<float>(), c.losses.data_ptr<float>(), c.mean.data_ptr<float>(),
-      c.kappa.data_ptr<int32_t>(), grad.data_ptr(), c.ws.data_ptr(), (size_t)c.ws.numel(),
-      current_stream(c.logits));
+  const auto f32 = z.options().dtype(torch::kFloat32);
+  at::Tensor H = torch::empty({N}, f32), losses = torch::empty({N}, f32), mean = torch::empty({}, f32);
+  at::Tensor kappa = torch::empty({N}, z.options().dtype(torch::kInt32));
+  at::Tensor l64;
+  if (losses64) l64 = torch::empty({N}, z.options().dtype(torch::kFloat64));
+  at::Tensor grad = torch::empty({N, K}, z.options().memory_format(at::MemoryFormat::Contiguous));
+  fwl_options opt;
+  opt.path = 0;
+  opt.cand_cap = 0;
+  const bool own = path >= 0 || cand_cap >= 0;
+  if (own) {
+    int dp = 0, dc = 0;
+    fwl_get_params(&dp, &dc);
+    opt.path = path >= 0 ? (int)path : dp;
+    opt.cand_cap = cand_cap >= 0 ? (int)cand_cap : dc;
+  }
+  const size_t ws_bytes = fwl_workspace_bytes_ex(N, K, own ? &opt : nullptr);
+  TORCH_CHECK(ws_bytes > 0, "fw_forward_backward: path must be in [0, 8] and cand_cap in [64, 512]");
+  at::Tensor ws = workspace(z, ws_bytes);
+  const int rc = fwl_forward_backward_ex(dtype, z.data_ptr(), ld, y.data_ptr<int64_t>(), N, K, scale, reduce_div,
+                                         H.data_ptr<float>(), losses.data_ptr<float>(),
+                                         losses64 ? l64.data_ptr<double>() : nullptr, mean.data_ptr<float>(),
+                                         kappa.data_ptr<int32_t>(), grad.data_ptr(), ws.data_ptr(),
+                                         (size_t)ws.numel(), own ? &opt : nullptr, current_stream(z));
   check_status(rc, "fw_forward_backward");
-  return {c.H, c.losses, c.mean, c.kappa, grad};
+  if (losses64) return {H, losses, mean, kappa, grad, l64};
+  return {H, losses, mean, kappa, grad};
 }
 
 // grad *= grad_output (a 0-dim factor, or one factor per row), in place; rows whose factor is 1
@@ -377,7 +415,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("fw_forward_small", &fw_forward_small, "FW loss forward with the support mask (MI355X)");
   m.def("fw_backward_small", &fw_backward_small, "FW loss backward from the support mask (MI355X)");
   m.def("fw_forward_backward", &fw_forward_backward, "Fused FW loss forward + backward (MI355X)",
-        py::arg("logits"), py::arg("targets"), py::arg("scale") = -1.0, py::arg("reduce_div") = -1.0);
+        py::arg("logits"), py::arg("targets"), py::arg("scale") = -1.0, py::arg("reduce_div") = -1.0,
+        py::arg("path") = -1, py::arg("cand_cap") = -1, py::arg("losses64") = false);
   m.def("fw_linear_state", &fw_linear_state, "Per-row state of the linear layer fused with the loss");
   m.def("fw_linear_chunk", &fw_linear_chunk, "Merge one vocabulary chunk of logits into the state");
   m.def("fw_linear_finish", &fw_linear_finish, "H, losses, kappa, support columns and overflow flags");
@@ -385,8 +424,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("hidden"), py::arg("weight"), py::arg("targets"), py::arg("kappa"), py::arg("support"),
         py::arg("row_scale"), py::arg("want_dh") = true, py::arg("want_dw") = true);
   m.def("fw_scale_grad", &fw_scale_grad, "In-place grad *= grad_output (device-side skip when 1)");
-  m.def("set_params", &set_params, "Dispatch switches: path (0 auto, 1 wave registers, 2 block stream, 3 block generic, "
-        "4 wave stream, 5 wave generic, 6 short-row segments, 7 split rows, 8 = 1 without line-aligned windows), cand_cap",
+  m.def("set_params", &set_params, "Default dispatch switches: path (0 auto, 1 wave registers, 2 block stream, "
+        "3 block stream with the overflow solve forced, 4 wave stream, 5 wave stream with the overflow solve forced, "
+        "6 short-row segments, 7 split rows, 8 = 1 without line-aligned windows), cand_cap",
         py::arg("path"), py::arg("cand_cap") = 512);
   m.def("get_params", &get_params);
 }

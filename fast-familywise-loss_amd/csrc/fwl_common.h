@@ -13,6 +13,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <map>
 #include <type_traits>
 #include <mutex>
@@ -165,13 +166,7 @@ constexpr int kMaxBlocksWave = 2048;   // grid cap of fwl_wave_rows (4 rows in f
 constexpr int kMaxBlocksRow = 4096;    // grid cap of fwl_block_rows
 constexpr int kStreamUnroll = 4;       // 128-bit loads per lane per streaming round
 constexpr int kRoundSlotsV1 = 16;      // 32-bit loads per lane per streaming round (unaligned rows)
-constexpr size_t kWsHeader = 256;      // the final ticket counter; then the mean's partial sums
-constexpr int kTicketGroup = 32;       // blocks per first-level ticket of the mean
-constexpr unsigned kOneTicketBlocks = 512;   // grids up to this size take a single ticket level
-                                             // (65536 x 1000, 512 blocks: 96.2 us against 96.9
-                                             // with two levels; 16384 x 100, 1280 blocks finishing
-                                             // together: 18.3 us against 10.0)
-constexpr int kTicketStride = 16;      // first-level tickets 64 bytes apart
+constexpr size_t kWsAlign = 256;       // alignment of the workspace's parts
 constexpr uint32_t kOffNone = 0x7FFFFFF0u;   // a buffer offset past every resource: access dropped
 
 enum Mode : int { kGrad = 0, kMask = 1, kCand = 2 };
@@ -179,8 +174,9 @@ enum Mode : int { kGrad = 0, kMask = 1, kCand = 2 };
 struct Outs {
   float* H;
   float* loss;
+  float* mean;         // the mean loss (null: none requested)
+  double* loss64;      // optional fp64 per-row losses (the value `loss` rounds)
   int32_t* kappa;
-  float* mean;
   void* grad;   // element type of the logits
   uint8_t* mask;
   float* cval;
@@ -189,9 +185,10 @@ struct Outs {
   double scale;        // gradient scale (1/N for the mean reduction)
   double reduce_div;   // mean = sum(losses) / reduce_div
   float scale_f;
-  unsigned* ticket;     // final ticket
-  double* partials;     // one per block
-  unsigned* gtickets;   // one per group (kTicketStride apart)
+  double* partials;    // one fp64 loss sum per block (null: no mean requested)
+  float* ovf_lo;       // streaming kernels: per row, a lower bound on tau for rows whose lists
+  float* ovf_mx;       // overflowed (NaN for the others) and the row maximum; null: no deferral
+  int64_t ld;          // row stride of the logits, in elements (>= C)
   int force_generic;
   int cap;             // LDS candidate capacity per wavefront (<= kCapMax)
   int cstride;         // candidate-list mode: row stride of cval/cidx (C for the drop-in op)
@@ -308,6 +305,16 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   v += dpp_mov_f64<kRowHalfMirror>(v);
   v += dpp_mov_f64<kRowMirror>(v);
   return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+}
+
+// integer sum over the wavefront, returned in every lane
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  v += dpp_mov<kQuadXor1>(v);
+  v += dpp_mov<kQuadXor2>(v);
+  v += dpp_mov<kRowHalfMirror>(v);
+  v += dpp_mov<kRowMirror>(v);
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
 __device__ __forceinline__ double wave_max_f64(double v) {
@@ -448,6 +455,39 @@ __device__ __forceinline__ double prev_f64(double r) {
   else if (r < 0.0) b += 1u;
   else b = 0x8000000000000001ull;
   return __longlong_as_double((int64_t)b);
+}
+
+// next float above a finite value
+__device__ __forceinline__ float next_f32(float r) {
+  unsigned b = __float_as_uint(r);
+  if (r > 0.0f) b += 1u;
+  else if (r < 0.0f) b -= 1u;
+  else b = 1u;
+  return __uint_as_float(b);
+}
+
+// A float strictly below H = (s - 1)/c, where s is the fp64 sum (any order) of c values of
+// magnitude <= B: below the exact H of those values whatever the rounding of the sum (at most
+// c*B*2^-53 per term added, so c*B*2^-53 after the division by c), of the subtraction and of the
+// division.  H of any non-empty subset of a row is <= tau (fw_cpu.cpp:201-211), so the result is
+// a safe lower bound on tau.  NaN/inf inputs give -inf (no bound).
+__device__ __forceinline__ float safe_lower(double s, int c, float B) {
+  if (c <= 0) return -INFINITY;
+  const double h = (s - 1.0) / (double)c;
+  const double err = ((double)c * (double)B + (fabs(s) + 1.0) / (double)c + fabs(h)) * 0x1p-51;
+  const float r = rd32(h - err);
+  return isfinite(r) ? prev_f32(r) : -INFINITY;
+}
+
+// safe_lower for a sum s accumulated partly in fp32 (per-lane partial sums of up to 16 values of
+// magnitude <= B, rounded at most 16 times each, then added in fp64): the rounding of each term's
+// contribution is below B*2^-19, so the bound moves down by B*2^-19 more.
+__device__ __forceinline__ float safe_lower32(double s, int c, float B) {
+  if (c <= 0) return -INFINITY;
+  const double h = (s - 1.0) / (double)c - (double)B * 0x1p-19;
+  const double err = ((double)c * (double)B + (fabs(s) + 1.0) / (double)c + fabs(h)) * 0x1p-51;
+  const float r = rd32(h - err);
+  return isfinite(r) ? prev_f32(r) : -INFINITY;
 }
 
 // largest float <= m - 1 (tau >= m - 1, so every support entry is > this bound).  For |m| >= 2^53

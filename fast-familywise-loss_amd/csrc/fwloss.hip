@@ -41,83 +41,40 @@
 namespace {
 
 // ------------------------------------------------------------------------------------------------
-// mean of the per-row losses: block partial sums, the last block reduces them (fixed order)
+// mean of the per-row losses: each block stores its fp64 partial sum; fwl_mean_finish, launched
+// after the rows on the same stream, adds the partials in a fixed order.  No counters: the
+// workspace holds no state from one call to the next.
 
 // Wait until this thread's earlier vector memory operations have completed (stores acknowledged).
 // Unlike a device-scope fence this does not write back the L2 cache.
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Sum of the grid's nb block partials, by wavefront 0 of the last block, in a fixed order: lane l
-// adds partials l, l + 64, l + 128, ... in turn, then a butterfly over the lanes (x + y == y + x,
-// so every lane ends with the same bits).  The loads are issued kSumBatch per lane at a time so
-// that their device-scope round trips overlap.
+// Called by every thread of a block with the block's loss sum (thread 0's value is used).
+__device__ __forceinline__ void mean_epilogue(double bsum, const Outs& o) {
+  if (o.partials != nullptr && threadIdx.x == 0) o.partials[blockIdx.x] = bsum;
+}
+
+// One wavefront: lane l adds partials l, l + 64, l + 128, ... in turn (loads issued kSumBatch at a
+// time, so that their round trips overlap), then a butterfly over the lanes (x + y == y + x, so
+// every lane ends with the same bits); mean = total / reduce_div.
 constexpr int kSumBatch = 8;
-__device__ double sum_partials(const double* p, unsigned nb, unsigned lane) {
+__global__ __launch_bounds__(kWave) void fwl_mean_finish(const double* __restrict__ p, unsigned nb,
+                                                        double reduce_div, float* __restrict__ mean) {
+  const unsigned lane = threadIdx.x;
   double acc = 0.0;
   for (unsigned base = 0; base < nb; base += kWave * kSumBatch) {
     double v[kSumBatch];
 #pragma unroll
     for (int k = 0; k < kSumBatch; ++k) {
       const unsigned i = base + lane + kWave * k;
-      v[k] = i < nb ? __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0;
+      v[k] = i < nb ? p[i] : 0.0;
     }
 #pragma unroll
     for (int k = 0; k < kSumBatch; ++k) acc += v[k];
   }
 #pragma unroll
   for (int m = kWave / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
-  return acc;
-}
-
-// Called by every thread of a block with the block's loss sum (thread 0's value is used), after the
-// block's last barrier: wavefront 0 publishes the partial and takes a ticket; the last block's
-// wavefront 0 sums every partial and writes the mean.
-__device__ void mean_epilogue(double bsum, const Outs& o) {
-  if (o.mean == nullptr || threadIdx.x >= kWave) return;
-  const unsigned lane = threadIdx.x;
-  const unsigned nb = gridDim.x;
-  if (nb <= kOneTicketBlocks) {
-    // One ticket: the last block sums every partial (one device-scope round trip fewer than two
-    // levels; with more blocks finishing together the single counter serialises too many atomics)
-    unsigned t = 0;
-    if (lane == 0) {
-      __hip_atomic_store(o.partials + blockIdx.x, bsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      wait_vmem();
-      t = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if ((unsigned)__builtin_amdgcn_readfirstlane((int)t) != nb - 1) return;
-  } else {
-    // Two ticket levels: the last block of each group of kTicketGroup blocks takes the final
-    // ticket; the last of those sums every block's partial.  When many blocks finish together, no
-    // single counter serialises more than max(kTicketGroup, groups) atomics.
-    const unsigned g = blockIdx.x / kTicketGroup;
-    const unsigned ng = (nb + kTicketGroup - 1) / kTicketGroup;
-    const unsigned g0 = g * kTicketGroup;
-    const unsigned gsize = nb - g0 < (unsigned)kTicketGroup ? nb - g0 : (unsigned)kTicketGroup;
-    unsigned* gt = o.gtickets + (size_t)g * kTicketStride;
-    unsigned t = 0;
-    if (lane == 0) {
-      // The partial is an agent-scope atomic store (coherent across the XCDs' L2 caches); once it
-      // has completed, the ticket increment publishes it.  A device-scope fence here would write
-      // back the whole L2 of the XCD at the end of every block.
-      __hip_atomic_store(o.partials + blockIdx.x, bsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      wait_vmem();
-      t = __hip_atomic_fetch_add(gt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if ((unsigned)__builtin_amdgcn_readfirstlane((int)t) != gsize - 1) return;
-    // every partial of the group is published (each before its block's group ticket)
-    unsigned t2 = 0;
-    if (lane == 0) {
-      __hip_atomic_store(gt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      t2 = __hip_atomic_fetch_add(o.ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if ((unsigned)__builtin_amdgcn_readfirstlane((int)t2) != ng - 1) return;
-  }
-  const double total = sum_partials(o.partials, nb, lane);
-  if (lane == 0) {
-    *o.mean = (float)(total / o.reduce_div);
-    __hip_atomic_store(o.ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (lane == 0) *mean = (float)(acc / reduce_div);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -184,6 +141,7 @@ __device__ __forceinline__ int wave_excl_scan_i32(int v, int& total) {
 struct RowResult {
   float H;
   float loss;
+  double l64;
   int kappa;
 };
 
@@ -200,6 +158,94 @@ __device__ __forceinline__ void row_bias(int C, int lane, float* bias) {
   constexpr int E = kUnit<T, VEC> * NV;
 #pragma unroll
   for (int i = 0; i < E; ++i) bias[i] = slot_index<T, VEC>(i, lane) < C ? -0.0f : -INFINITY;
+}
+
+// A register row with more than 64 candidates z > t0, all of them in its LDS list cl (n of them;
+// indices in ci_lds in candidate-list mode).  The tau of the 64 lane maxima, a subset of the row, is
+// a lower bound t1 on tau, usually close to it: the list is cut at t1, and a list of at most 64
+// entries is sorted (resolve_list); a longer one takes fixed-point steps t <- H({z > t}) from t1
+// (each iterate <= tau, the set shrinking every step until it is the support), and after
+// kListSteps of them a bisection over the keys of (t1, m], so that the passes over the list are
+// bounded.  Works on the LDS list only: the register row stays untouched for the outputs.
+constexpr int kListSteps = 32;
+template <int MODE>
+__device__ __forceinline__ void solve_many(float lm, float t0, float m, int lane, float* cl, int* ci_lds, int& n,
+                                           double& tau, int& kappa, uint64_t& support) {
+  const double tl = select_tier<kWave>(lm, kWave, lane);
+  float t1 = t0;
+  if (tl == tl) {
+    const double B = (double)fabsf(m) + 1.0;
+    const float r = rd32(tl - ((double)kWave * B + fabs(tl) + 1.0) * 0x1p-51);
+    if (isfinite(r)) t1 = fmaxf(t0, prev_f32(r));
+  }
+  // keep the list entries > t1 (order kept)
+  int w = 0;
+  for (int p0 = 0; p0 < n; p0 += kWave) {
+    const int p = p0 + lane;
+    const float v = p < n ? cl[p] : -INFINITY;
+    int id = 0;
+    if constexpr (MODE == kCand) id = p < n ? ci_lds[p] : 0;
+    const bool keep = v > t1;
+    const uint64_t b = ballot(keep);
+    __builtin_amdgcn_wave_barrier();
+    if (keep) {
+      cl[w + rank_in(b)] = v;
+      if constexpr (MODE == kCand) ci_lds[w + rank_in(b)] = id;
+    }
+    w += __popcll(b);
+    __builtin_amdgcn_wave_barrier();
+  }
+  n = w;
+  if (n <= kWave) {
+    resolve_list(cl, n, t1, m, lane, tau, kappa, support);
+    return;
+  }
+  support = 0;
+  double t = (double)t1, s;
+  int c;
+  list_sum_count(cl, n, t1, lane, s, c);
+  bool conv = false;
+  tau = NAN;
+  kappa = 0;
+  for (int it = 0; it < kListSteps; ++it) {
+    const double tn = (s - 1.0) / (double)c;
+    double s2;
+    int c2;
+    list_sum_count(cl, n, rd32(tn), lane, s2, c2);
+    if (c2 == c || !(tn > t)) {
+      tau = tn;
+      kappa = c2;
+      conv = true;
+      break;
+    }
+    t = tn;
+    s = s2;
+    c = c2;
+  }
+  if (!conv) {
+    // G(a) >= 1 > G(b) over keys: tau in [a, b), the support {z > a}
+    int ka = fkey(t1 + 0.0f), kb = fkey(m + 0.0f);
+    while ((int64_t)kb - ka > 1) {
+      const int km = (int)(((int64_t)ka + kb) >> 1);
+      const float v = fkey_inv(km);
+      double s3;
+      int c3;
+      list_sum_count(cl, n, v, lane, s3, c3);
+      if (s3 - (double)c3 * (double)v >= 1.0) ka = km;
+      else kb = km;
+    }
+    double s3;
+    int c3;
+    list_sum_count(cl, n, fkey_inv(ka), lane, s3, c3);
+    kappa = c3;
+    tau = c3 > 0 ? (s3 - 1.0) / (double)c3 : NAN;
+  }
+  const double tc = clamp_below_max(tau, m);
+  if (tc != tau) {
+    double s3;
+    tau = tc;
+    list_sum_count(cl, n, rd32(tau), lane, s3, kappa);
+  }
 }
 
 // One row: x holds it (E values per lane).  Once its candidates are in the LDS list, the loads of
@@ -262,7 +308,8 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
   double tau;
   int kappa;
   uint64_t support;
-  resolve_list(cl, n, t0, m, lane, tau, kappa, support);
+  if (n <= kWave) resolve_list(cl, n, t0, m, lane, tau, kappa, support);
+  else solve_many<MODE>(lm, t0, m, lane, cl, ci_lds, n, tau, kappa, support);
   const float Hf = rd32(tau);
   __builtin_amdgcn_wave_barrier();
 
@@ -321,7 +368,8 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
 
   RowResult res;
   res.H = Hf;
-  res.loss = (float)((1.0 - (double)zy) + tau);
+  res.l64 = (1.0 - (double)zy) + tau;
+  res.loss = (float)res.l64;
   res.kappa = kappa;
   return res;
 }
@@ -376,18 +424,19 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
   const int fit = kWave * NV - (C + kUnit<T, V4> - 1) / kUnit<T, V4>;
   auto row_shift = [&](int k) {
     if constexpr (!AW) return 0;
-    const uintptr_t p = reinterpret_cast<uintptr_t>(z) + (uintptr_t)((w + (int64_t)k * stride) * C * kElemBytes<T>);
+    const uintptr_t p = reinterpret_cast<uintptr_t>(z) + (uintptr_t)((w + (int64_t)k * stride) * o.ld * kElemBytes<T>);
     const int a = (int)((p >> 4) & 7);
     return k < nrows && a <= fit ? uniform(a) : 0;
   };
   auto row_rsrc = [&](int k) {
     const int sh = row_shift(k);
-    return k < nrows ? make_rsrc(static_cast<const char*>(z) + (w + (int64_t)k * stride) * C * kElemBytes<T> - 16 * sh,
+    return k < nrows ? make_rsrc(static_cast<const char*>(z) + (w + (int64_t)k * stride) * o.ld * kElemBytes<T> - 16 * sh,
                                  row_bytes + 16u * (uint32_t)sh)
                      : make_rsrc(z, 0u);
   };
   const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
   float my_H = 0.0f, my_loss = 0.0f;
+  double my_l64 = 0.0;
   int my_kappa = 0;
   double lsum = 0.0;
   float xa[E], xb[E], bias[E];
@@ -402,6 +451,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
     if (lane == k) {
       my_H = res.H;
       my_loss = res.loss;
+      my_l64 = res.l64;
       my_kappa = res.kappa;
     }
   };
@@ -424,6 +474,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_rows(const void* __restrict__
     const int64_t r = w + (int64_t)lane * stride;
     if (o.H) o.H[r] = my_H;
     if (o.loss) o.loss[r] = my_loss;
+    if (o.loss64) o.loss64[r] = my_l64;
     if (o.kappa) o.kappa[r] = my_kappa;
     if constexpr (MODE == kCand) o.ccnt[r] = my_kappa;
   }
@@ -631,15 +682,16 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
   const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;
   const int ngroups = w < G ? (int)((G - 1 - w) / stride + 1) : 0;   // <= kWave / R (host grid)
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
-  const int units_row = C / U;                               // V4 rows: C is a multiple of U
+  const uint32_t ld_bytes = (uint32_t)(kElemBytes<T> * o.ld);   // logits row stride (>= row_bytes)
+  const int units_row = C / U;                               // V4 rows: C and ld are multiples of U
   auto group_rows = [&](int k) -> int {
     const int64_t r0 = (w + (int64_t)k * stride) * R;
     return k < ngroups ? (int)(N - r0 < R ? N - r0 : R) : 0;
   };
   auto group_rsrc = [&](int k) {
     const int rows = group_rows(k);
-    const char* base = static_cast<const char*>(z) + (w + (int64_t)(k < ngroups ? k : 0) * stride) * R * (int64_t)row_bytes;
-    return make_rsrc(base, (uint32_t)rows * row_bytes);
+    const char* base = static_cast<const char*>(z) + (w + (int64_t)(k < ngroups ? k : 0) * stride) * R * (int64_t)ld_bytes;
+    return make_rsrc(base, rows > 0 ? (uint32_t)(rows - 1) * ld_bytes + row_bytes : 0u);
   };
   int64_t my_y = 0;
   {
@@ -654,7 +706,7 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
     return (int64_t)(((uint64_t)(unsigned)hi << 32) | (unsigned)lo);
   };
   auto label_off = [&](int64_t y) -> uint32_t {
-    return (y >= 0 && y < C) ? (uint32_t)seg * row_bytes + (uint32_t)(y * kElemBytes<T>) : kOffNone;
+    return (y >= 0 && y < C) ? (uint32_t)seg * ld_bytes + (uint32_t)(y * kElemBytes<T>) : kOffNone;
   };
   double lsum = 0.0;   // losses of the rows whose results this lane (a segment's lane 0) wrote
   float xa[E], xb[E], bias[E];
@@ -665,7 +717,7 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int u = li + L * k;
-      load_unit<T, V4>(rs, u < units_row ? (uint32_t)(seg * (row_bytes / (U * kElemBytes<T>)) + u) : (kOffNone >> 4),
+      load_unit<T, V4>(rs, u < units_row ? (uint32_t)(seg * (ld_bytes / (U * kElemBytes<T>)) + u) : (kOffNone >> 4),
                        xx + U * k);
     }
   };
@@ -804,10 +856,12 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
     __builtin_amdgcn_wave_barrier();
     // per-row results, written by lane 0 of each segment
     if (li == 0 && seg < rows) {
-      const float loss = (float)((1.0 - (double)(yok ? zy : NAN)) + tau);
+      const double l64 = (1.0 - (double)(yok ? zy : NAN)) + tau;
+      const float loss = (float)l64;
       const int64_t r = row0 + seg;
       if (o.H) o.H[r] = Hf;
       if (o.loss) o.loss[r] = loss;
+      if (o.loss64) o.loss64[r] = l64;
       if (o.kappa) o.kappa[r] = kappa;
       lsum += (double)loss;
     }
@@ -845,55 +899,57 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
 // ------------------------------------------------------------------------------------------------
 // fwl_block_rows: one block per row, streaming with LDS candidate lists
 
+constexpr int kHistBlock = 1024;    // bins of a block's histogram (select_in_memory, W = 4)
+constexpr int kHistWave = 256;      // bins of a wavefront's histogram (W = 1)
+constexpr int kTightenSteps = 12;   // fixed-point steps per tightening of a candidate list
+
+// LDS of the block kernels.  While a row streams, each wavefront keeps its candidate list (value,
+// index) in bval/bidx; the overflow solve (select_in_memory) reuses the same bytes, first as a
+// histogram, then as one list of values.
 struct BlockShared {
-  float bval[kWavesPerBlock][kCapMax];
-  int bidx[kWavesPerBlock][kCapMax];
+  union {
+    struct {
+      float bval[kWavesPerBlock][kCapMax];
+      int bidx[kWavesPerBlock][kCapMax];
+    };
+    struct {
+      unsigned hcnt[kHistBlock];
+      double hsum[kHistBlock];
+    };
+    float blist[2 * kWavesPerBlock * kCapMax];
+  };
   float sel[kWave];
   float wmax[kWavesPerBlock];
+  float wlo[kWavesPerBlock];      // each wavefront's lower bound on tau
+  float wB[kWavesPerBlock];       // bound on the magnitude of the entries summed for wlo
   int wn[kWavesPerBlock];
   int wsel[kWavesPerBlock];
   int ovf[kWavesPerBlock];
   double red_s[kWavesPerBlock];
-  double red_c[kWavesPerBlock];
-  float red_m[kWavesPerBlock];
+  int red_c[kWavesPerBlock];
+  int ncol;
   double tau;
   int kappa;
 };
+static_assert(sizeof(unsigned) * kHistBlock + sizeof(double) * kHistBlock <= 8 * kWavesPerBlock * kCapMax,
+              "the histogram reuses the candidate lists");
 
-// Raise the wavefront's lower bound t with a few fixed-point steps on its list, then drop the
-// entries <= t (not in the support: their output stays the zero written while streaming).
-__device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, int lane) {
-  float tf = t;
-  for (int it = 0; it < 8; ++it) {
-    double s;
-    int c;
-    list_sum_count(bv, n, tf, lane, s, c);
-    if (c == 0) break;
-    // H(A) <= tau for the non-empty set A; one float lower absorbs the fp64 rounding of H(A)
-    float nt = rd32((s - 1.0) / (double)c);
-    if (isfinite(nt)) nt = prev_f32(nt);
-    if (!(nt > tf)) break;
-    tf = nt;
-  }
-  t = fmaxf(t, tf);
-  int w = 0;
-  for (int p0 = 0; p0 < n; p0 += kWave) {
-    const int p = p0 + lane;
-    const float v = p < n ? bv[p] : -INFINITY;
-    const int id = p < n ? bi[p] : -1;
-    const bool keep = v > t;
-    const uint64_t b = ballot(keep);
-    __builtin_amdgcn_wave_barrier();
-    if (keep) {
-      const int pos = w + rank_in(b);
-      bv[pos] = v;
-      bi[pos] = id;
-    }
-    w += __popcll(b);
-    __builtin_amdgcn_wave_barrier();
-  }
-  n = w;
-}
+// the same for one wavefront of fwl_wave_stream_rows
+struct WaveShared {
+  union {
+    struct {
+      float val[kCapMax];
+      int idx[kCapMax];
+    };
+    struct {
+      unsigned hcnt[kHistWave];
+      double hsum[kHistWave];
+    };
+    float list[2 * kCapMax];
+  };
+};
+static_assert(sizeof(unsigned) * kHistWave + sizeof(double) * kHistWave <= 8 * kCapMax,
+              "the histogram reuses the candidate list");
 
 // Streaming rounds.  A row is shared by W wavefronts (W = 4: one block per row; W = 1: one
 // wavefront per row).  In round `round`, access group u of a lane covers unit
@@ -946,11 +1002,83 @@ __device__ __forceinline__ void zero_round(rsrc_t out, int round, int wid, int l
   }
 }
 
-// Candidates of one round: the running maximum m gives the bound t = (m - 1 rounded down), and
-// the entries z > t are appended to the wavefront's list.  Returns false on list overflow.
+// One wavefront's state while a row (or a stretch of one) streams.
+struct StreamState {
+  int n;          // entries in the wavefront's list: every entry seen so far that is > t
+  float m;        // running maximum
+  float t;        // running lower bound on tau
+  bool ovf;       // the list could not hold the entries > t; from then on the scan only sums
+  float tov;      // the bound at the overflow: acc_s/acc_c hold the entries > tov seen since
+  double acc_s;   // (per lane)
+  int acc_c;      // (per lane)
+};
+
+__device__ __forceinline__ StreamState stream_state(bool force) {
+  StreamState st;
+  st.n = 0;
+  st.m = -INFINITY;
+  st.t = -INFINITY;
+  st.ovf = force;   // forced: no list, only the sums (the overflow solve's path for every row)
+  st.tov = NAN;     // set at the overflow (forced: at the first round)
+  st.acc_s = 0.0;
+  st.acc_c = 0;
+  return st;
+}
+
+// Raise the wavefront's lower bound t with fixed-point steps t <- H({entries > t}) over its list
+// and the round held in registers (a subset of the row, so H of it is <= tau), then drop the list
+// entries <= t (not in the support: their output stays the zero written while streaming).
+template <int S>
+__device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, const float* x, float m, int lane) {
+  const float B = fmaxf(fabsf(m), fabsf(t));
+  float tf = t;
+  for (int it = 0; it < kTightenSteps; ++it) {
+    double s;
+    int c;
+    list_sum_count(bv, n, tf, lane, s, c);
+    // the round's entries: per-lane fp32 partial sums (a bound needs no exact sum)
+    float rs = 0.0f;
+    int rc = 0;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const bool k = x[i] > tf;
+      rs += k ? x[i] : 0.0f;
+      rc += k ? 1 : 0;
+    }
+    s += wave_sum_f64((double)rs);
+    c += wave_sum_i32(rc);
+    const float nt = safe_lower32(s, c, B);
+    if (!(nt > tf)) break;
+    tf = nt;
+  }
+  t = fmaxf(t, tf);
+  int w = 0;
+  for (int p0 = 0; p0 < n; p0 += kWave) {
+    const int p = p0 + lane;
+    const float v = p < n ? bv[p] : -INFINITY;
+    const int id = p < n ? bi[p] : -1;
+    const bool keep = v > t;
+    const uint64_t b = ballot(keep);
+    __builtin_amdgcn_wave_barrier();
+    if (keep) {
+      const int pos = w + rank_in(b);
+      bv[pos] = v;
+      bi[pos] = id;
+    }
+    w += __popcll(b);
+    __builtin_amdgcn_wave_barrier();
+  }
+  n = w;
+}
+
+// Candidates of one round: the running maximum m gives the bound t (>= m - 1 rounded down), and
+// the entries z > t are appended to the wavefront's list.  A round whose entries do not fit is
+// first used to tighten t; if they still do not fit, the list is abandoned: from then on the
+// entries above the bound of that moment (tov) are only summed (their H is a lower bound on tau
+// for the overflow solve).
 template <int W, typename T, bool VEC>
-__device__ __forceinline__ bool scan_round(Round<T, VEC>& a, int round, int C, int wid, int lane, float* bv,
-                                           int* bi, int cap, int& n, float& m, float& t) {
+__device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, int wid, int lane, float* bv,
+                                           int* bi, int cap, StreamState& st) {
   constexpr int S = Round<T, VEC>::kSlots;
   constexpr int kRoundElems = kUnit<T, VEC> * kWave * W * Round<T, VEC>::kPer;
   float lm = -INFINITY;
@@ -966,47 +1094,71 @@ __device__ __forceinline__ bool scan_round(Round<T, VEC>& a, int round, int C, i
       lm = fmaxf(lm, a.x[i]);
     }
   }
-  m = fmaxf(m, wave_max_f32(lm));
-  t = fmaxf(t, bound_below_max(m));
-  if (ballot(lm > t) == 0) return true;   // no candidate in this round (the common case)
-  int cnt = 0;
+  st.m = fmaxf(st.m, wave_max_f32(lm));
+  st.t = fmaxf(st.t, bound_below_max(st.m));
+  if (!st.ovf) {
+    if (ballot(lm > st.t) == 0) return;   // no candidate in this round (the common case)
+    int cnt = 0;
 #pragma unroll
-  for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > t));
-  if (n + cnt > cap) {
-    tighten(bv, bi, n, t, lane);
-    cnt = 0;
+    for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > st.t));
+    if (st.n + cnt > cap) {
+      tighten<S>(bv, bi, st.n, st.t, a.x, st.m, lane);
+      cnt = 0;
 #pragma unroll
-    for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > t));
-    if (n + cnt > cap) return false;
+      for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > st.t));
+      if (st.n + cnt > cap) {
+        // the list cannot hold every entry above the bound: keep its sum and go on summing
+        st.ovf = true;
+        st.tov = st.t;
+        double s;
+        int c;
+        list_sum_count(bv, st.n, st.tov, lane, s, c);
+        if (lane == 0) {
+          st.acc_s += s;
+          st.acc_c += c;
+        }
+      }
+    }
+    if (!st.ovf) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        const bool p = a.x[i] > st.t;
+        const uint64_t b = ballot(p);
+        if (p) {
+          const int pos = st.n + rank_in(b);
+          bv[pos] = a.x[i];
+          bi[pos] = round_slot_index<W, T, VEC>(round, i, wid, lane);
+        }
+        st.n += __popcll(b);
+      }
+      return;
+    }
   }
+  if (isnan(st.tov)) st.tov = st.t;   // forced overflow: the first round's bound
+  // per-lane fp32 partial sum of the round (the bound derived from it allows for its rounding)
+  float rs = 0.0f;
 #pragma unroll
   for (int i = 0; i < S; ++i) {
-    const bool p = a.x[i] > t;
-    const uint64_t b = ballot(p);
-    if (p) {
-      const int pos = n + rank_in(b);
-      bv[pos] = a.x[i];
-      bi[pos] = round_slot_index<W, T, VEC>(round, i, wid, lane);
-    }
-    n += __popcll(b);
+    const bool k = a.x[i] > st.tov;
+    rs += k ? a.x[i] : 0.0f;
+    st.acc_c += k ? 1 : 0;
   }
-  return true;
+  st.acc_s += (double)rs;
 }
 
-// Stream this wavefront's share of row r once: loads run one round ahead of the candidate scan,
-// and every output element gets its zero placeholder.  Returns false if the list overflowed.
-// (`out_row`: the row's dense output -- gradient or mask -- or null in candidate-list mode; a
-// stretch of a row streams the same way, with `row`, `out_row` and C narrowed to it)
 // the first round of a row (or stretch), loaded ahead of stream_span (C = 0: no row, no traffic)
 template <int W, typename T, bool VEC>
 __device__ __forceinline__ void stream_first(const void* __restrict__ row, int C, int lane, int wid, Round<T, VEC>& a) {
   load_round<W, T, VEC>(make_rsrc(row, (uint32_t)(kElemBytes<T> * C)), 0, wid, lane, a);
 }
 
-// (`a` holds the span's first round, from stream_first)
+// Stream this wavefront's share of a row (or of a stretch of one: `row`, `out_row` and C narrowed
+// to it) once: loads run one round ahead of the candidate scan, and every dense output element
+// (gradient or mask; `out_row` null in candidate-list mode) gets its zero placeholder.  `a` holds
+// the first round, from stream_first.
 template <int W, typename T, int MODE, bool VEC>
-__device__ __forceinline__ bool stream_span(const void* __restrict__ row, void* out_row, int C, int lane, int wid, float* bv,
-                            int* bi, int cap, int& n, float& m, float& t, Round<T, VEC>& a) {
+__device__ __forceinline__ void stream_span(const void* __restrict__ row, void* out_row, int C, int lane, int wid,
+                                            float* bv, int* bi, int cap, StreamState& st, Round<T, VEC>& a) {
   constexpr int per_round = kWave * W * Round<T, VEC>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
@@ -1024,26 +1176,31 @@ __device__ __forceinline__ bool stream_span(const void* __restrict__ row, void* 
   while (true) {
     load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
-    if (!scan_round<W, T, VEC>(a, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
+    scan_round<W, T, VEC>(a, k, C, wid, lane, bv, bi, cap, st);
     if (++k >= rounds) break;
     load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
-    if (!scan_round<W, T, VEC>(b, k, C, wid, lane, bv, bi, cap, n, m, t)) return false;
+    scan_round<W, T, VEC>(b, k, C, wid, lane, bv, bi, cap, st);
     if (++k >= rounds) break;
   }
-  return true;
 }
 
-template <int W, typename T, int MODE, bool VEC>
-__device__ __forceinline__ bool stream_row(const void* __restrict__ row, int64_t r, int C, int lane, int wid, float* bv,
-                           int* bi, const Outs& o, int& n, float& m, float& t, Round<T, VEC>& a) {
-  void* out_row = nullptr;
-  if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
-  else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-  return stream_span<W, T, MODE, VEC>(row, out_row, C, lane, wid, bv, bi, o.cap, n, m, t, a);
+// The wavefront's contribution to the overflow solve's first lower bound: the sum and count of a
+// set of its entries (the accumulated entries > tov after an overflow, else its list entries > t)
+// and a bound on their magnitudes.  H of the union over wavefronts is <= tau.
+__device__ __forceinline__ void stream_lower_set(const StreamState& st, const float* bv, int lane, double& s, int& c,
+                                                 float& B) {
+  if (st.ovf) {
+    s = wave_sum_f64(st.acc_s);
+    c = wave_sum_i32(st.acc_c);
+    B = fmaxf(fabsf(st.m), fabsf(st.tov));
+  } else {
+    list_sum_count(bv, st.n, st.t, lane, s, c);
+    B = fmaxf(fabsf(st.m), fabsf(st.t));
+  }
+  if (c == 0) B = 0.0f;
 }
 
-// block-wide fp64 sum and count of the row entries > thr (fixed order)
 // The wavefronts' candidate lists of a row (or of a stretch of one) in `sh` hold every entry above
 // each wavefront's final bound; cut them at the block maximum and resolve tau and kappa into
 // sh.tau / sh.kappa (valid after the caller's next barrier).
@@ -1132,102 +1289,520 @@ __device__ __forceinline__ void block_merge_resolve(BlockShared& sh, int n, int 
   }
 }
 
-template <typename T>
-__device__ void block_sum_count(const void* __restrict__ row, int C, float thr, BlockShared& sh,
-                                int lane, int wid, double& s, int& c) {
-  double acc = 0.0;
-  int cnt = 0;
-  for (int j = threadIdx.x; j < C; j += kBlock) {
-    const float v = load_elem<T>(row, j);
-    if (v > thr) {
-      acc += (double)v;
-      ++cnt;
-    }
+// ------------------------------------------------------------------------------------------------
+// The overflow solve: tau of a row whose candidates did not fit the LDS lists, from the row in
+// memory, in a bounded number of passes, by W wavefronts (W = 1: the calling wavefront alone;
+// W = kWavesPerBlock: every thread of the block calls).
+//
+//   1. A histogram pass: count and fp64 sum of the entries in (t1, M] (t1 a lower bound on tau, M
+//      the row maximum) in bins of width w = 2^e, bin b holding t1 + b*w <= z < t1 + (b+1)*w
+//      (bins and edges exact in fp64; LDS atomics).  G(e) = sum_{z >= e} (z - e) is decreasing
+//      and G(tau) = 1, so the highest bin whose lower edge has G >= 1 holds tau.
+//   2. When that bin holds more entries than the LDS list, another histogram pass splits it by the
+//      order-preserving keys of its floats (at most 4 such passes: each divides a key range of
+//      at most 2^32 by the number of bins; a bin of one key holds equal values, none of which is
+//      in the support since tau >= the bin's edge).
+//   3. A collect pass gathers the bin's entries into the LDS list and sums every entry above the
+//      bin exactly (fixed order, fp64); the support is those entries plus the top j of the bin,
+//      with j from the sparsemax condition k z_(k) > S_k - 1 (a sort of <= 64 entries, or
+//      fixed-point steps over the list); the result is checked to lie in the bin.
+//   4. The histogram's sums are fp64 atomics, so a bin choice can be off when G is within a few
+//      ulps of 1; the check in 3 catches that, and a bisection over the keys of [t1, M] with exact
+//      fixed-order G (at most 34 passes) gives the answer then.
+// Every decision that fixes the result is taken on fixed-order fp64 sums, so the result does not
+// depend on the order of the atomics.
+
+struct SelMem {
+  unsigned* hcnt;
+  double* hsum;
+  float* list;
+  int nbins;    // bins per histogram pass: a multiple of 64
+  int cap;      // list capacity of the collect pass
+  double* red_s;
+  int* red_c;
+  int* ncol;
+};
+
+// the histogram, the list and the block scalars share LDS bytes under different types: every
+// change of role goes through this barrier (a fence keeps the compiler from moving the LDS
+// accesses across it)
+template <int W>
+__device__ __forceinline__ void sel_sync() {
+  if constexpr (W == 1) {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  } else {
+    __syncthreads();
   }
-  const double ws = wave_sum_f64(acc);
-  const double wc = wave_sum_f64((double)cnt);
-  __syncthreads();
-  if (lane == 0) {
-    sh.red_s[wid] = ws;
-    sh.red_c[wid] = wc;
-  }
-  __syncthreads();
-  s = (sh.red_s[0] + sh.red_s[1]) + (sh.red_s[2] + sh.red_s[3]);
-  c = (int)((sh.red_c[0] + sh.red_c[1]) + (sh.red_c[2] + sh.red_c[3]));
 }
 
-// Generic path: fixed-point iterations over the row in global memory, then every output is
-// (re)written.  Used when a candidate list overflows and when forced by fwl_set_params(3, .).
-template <typename T, int MODE>
-__device__ void generic_row(const void* __restrict__ row, int64_t r, int C, int yr, int lane,
-                            int wid, BlockShared& sh, const Outs& o, double& tau, int& kappa) {
-  float lm = -INFINITY;
-  for (int j = threadIdx.x; j < C; j += kBlock) lm = fmaxf(lm, load_elem<T>(row, j));
-  const float wm = wave_max_f32(lm);
-  __syncthreads();
-  if (lane == 0) sh.red_m[wid] = wm;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(sh.red_m[0], sh.red_m[1]), fmaxf(sh.red_m[2], sh.red_m[3]));
-  const float t0 = bound_below_max(M);
-  double t = (double)t0, s;
-  int c;
-  block_sum_count<T>(row, C, t0, sh, lane, wid, s, c);
-  tau = NAN;
-  kappa = 0;
-  if (c > 0) {
-    for (int it = 0; it <= C + 1; ++it) {
-      const double tn = (s - 1.0) / (double)c;
+// fp64 sum and count over the W wavefronts in a fixed order (every lane receives them)
+template <int W>
+__device__ __forceinline__ void sel_reduce(double& s, int& c, const SelMem& sm, int wid, int lane) {
+  s = wave_sum_f64(s);
+  c = wave_sum_i32(c);
+  if constexpr (W > 1) {
+    static_assert(W == kWavesPerBlock, "one wavefront or the whole block");
+    __syncthreads();
+    if (lane == 0) {
+      sm.red_s[wid] = s;
+      sm.red_c[wid] = c;
+    }
+    __syncthreads();
+    s = (sm.red_s[0] + sm.red_s[1]) + (sm.red_s[2] + sm.red_s[3]);
+    c = (sm.red_c[0] + sm.red_c[1]) + (sm.red_c[2] + sm.red_c[3]);
+    __syncthreads();
+  }
+}
+
+// One pass over a row: f(z, j) for every slot of every round (z = -inf for slots past the row;
+// all lanes call f for a slot together), W wavefronts interleaved as in the streaming rounds.  DB:
+// two rounds of loads in flight (fwl_overflow_rows); without it one round at a time, so that the
+// solve inside the streaming kernels (no workspace) holds no more registers than their stream.
+template <int W, typename T, bool VEC, bool DB, typename F>
+__device__ __forceinline__ void row_pass(const void* row, int C, int lane, int wid, F&& f) {
+  constexpr int S = Round<T, VEC>::kSlots;
+  constexpr int per_round = kWave * W * S;
+  const int rounds = (C + per_round - 1) / per_round;
+  const rsrc_t in = make_rsrc(row, (uint32_t)(kElemBytes<T> * C));
+  const rsrc_t none = make_rsrc(row, 0u);
+  auto process = [&](Round<T, VEC>& a, int k) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int j = round_slot_index<W, T, VEC>(k, i, wid, lane);
+      f(j < C ? a.x[i] : -INFINITY, j);
+    }
+  };
+  if constexpr (DB) {
+    Round<T, VEC> a, b;
+    load_round<W, T, VEC>(in, 0, wid, lane, a);
+    for (int k = 0; k < rounds; k += 2) {
+      load_round<W, T, VEC>(k + 1 < rounds ? in : none, k + 1, wid, lane, b);
+      process(a, k);
+      if (k + 1 >= rounds) break;
+      load_round<W, T, VEC>(k + 2 < rounds ? in : none, k + 2, wid, lane, a);
+      process(b, k + 1);
+    }
+  } else {
+    for (int k = 0; k < rounds; ++k) {
+      Round<T, VEC> a;
+      load_round<W, T, VEC>(in, k, wid, lane, a);
+      process(a, k);
+    }
+  }
+}
+
+// Bins of one histogram pass.  Linear: bin b holds base + b*w <= z < base + (b+1)*w for z > lo
+// (w a power of two: the edges are exact in fp64); by key: bin b holds the floats whose keys lie
+// in [kbase + (b << sh), kbase + ((b + 1) << sh)), for keys in [kbase, kmax].
+struct BinMap {
+  bool by_key;
+  double base, w, inv_w;
+  float lo;
+  int kbase, kmax, sh;
+  int nb;
+};
+
+__device__ __forceinline__ int canon_key(float z) { return fkey(z + 0.0f); }   // -0.0 -> +0.0
+
+__device__ __forceinline__ double bin_edge(const BinMap& bm, int b) {
+  if (bm.by_key) return (double)fkey_inv((int)((int64_t)bm.kbase + ((int64_t)b << bm.sh)));
+  return bm.base + (double)b * bm.w;
+}
+
+// bin of z, or -1 outside the map's range
+__device__ __forceinline__ int bin_of(const BinMap& bm, float z) {
+  if (bm.by_key) {
+    const int k = canon_key(z);
+    if (!(z == z) || k < bm.kbase || k > bm.kmax) return -1;
+    return (int)(((int64_t)k - bm.kbase) >> bm.sh);
+  }
+  if (!(z > bm.lo) || !(z < INFINITY)) return -1;
+  const double d = ((double)z - bm.base) * bm.inv_w;
+  int b = d < (double)bm.nb ? (int)d : bm.nb - 1;
+  b = b < 0 ? 0 : b;
+  // the difference may round when z and the base are far apart: place z by exact compares
+  if ((double)z < bin_edge(bm, b)) b = b > 0 ? b - 1 : 0;
+  else if (b + 1 < bm.nb && (double)z >= bin_edge(bm, b + 1)) b += 1;
+  return b;
+}
+
+// linear bins over (t1, M]: the smallest power-of-two width with nbins * w >= M - t1
+__device__ __forceinline__ BinMap linear_bins(float t1, float M, int nbins) {
+  BinMap bm;
+  bm.by_key = false;
+  bm.base = (double)t1;
+  bm.lo = t1;
+  int e = 0;
+  const double span = ((double)M - (double)t1) / (double)nbins;
+  frexp(span > 0.0 ? span : 0x1p-1074, &e);   // span < 2^e
+  bm.w = ldexp(1.0, e);
+  bm.inv_w = ldexp(1.0, -e);
+  bm.kbase = bm.kmax = bm.sh = 0;
+  bm.nb = nbins;
+  return bm;
+}
+
+// key bins over the floats in [lo, hi) (lo, hi exact fp64 values, lo < hi)
+__device__ __forceinline__ BinMap key_bins(double lo, double hi, int nbins) {
+  float f = (float)lo;
+  if ((double)f < lo) f = next_f32(f);
+  float g = (float)hi;
+  if ((double)g >= hi) g = prev_f32(g);
+  BinMap bm;
+  bm.by_key = true;
+  bm.base = bm.w = bm.inv_w = 0.0;
+  bm.lo = f;
+  bm.kbase = canon_key(f);
+  bm.kmax = canon_key(g);
+  if (bm.kmax < bm.kbase) bm.kmax = bm.kbase;
+  const int64_t range = (int64_t)bm.kmax - bm.kbase + 1;
+  int sh = 0;
+  while (((range - 1) >> sh) >= nbins) ++sh;
+  bm.sh = sh;
+  bm.nb = (int)(((range - 1) >> sh) + 1);
+  return bm;
+}
+
+// one histogram pass (counts exact, sums approximate: fp64 atomics in any order)
+template <int W, typename T, bool VEC>
+__device__ void hist_pass(const void* row, int C, const BinMap& bm, const SelMem& sm, int lane, int wid) {
+  const int t0 = W > 1 ? (int)threadIdx.x : lane;
+  for (int b = t0; b < sm.nbins; b += kWave * W) {
+    sm.hcnt[b] = 0u;
+    sm.hsum[b] = 0.0;
+  }
+  sel_sync<W>();
+  row_pass<W, T, VEC, true>(row, C, lane, wid, [&](float z, int) {
+    const int b = bin_of(bm, z);
+    if (b >= 0) {
+      __hip_atomic_fetch_add(sm.hcnt + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_fetch_add(sm.hsum + b, (double)z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  });
+  sel_sync<W>();
+}
+
+// The highest bin whose lower edge e has G(e) = S_up + sum_{bins >= b} - (C_up + count_{bins >= b}) e
+// >= 1, by one wavefront (every lane gets the results): lane l holds bins nbins-1 - (l*q + i),
+// i < q, so an inclusive scan over the lanes adds the bins from the top.  Returns the bin, its
+// count and the approximate count and sum of the entries above it.
+__device__ int find_boundary(const BinMap& bm, const SelMem& sm, int C_up, double S_up, int lane, int& cnt_b,
+                             int& c_above, double& s_above) {
+  const int q = sm.nbins / kWave;
+  int tc = 0;
+  double ts = 0.0;
+  for (int i = 0; i < q; ++i) {
+    const int b = sm.nbins - 1 - (lane * q + i);
+    tc += (int)sm.hcnt[b];
+    ts += sm.hsum[b];
+  }
+  int tot;
+  const int pc = wave_excl_scan_i32(tc, tot);   // exclusive: the lanes above this one
+  const double ps_incl = scan_f64<kWave>(ts);
+  const double ps = ps_incl - ts;
+  const double tsum = readlane_f64(ps_incl, kWave - 1);
+  int ac = C_up + pc;
+  double as = S_up + ps;
+  int found = -1, f_cnt = 0, f_ac = 0;
+  double f_as = 0.0;
+  for (int i = 0; i < q; ++i) {
+    const int b = sm.nbins - 1 - (lane * q + i);
+    const int cb = (int)sm.hcnt[b];
+    const double sb = sm.hsum[b];
+    const int a2 = ac + cb;
+    const double s2 = as + sb;
+    if (found < 0 && b < bm.nb && s2 - (double)a2 * bin_edge(bm, b) >= 1.0) {
+      found = b;
+      f_cnt = cb;
+      f_ac = ac;
+      f_as = as;
+    }
+    ac = a2;
+    as = s2;
+  }
+  const uint64_t has = ballot(found >= 0);
+  if (has == 0) {
+    // no edge with G >= 1 (only from rounding: G(t1) >= 1): the lowest bin
+    cnt_b = (int)sm.hcnt[0];
+    c_above = C_up + tot - cnt_b;
+    s_above = S_up + tsum - sm.hsum[0];
+    return 0;
+  }
+  const int src = (int)__builtin_ctzll(has);   // the lowest lane: the highest bin
+  cnt_b = __builtin_amdgcn_readlane(f_cnt, src);
+  c_above = __builtin_amdgcn_readlane(f_ac, src);
+  s_above = readlane_f64(f_as, src);
+  return __builtin_amdgcn_readlane(found, src);
+}
+
+// tau of the support {entries above the bin} U {the top j of the bin's n entries in the list},
+// given the exact count and sum above the bin (C_hi, S_hi); the bin's entries are >= lo and < hi.
+// Returns false if tau does not lie in [lo, hi) (then the bin was not the boundary).
+__device__ bool resolve_bin(const float* list, int n, int C_hi, double S_hi, double lo, double hi, int lane,
+                            double& tau, int& kappa) {
+  int j = 0;
+  double Sj = 0.0;
+  if (n <= kWave) {
+    const float c = lane < n ? list[lane] : -INFINITY;
+    int key = canon_key(lane < n ? c : -INFINITY);
+    key = sort_desc_i<kWave>(key, lane);
+    const float v = fkey_inv(key);
+    const double P = scan_f64<kWave>(lane < n ? (double)v : 0.0);
+    const uint64_t in = ballot(lane < n && (double)v * (double)(C_hi + lane + 1) > S_hi + P - 1.0);
+    j = in == 0 ? 0 : 64 - (int)__builtin_clzll(in);
+    j = uniform(j);
+    Sj = j > 0 ? readlane_f64(P, j - 1) : 0.0;
+  } else {
+    // fixed-point steps from lo (a lower bound on tau if the bin is the boundary)
+    double t = lo, s = 0.0;
+    int c = 0, it = 0;
+    list_sum_count(list, n, rd32(t), lane, s, c);
+    for (; it < n + 2; ++it) {
+      if (C_hi + c == 0) break;
+      const double tn = (S_hi + s - 1.0) / (double)(C_hi + c);
       double s2;
       int c2;
-      block_sum_count<T>(row, C, rd32(tn), sh, lane, wid, s2, c2);
+      list_sum_count(list, n, rd32(tn), lane, s2, c2);
       if (c2 == c || !(tn > t)) {
-        tau = tn;
-        kappa = c2;
+        s = s2;
+        c = c2;
         break;
       }
       t = tn;
       s = s2;
       c = c2;
     }
-    const double tc = clamp_below_max(tau, M);
-    if (tc != tau) {
-      double s3;
-      tau = tc;
-      block_sum_count<T>(row, C, rd32(tau), sh, lane, wid, s3, kappa);
-    }
+    j = c;
+    Sj = s;
   }
-  // outputs written while streaming must land before these rewrites (same block, so the same L2)
-  wait_vmem();
-  __syncthreads();
-  const float Hf = rd32(tau);
-  const float inv = (float)(o.scale / (double)kappa);
-  if constexpr (MODE == kGrad) {
-    for (int j = threadIdx.x; j < C; j += kBlock)
-      if (j != yr) store_elem<T>(o.grad, r * (int64_t)C + j, load_elem<T>(row, j) > Hf ? inv : 0.0f);
-  } else if constexpr (MODE == kMask) {
-    uint8_t* mk = o.mask + r * (int64_t)C;
-    for (int j = threadIdx.x; j < C; j += kBlock)
-      if (j != yr) mk[j] = (uint8_t)(load_elem<T>(row, j) > Hf);
+  kappa = C_hi + j;
+  if (kappa == 0) return false;
+  tau = (S_hi + Sj - 1.0) / (double)kappa;
+  return tau >= lo && tau < hi;
+}
+
+// exact fixed-order G(v) = sum_{z > v} (z - v) of the row, as (sum, count) of the entries > v
+template <int W, typename T, bool VEC, bool DB>
+__device__ void row_above(const void* row, int C, float v, const SelMem& sm, int lane, int wid, double& s, int& c) {
+  double acc = 0.0;
+  int cnt = 0;
+  row_pass<W, T, VEC, DB>(row, C, lane, wid, [&](float z, int) {
+    const bool k = z > v;
+    acc += k ? (double)z : 0.0;
+    cnt += k ? 1 : 0;
+  });
+  s = acc;
+  c = cnt;
+  sel_reduce<W>(s, c, sm, wid, lane);
+}
+
+// tau < M: only when the 1 of S - 1 was lost (|z| >= 2^53) is it clamped below the maximum, and
+// kappa counted again
+template <int W, typename T, bool VEC, bool DB>
+__device__ void clamp_row(const void* row, int C, float M, const SelMem& sm, int lane, int wid, double& tau,
+                          int& kappa) {
+  const double tc = clamp_below_max(tau, M);
+  if (tc != tau) {
+    double s;
+    int c;
+    tau = tc;
+    row_above<W, T, VEC, DB>(row, C, rd32(tau), sm, lane, wid, s, c);
+    kappa = c;
+  }
+}
+
+// Bisection over the keys of [t1, M] with exact fixed-order G at every step (at most 32 passes
+// over the row, then one for the sums): G(a) >= 1 > G(b) brackets tau in [a, b) for adjacent keys
+// a, b, so the support is {z > a}.  Needs nothing but the row; the last resort of
+// select_in_memory and the whole solve where there is no workspace to defer rows to.
+template <int W, typename T, bool VEC, bool DB>
+__device__ void select_bisect(const void* row, int C, float t1, float M, const SelMem& sm, int lane, int wid,
+                              double& tau, int& kappa) {
+  tau = NAN;
+  kappa = 0;
+  if (!isfinite(M) || !(t1 < M)) return;
+  int ka = canon_key(t1), kb = canon_key(M);
+  while ((int64_t)kb - ka > 1) {
+    const int km = (int)(((int64_t)ka + kb) >> 1);
+    const float v = fkey_inv(km);
+    double s;
+    int c;
+    row_above<W, T, VEC, DB>(row, C, v, sm, lane, wid, s, c);
+    if (s - (double)c * (double)v >= 1.0) ka = km;
+    else kb = km;
+  }
+  double s;
+  int c;
+  row_above<W, T, VEC, DB>(row, C, fkey_inv(ka), sm, lane, wid, s, c);
+  kappa = c;
+  tau = c > 0 ? (s - 1.0) / (double)c : NAN;
+  clamp_row<W, T, VEC, DB>(row, C, M, sm, lane, wid, tau, kappa);
+}
+
+template <int W, typename T, bool VEC>
+__device__ void select_in_memory(const void* row, int C, float t1, float M, const SelMem& sm, int lane, int wid,
+                                 double& tau, int& kappa) {
+  tau = NAN;
+  kappa = 0;
+  if (!isfinite(M) || !(t1 < M)) return;   // no finite maximum: no finite tau (as the list path)
+  BinMap bm = linear_bins(t1, M, sm.nbins);
+  int C_up = 0;
+  double S_up = 0.0;
+  bool done = false;
+  for (int pass = 0; pass < 6 && !done; ++pass) {
+    hist_pass<W, T, VEC>(row, C, bm, sm, lane, wid);
+    int bstar = 0, cnt_b = 0, c_above = 0;
+    double s_above = 0.0;
+    if (W == 1 || wid == 0) bstar = find_boundary(bm, sm, C_up, S_up, lane, cnt_b, c_above, s_above);
+    if constexpr (W > 1) {
+      if (threadIdx.x == 0) {
+        sm.red_c[0] = bstar;
+        sm.red_c[1] = cnt_b;
+        sm.red_c[2] = c_above;
+        sm.red_s[0] = s_above;
+      }
+      __syncthreads();
+      bstar = sm.red_c[0];
+      cnt_b = sm.red_c[1];
+      c_above = sm.red_c[2];
+      s_above = sm.red_s[0];
+      __syncthreads();
+    }
+    const double lo = bin_edge(bm, bstar);
+    const double hi = bstar + 1 < bm.nb ? bin_edge(bm, bstar + 1)
+                                        : (bm.by_key ? (double)next_f32(fkey_inv(bm.kmax)) : bm.base + bm.nb * bm.w);
+    sel_sync<W>();
+    const bool single = bm.by_key && bm.sh == 0;   // one key per bin: equal values, none in the support
+    if (cnt_b > sm.cap && !single && pass < 5) {
+      bm = key_bins(lo, hi, sm.nbins);
+      C_up = c_above;
+      S_up = s_above;
+      continue;
+    }
+    // collect pass: the bin's entries into the list, exact count and sum above the bin
+    if constexpr (W > 1) {
+      if (threadIdx.x == 0) *sm.ncol = 0;
+      __syncthreads();
+    }
+    int ncol = 0;
+    bool lost = false;
+    double acc = 0.0;
+    int cnt = 0;
+    row_pass<W, T, VEC, true>(row, C, lane, wid, [&](float z, int) {
+      const double zd = (double)z;
+      const bool above = zd >= hi;
+      acc += above ? zd : 0.0;
+      cnt += above ? 1 : 0;
+      const bool in = !single && zd >= lo && zd < hi;
+      const uint64_t bl = ballot(in);
+      if (bl != 0) {
+        const int k = __popcll(bl);
+        int base;
+        if constexpr (W > 1) {
+          int b0 = 0;
+          if (lane == 0) b0 = atomicAdd(sm.ncol, k);
+          base = __builtin_amdgcn_readfirstlane(b0);
+        } else {
+          base = ncol;
+          ncol += k;
+        }
+        const int pos = base + rank_in(bl);
+        if (in && pos < sm.cap) sm.list[pos] = z;
+        if (base + k > sm.cap) lost = true;
+      }
+    });
+    double S_hi = acc;
+    int C_hi = cnt;
+    sel_reduce<W>(S_hi, C_hi, sm, wid, lane);
+    if constexpr (W > 1) {
+      ncol = *sm.ncol;
+      const int lost_any = __syncthreads_or(lost ? 1 : 0);
+      lost = lost_any != 0;
+    }
+    sel_sync<W>();
+    if (!lost) {
+      bool ok = false;
+      double tt = NAN;
+      int kk = 0;
+      if (W == 1 || wid == 0) ok = resolve_bin(sm.list, ncol, C_hi, S_hi, lo, hi, lane, tt, kk);
+      if constexpr (W > 1) {
+        if (threadIdx.x == 0) {
+          sm.red_c[0] = ok ? 1 : 0;
+          sm.red_c[1] = kk;
+          sm.red_s[0] = tt;
+        }
+        __syncthreads();
+        ok = sm.red_c[0] != 0;
+        kk = sm.red_c[1];
+        tt = sm.red_s[0];
+        __syncthreads();
+      }
+      if (ok) {
+        tau = tt;
+        kappa = kk;
+        done = true;
+      }
+    }
+    break;
+  }
+  if (!done) select_bisect<W, T, VEC, true>(row, C, t1, M, sm, lane, wid, tau, kappa);
+  else clamp_row<W, T, VEC, true>(row, C, M, sm, lane, wid, tau, kappa);
+}
+
+// The support of a row solved in memory, written from the row: the gradient (inv) or mask (1) at
+// every entry > Hf but the label (the placeholders hold 0 everywhere else), or the candidate list
+// (at most o.ccap entries, in pass order).
+template <int W, typename T, int MODE, bool VEC, bool DB>
+__device__ void write_support(const void* row, int64_t r, int C, int yr, float Hf, float inv, const Outs& o,
+                              int* wsel, int lane, int wid) {
+  if constexpr (MODE == kGrad || MODE == kMask) {
+    row_pass<W, T, VEC, DB>(row, C, lane, wid, [&](float z, int j) {
+      if (z > Hf && j != yr) {
+        if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + j, inv);
+        else o.mask[r * (int64_t)C + j] = 1;
+      }
+    });
   } else {
+    // candidate lists in a deterministic order: per round, the wavefronts in order, then their slots
+    constexpr int S = Round<T, VEC>::kSlots;
+    constexpr int per_round = kWave * W * S;
+    const int rounds = (C + per_round - 1) / per_round;
+    const rsrc_t in = make_rsrc(row, (uint32_t)(kElemBytes<T> * C));
     float* cv = o.cval + r * (int64_t)o.cstride;
     int32_t* ci = o.cidx + r * (int64_t)o.cstride;
     int base = 0;
-    for (int j0 = 0; j0 < C; j0 += kBlock) {
-      const int j = j0 + (int)threadIdx.x;
-      const float v = j < C ? load_elem<T>(row, j) : -INFINITY;
-      const bool p = v > Hf;
-      const uint64_t b = ballot(p);
-      __syncthreads();
-      if (lane == 0) sh.wsel[wid] = __popcll(b);
-      __syncthreads();
-      int off = base;
-      for (int w = 0; w < wid; ++w) off += sh.wsel[w];
-      if (p && off + rank_in(b) < o.ccap) {
-        const int pos = off + rank_in(b);
-        cv[pos] = v;
-        ci[pos] = j;
+    for (int k = 0; k < rounds; ++k) {
+      Round<T, VEC> a;
+      load_round<W, T, VEC>(in, k, wid, lane, a);
+      int mine = 0;
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        const int j = round_slot_index<W, T, VEC>(k, i, wid, lane);
+        mine += __popcll(ballot(j < C && a.x[i] > Hf));
       }
-      base += (sh.wsel[0] + sh.wsel[1]) + (sh.wsel[2] + sh.wsel[3]);
+      int off = base;
+      if constexpr (W > 1) {
+        __syncthreads();
+        if (lane == 0) wsel[wid] = mine;
+        __syncthreads();
+        for (int w = 0; w < wid; ++w) off += wsel[w];
+        base += (wsel[0] + wsel[1]) + (wsel[2] + wsel[3]);
+      } else {
+        base += mine;
+      }
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        const int j = round_slot_index<W, T, VEC>(k, i, wid, lane);
+        const bool sel = j < C && a.x[i] > Hf;
+        const uint64_t b = ballot(sel);
+        const int pos = off + rank_in(b);
+        if (sel && pos < o.ccap) {
+          cv[pos] = a.x[i];
+          ci[pos] = j;
+        }
+        off += __popcll(b);
+      }
     }
   }
 }
@@ -1240,11 +1815,12 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
   double bsum = 0.0;
-  auto row_at = [&](int64_t rr) { return static_cast<const char*>(z) + rr * (int64_t)C * kElemBytes<T>; };
+  auto row_at = [&](int64_t rr) { return static_cast<const char*>(z) + rr * o.ld * kElemBytes<T>; };
   // the first round of the next row is loaded before this row is resolved, so that the stream of
   // every row after the first starts with its loads in flight
   Round<T, V4> first;
-  if (blockIdx.x < N) stream_first<kWavesPerBlock, T, V4>(row_at(blockIdx.x), o.force_generic ? 0 : C, lane, wid, first);
+  if (blockIdx.x < N) stream_first<kWavesPerBlock, T, V4>(row_at(blockIdx.x), C, lane, wid, first);
+  const SelMem sm = {nullptr, nullptr, nullptr, 0, 0, sh.red_s, sh.red_c, nullptr};
   for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
     const void* row = row_at(r);
     const int64_t y64 = tgt[r];
@@ -1253,28 +1829,30 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
     float* bv = sh.bval[wid];
     int* bi = sh.bidx[wid];
 
-    int n = 0;
-    float m = -INFINITY, t = -INFINITY;
-    bool ok = !o.force_generic;
-    if (ok) ok = stream_row<kWavesPerBlock, T, MODE, V4>(row, r, C, lane, wid, bv, bi, o, n, m, t, first);
+    StreamState st = stream_state(o.force_generic != 0);
+    void* out_row = nullptr;
+    if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
+    else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
+    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, o.cap, st, first);
     if (lane == 0) {
-      sh.wmax[wid] = m;
-      sh.wn[wid] = n;
-      sh.ovf[wid] = !ok;
+      sh.wmax[wid] = st.m;
+      sh.wn[wid] = st.n;
+      sh.ovf[wid] = st.ovf;
     }
     const int64_t rn = r + gridDim.x;
     if constexpr (MODE == kGrad || MODE == kMask) {
       // every wavefront's zero placeholders have landed before any support entry is rewritten
       wait_vmem();
     }
-    if (rn < N && !o.force_generic) stream_first<kWavesPerBlock, T, V4>(row_at(rn), C, lane, wid, first);
+    if (rn < N) stream_first<kWavesPerBlock, T, V4>(row_at(rn), C, lane, wid, first);
     __syncthreads();
     const bool overflow = sh.ovf[0] | sh.ovf[1] | sh.ovf[2] | sh.ovf[3];
 
     double tau = NAN;
     int kappa = 0;
+    bool deferred = false;
     if (!overflow) {
-      block_merge_resolve(sh, n, wid, lane);
+      block_merge_resolve(sh, st.n, wid, lane);
       __syncthreads();
       tau = sh.tau;
       kappa = sh.kappa;
@@ -1282,7 +1860,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
       const float inv = (float)(o.scale / (double)kappa);
       if constexpr (MODE == kGrad || MODE == kMask) {
         // the zero placeholders stand for every other entry
-        for (int p = lane; p < n; p += kWave) {
+        for (int p = lane; p < st.n; p += kWave) {
           const int id = bi[p];
           if (id == yr || !(bv[p] > Hf)) continue;
           if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + id, inv);
@@ -1290,9 +1868,9 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
         }
       } else {
         int ns = 0;
-        for (int p0 = 0; p0 < n; p0 += kWave) {
+        for (int p0 = 0; p0 < st.n; p0 += kWave) {
           const int p = p0 + lane;
-          ns += __popcll(ballot(p < n && bv[p] > Hf));
+          ns += __popcll(ballot(p < st.n && bv[p] > Hf));
         }
         __syncthreads();
         if (lane == 0) sh.wsel[wid] = ns;
@@ -1301,9 +1879,9 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
         for (int w = 0; w < wid; ++w) off += sh.wsel[w];
         float* cv = o.cval + r * (int64_t)o.cstride;
         int32_t* ci = o.cidx + r * (int64_t)o.cstride;
-        for (int p0 = 0; p0 < n; p0 += kWave) {
+        for (int p0 = 0; p0 < st.n; p0 += kWave) {
           const int p = p0 + lane;
-          const float v = p < n ? bv[p] : -INFINITY;
+          const float v = p < st.n ? bv[p] : -INFINITY;
           const bool k = v > Hf;
           const uint64_t b = ballot(k);
           if (k && off + rank_in(b) < o.ccap) {
@@ -1315,10 +1893,43 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
         }
       }
     } else {
-      generic_row<T, MODE>(row, r, C, yr, lane, wid, sh, o, tau, kappa);
+      // the overflow solve, from the best lower bound the stream left: every wavefront's bound and
+      // H of the union of the sets they summed
+      double ls;
+      int lc;
+      float lB;
+      stream_lower_set(st, bv, lane, ls, lc, lB);
+      if (lane == 0) {
+        sh.wlo[wid] = st.t;
+        sh.wB[wid] = lB;
+        sh.red_s[wid] = ls;
+        sh.red_c[wid] = lc;
+      }
+      __syncthreads();
+      const float M = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
+      const double S = (sh.red_s[0] + sh.red_s[1]) + (sh.red_s[2] + sh.red_s[3]);
+      const int Cn = (sh.red_c[0] + sh.red_c[1]) + (sh.red_c[2] + sh.red_c[3]);
+      const float B = fmaxf(fmaxf(sh.wB[0], sh.wB[1]), fmaxf(sh.wB[2], sh.wB[3]));
+      float t1 = fmaxf(fmaxf(fmaxf(sh.wlo[0], sh.wlo[1]), fmaxf(sh.wlo[2], sh.wlo[3])), bound_below_max(M));
+      t1 = fmaxf(t1, safe_lower32(S, Cn, B));
+      __syncthreads();
+      if (o.ovf_lo != nullptr) {
+        // fwl_overflow_rows solves the row and writes its outputs
+        deferred = true;
+        if (threadIdx.x == 0) {
+          o.ovf_lo[r] = t1;
+          o.ovf_mx[r] = M;
+        }
+      } else {
+        select_bisect<kWavesPerBlock, T, V4, false>(row, C, t1, M, sm, lane, wid, tau, kappa);
+        __syncthreads();
+        write_support<kWavesPerBlock, T, MODE, V4, false>(row, r, C, yr, rd32(tau), (float)(o.scale / (double)kappa), o,
+                                                          sh.wsel, lane, wid);
+      }
     }
+    if (threadIdx.x == 0 && !overflow && o.ovf_lo != nullptr) o.ovf_lo[r] = NAN;
 
-    if (threadIdx.x == 0) {
+    if (threadIdx.x == 0 && !deferred) {
       const float Hf = rd32(tau);
       const float inv = (float)(o.scale / (double)kappa);
       const float zy = yok ? load_elem<T>(row, yr) : NAN;
@@ -1326,9 +1937,11 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
         if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + yr, (zy > Hf ? inv : 0.0f) - o.scale_f);
         else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
       }
-      const float loss = (float)((1.0 - (double)zy) + tau);
+      const double l64 = (1.0 - (double)zy) + tau;
+      const float loss = (float)l64;
       if (o.H) o.H[r] = Hf;
       if (o.loss) o.loss[r] = loss;
+      if (o.loss64) o.loss64[r] = l64;
       if (o.kappa) o.kappa[r] = kappa;
       if constexpr (MODE == kCand) o.ccnt[r] = kappa;
       bsum += (double)loss;
@@ -1343,82 +1956,32 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
 // one round ahead, zero placeholders for every output), its candidates kept in the wavefront's
 // LDS list, which is then cut at the final bound max - 1 and resolved like a register row; only
 // the support entries and the label are rewritten.  No block-wide barrier: each wavefront runs
-// its own rows, as in fwl_wave_rows.
-
-// fp64 sum and count of the row entries > thr, over the wavefront (fixed order)
-template <typename T>
-__device__ void wave_row_sum_count(const void* __restrict__ row, int C, float thr, int lane, double& s, int& c) {
-  double acc = 0.0;
-  int cnt = 0;
-  for (int j = lane; j < C; j += kWave) {
-    const float v = load_elem<T>(row, j);
-    if (v > thr) {
-      acc += (double)v;
-      ++cnt;
-    }
-  }
-  s = wave_sum_f64(acc);
-  c = (int)wave_sum_f64((double)cnt);
-}
-
-// generic solve of one row by one wavefront: fixed-point iterations over the row in memory
-template <typename T>
-__device__ void wave_generic_solve(const void* __restrict__ row, int C, int lane, float& m, double& tau,
-                                   int& kappa) {
-  float lm = -INFINITY;
-  for (int j = lane; j < C; j += kWave) lm = fmaxf(lm, load_elem<T>(row, j));
-  m = wave_max_f32(lm);
-  const float t0 = bound_below_max(m);
-  double t = (double)t0, s;
-  int c;
-  wave_row_sum_count<T>(row, C, t0, lane, s, c);
-  tau = NAN;
-  kappa = 0;
-  if (c == 0) return;
-  for (int it = 0; it <= C + 1; ++it) {
-    const double tn = (s - 1.0) / (double)c;
-    double s2;
-    int c2;
-    wave_row_sum_count<T>(row, C, rd32(tn), lane, s2, c2);
-    if (c2 == c || !(tn > t)) {
-      tau = tn;
-      kappa = c2;
-      break;
-    }
-    t = tn;
-    s = s2;
-    c = c2;
-  }
-  const double tc = clamp_below_max(tau, m);
-  if (tc != tau) {
-    double s3;
-    tau = tc;
-    wave_row_sum_count<T>(row, C, rd32(tau), lane, s3, kappa);
-  }
-}
-
+// its own rows, as in fwl_wave_rows.  A row whose list overflows is solved in memory by its
+// wavefront (select_in_memory with W = 1).
 template <typename T, int MODE, bool V4>
 __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __restrict__ z,
                                                                const int64_t* __restrict__ tgt, int64_t N,
                                                                int C, Outs o) {
-  __shared__ float s_val[kWavesPerBlock][kCapMax];
-  __shared__ int s_idx[kWavesPerBlock][kCapMax];
+  __shared__ WaveShared s_w[kWavesPerBlock];
   __shared__ double s_wsum[kWavesPerBlock];
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
   const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;   // this wavefront's rows: w + k*stride
   const int nrows = w < N ? (int)((N - 1 - w) / stride + 1) : 0;   // <= kRowsPerWave (host grid)
-  float* bv = s_val[wid];
-  int* bi = s_idx[wid];
+  float* bv = s_w[wid].val;
+  int* bi = s_w[wid].idx;
+  const SelMem sm = {nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr};
   const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
   float my_H = 0.0f, my_loss = 0.0f;
+  double my_l64 = 0.0;
   int my_kappa = 0;
+  bool my_def = false;   // this lane's row was deferred to fwl_overflow_rows
   double lsum = 0.0;
-  auto row_at = [&](int k) { return static_cast<const char*>(z) + (w + (int64_t)k * stride) * C * kElemBytes<T>; };
+  auto row_at = [&](int k) { return static_cast<const char*>(z) + (w + (int64_t)k * stride) * o.ld * kElemBytes<T>; };
   // the next row's first round is loaded before this row is resolved (see fwl_block_rows)
   Round<T, V4> first;
-  if (nrows > 0) stream_first<1, T, V4>(row_at(0), o.force_generic ? 0 : C, lane, 0, first);
+  if (nrows > 0) stream_first<1, T, V4>(row_at(0), C, lane, 0, first);
   for (int k = 0; k < nrows; ++k) {
     const int64_t r = w + (int64_t)k * stride;
     const void* row = row_at(k);
@@ -1427,21 +1990,23 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     const bool yok = y64 >= 0 && y64 < C;
     const int yr = yok ? (int)y64 : -1;
 
-    int n = 0;
-    float m = -INFINITY, t = -INFINITY;
-    const bool ok = !o.force_generic && stream_row<1, T, MODE, V4>(row, r, C, lane, 0, bv, bi, o, n, m, t, first);
-    if (k + 1 < nrows && !o.force_generic) stream_first<1, T, V4>(row_at(k + 1), C, lane, 0, first);
+    StreamState st = stream_state(o.force_generic != 0);
+    void* out_row = nullptr;
+    if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
+    else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
+    stream_span<1, T, MODE, V4>(row, out_row, C, lane, 0, bv, bi, o.cap, st, first);
+    if (k + 1 < nrows) stream_first<1, T, V4>(row_at(k + 1), C, lane, 0, first);
     double tau;
     int kappa;
     uint64_t support = 0;
-    if (ok) {
+    if (!st.ovf) {
       // keep the entries above the final bound (every support entry is among them)
-      const float tb = bound_below_max(m);
+      const float tb = bound_below_max(st.m);
       int kept = 0;
-      for (int p0 = 0; p0 < n; p0 += kWave) {
+      for (int p0 = 0; p0 < st.n; p0 += kWave) {
         const int p = p0 + lane;
-        const float v = p < n ? bv[p] : -INFINITY;
-        const int id = p < n ? bi[p] : -1;
+        const float v = p < st.n ? bv[p] : -INFINITY;
+        const int id = p < st.n ? bi[p] : -1;
         const bool keep = v > tb;
         const uint64_t b = ballot(keep);
         __builtin_amdgcn_wave_barrier();
@@ -1452,18 +2017,34 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
         kept += __popcll(b);
         __builtin_amdgcn_wave_barrier();
       }
-      n = kept;
-      resolve_list(bv, n, tb, m, lane, tau, kappa, support);
+      st.n = kept;
+      resolve_list(bv, st.n, tb, st.m, lane, tau, kappa, support);
     } else {
-      wave_generic_solve<T>(row, C, lane, m, tau, kappa);
+      double ls;
+      int lc;
+      float lB;
+      stream_lower_set(st, bv, lane, ls, lc, lB);
+      const float t1 = fmaxf(fmaxf(st.t, bound_below_max(st.m)), safe_lower32(ls, lc, lB));
+      if (o.ovf_lo != nullptr) {
+        // fwl_overflow_rows solves the row and writes its outputs
+        if (lane == 0) {
+          o.ovf_lo[r] = t1;
+          o.ovf_mx[r] = st.m;
+        }
+        if (lane == k) my_def = true;
+        __builtin_amdgcn_wave_barrier();
+        continue;
+      }
+      select_bisect<1, T, V4, false>(row, C, t1, st.m, sm, lane, 0, tau, kappa);
     }
+    if (lane == 0 && !st.ovf && o.ovf_lo != nullptr) o.ovf_lo[r] = NAN;
     const float Hf = rd32(tau);
     const float inv = (float)(o.scale / (double)kappa);
     // this wavefront's zero placeholders have landed before any entry is rewritten
     wait_vmem();
-    if (ok) {
+    if (!st.ovf) {
       if constexpr (MODE == kGrad || MODE == kMask) {
-        for (int p = lane; p < n; p += kWave) {
+        for (int p = lane; p < st.n; p += kWave) {
           const int id = bi[p];
           if (id == yr || !(bv[p] > Hf)) continue;
           if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + id, inv);
@@ -1471,9 +2052,9 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
         }
       } else {
         int out = 0;
-        for (int p0 = 0; p0 < n; p0 += kWave) {
+        for (int p0 = 0; p0 < st.n; p0 += kWave) {
           const int p = p0 + lane;
-          const float v = p < n ? bv[p] : -INFINITY;
+          const float v = p < st.n ? bv[p] : -INFINITY;
           const bool sel = v > Hf;
           const uint64_t b = ballot(sel);
           if (sel && out + rank_in(b) < o.ccap) {
@@ -1484,51 +2065,89 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
         }
       }
     } else {
-      if constexpr (MODE == kGrad) {
-        for (int j = lane; j < C; j += kWave)
-          if (j != yr) store_elem<T>(o.grad, r * (int64_t)C + j, load_elem<T>(row, j) > Hf ? inv : 0.0f);
-      } else if constexpr (MODE == kMask) {
-        for (int j = lane; j < C; j += kWave)
-          if (j != yr) o.mask[r * (int64_t)C + j] = (uint8_t)(load_elem<T>(row, j) > Hf);
-      } else {
-        int out = 0;
-        for (int j0 = 0; j0 < C; j0 += kWave) {
-          const int j = j0 + lane;
-          const float v = j < C ? load_elem<T>(row, j) : -INFINITY;
-          const bool sel = v > Hf;
-          const uint64_t b = ballot(sel);
-          if (sel && out + rank_in(b) < o.ccap) {
-            o.cval[r * (int64_t)o.cstride + out + rank_in(b)] = v;
-            o.cidx[r * (int64_t)o.cstride + out + rank_in(b)] = j;
-          }
-          out += __popcll(b);
-        }
-      }
+      write_support<1, T, MODE, V4, false>(row, r, C, yr, Hf, inv, o, nullptr, lane, 0);
     }
     const float zy = yok ? load_elem<T>(row, yr) : NAN;
     if (lane == 0 && yok) {
       if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + yr, (zy > Hf ? inv : 0.0f) - o.scale_f);
       else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
     }
-    const float loss = (float)((1.0 - (double)zy) + tau);
+    const double l64 = (1.0 - (double)zy) + tau;
+    const float loss = (float)l64;
     lsum += (double)loss;
     if (lane == k) {
       my_H = Hf;
       my_loss = loss;
+      my_l64 = l64;
       my_kappa = kappa;
     }
     __builtin_amdgcn_wave_barrier();
   }
-  if (lane < nrows) {
+  if (lane < nrows && !my_def) {
     const int64_t r = w + (int64_t)lane * stride;
     if (o.H) o.H[r] = my_H;
     if (o.loss) o.loss[r] = my_loss;
+    if (o.loss64) o.loss64[r] = my_l64;
     if (o.kappa) o.kappa[r] = my_kappa;
     if constexpr (MODE == kCand) o.ccnt[r] = my_kappa;
   }
   if (lane == 0) s_wsum[wid] = lsum;
   __syncthreads();
   const double bsum = (s_wsum[0] + s_wsum[1]) + (s_wsum[2] + s_wsum[3]);
+  mean_epilogue(bsum, o);
+}
+
+// ------------------------------------------------------------------------------------------------
+// fwl_overflow_rows: the rows whose candidate lists overflowed in fwl_block_rows or
+// fwl_wave_stream_rows (ovf_lo[r] not NaN), one block per row, each solved in memory by
+// select_in_memory from the lower bound and maximum the stream left.  The stream wrote the row's
+// zero placeholders; this kernel writes its support, its label element, H, loss, kappa and its
+// share of the mean (the block partials after those of the streaming kernel).  Launched after
+// every streaming launch (it returns at once for rows without overflow).
+template <typename T, int MODE, bool V4>
+__global__ __launch_bounds__(kBlock) void fwl_overflow_rows(const void* __restrict__ z,
+                                                            const int64_t* __restrict__ tgt, int64_t N, int C,
+                                                            Outs o) {
+  __shared__ BlockShared sh;
+  const int lane = lane_id();
+  const int wid = uniform((int)(threadIdx.x >> 6));
+  const SelMem sm = {sh.hcnt, sh.hsum, sh.blist, kHistBlock, o.cap * 2 * kWavesPerBlock, sh.red_s, sh.red_c, &sh.ncol};
+  double bsum = 0.0;
+  for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
+    const float lo = o.ovf_lo[r];
+    if (!(lo == lo)) continue;   // solved by the streaming kernel
+    const float M = o.ovf_mx[r];
+    const void* row = static_cast<const char*>(z) + r * o.ld * kElemBytes<T>;
+    const int64_t y64 = tgt[r];
+    const bool yok = y64 >= 0 && y64 < C;
+    const int yr = yok ? (int)y64 : -1;
+    double tau;
+    int kappa;
+    select_in_memory<kWavesPerBlock, T, V4>(row, C, lo, M, sm, lane, wid, tau, kappa);
+    __syncthreads();
+    const float Hf = rd32(tau);
+    const float inv = (float)(o.scale / (double)kappa);
+    // candidate lists cut at ccap (the two-pass op's read pass) leave rows with a longer support
+    // to fwl_scatter_support, which writes them from the logits
+    if (MODE != kCand || kappa <= o.ccap)
+      write_support<kWavesPerBlock, T, MODE, V4, true>(row, r, C, yr, Hf, inv, o, sh.wsel, lane, wid);
+    if (threadIdx.x == 0) {
+      const float zy = yok ? load_elem<T>(row, yr) : NAN;
+      if (yok) {
+        if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + yr, (zy > Hf ? inv : 0.0f) - o.scale_f);
+        else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
+      }
+      const double l64 = (1.0 - (double)zy) + tau;
+      const float loss = (float)l64;
+      if (o.H) o.H[r] = Hf;
+      if (o.loss) o.loss[r] = loss;
+      if (o.loss64) o.loss64[r] = l64;
+      if (o.kappa) o.kappa[r] = kappa;
+      if constexpr (MODE == kCand) o.ccnt[r] = kappa;
+      bsum += (double)loss;
+    }
+    __syncthreads();
+  }
   mean_epilogue(bsum, o);
 }
 
@@ -1552,8 +2171,9 @@ constexpr int kSplitMaxChunks = 256;
 constexpr int kSplitListCap = 2048;     // entries of a row's list in the finishing kernel
 
 struct SplitScratch {
-  int* count;     // [N * nch]: support size of the chunk, -1 = the row needs the generic solve
-  double* tau;    // [N * nch]: tau_c
+  int* count;     // [N * nch]: support size of the chunk, -1 = the row needs the overflow solve
+  double* tau;    // [N * nch]: tau_c, or a lower bound on tau where count = -1
+  float* mx;      // [N * nch]: the chunk's maximum
   float* val;     // [N * nch * kSplitCap]
   int* idx;       // [N * nch * kSplitCap] (index within the row)
 };
@@ -1571,40 +2191,40 @@ __global__ __launch_bounds__(kBlock) void fwl_split_chunks(const void* __restric
     const int c = (int)(it - r * nch);
     const int c0 = c * CH;
     const int len = C - c0 < CH ? C - c0 : CH;
-    const void* span = static_cast<const char*>(z) + (r * (int64_t)C + c0) * kElemBytes<T>;
+    const void* span = static_cast<const char*>(z) + (r * o.ld + c0) * kElemBytes<T>;
     void* out_span = nullptr;
     if constexpr (MODE == kGrad) out_span = static_cast<char*>(o.grad) + (r * (int64_t)C + c0) * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_span = o.mask + r * (int64_t)C + c0;
     float* bv = sh.bval[wid];
     int* bi = sh.bidx[wid];
-    int n = 0;
-    float m = -INFINITY, t = -INFINITY;
+    StreamState st = stream_state(o.force_generic != 0);
     Round<T, V4> first;
-    if (!o.force_generic) stream_first<kWavesPerBlock, T, V4>(span, len, lane, wid, first);
-    const bool ok = !o.force_generic &&
-                    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, n, m, t, first);
+    stream_first<kWavesPerBlock, T, V4>(span, len, lane, wid, first);
+    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, st, first);
     if (lane == 0) {
-      sh.wmax[wid] = m;
-      sh.wn[wid] = n;
-      sh.ovf[wid] = !ok;
+      sh.wmax[wid] = st.m;
+      sh.wn[wid] = st.n;
+      sh.ovf[wid] = st.ovf;
     }
     __syncthreads();
     const bool overflow = sh.ovf[0] | sh.ovf[1] | sh.ovf[2] | sh.ovf[3];
-    if (!overflow) {
-      block_merge_resolve(sh, n, wid, lane);
-      __syncthreads();
-    }
-    // the chunk's support, {list entries > rd32(tau_c)}, or -1: the row needs the generic solve
-    // (lists overflowed; a support too large to keep; a +inf maximum, whose row has no finite tau)
     const float Mc = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
+    // the chunk's support, {list entries > rd32(tau_c)}, or -1: the row needs the overflow solve
+    // (lists overflowed; a support too large to keep; a +inf maximum, whose row has no finite
+    // tau).  tau_c (or, after an overflow, H of the entries the stream summed, a lower bound) is
+    // kept either way: the largest over the chunks is where the row's solve starts.
     int status = -1;
+    double lower = -INFINITY;
     if (!overflow) {
+      block_merge_resolve(sh, st.n, wid, lane);
+      __syncthreads();
       if (sh.kappa == 0) {
         status = Mc == -INFINITY ? 0 : -1;   // 0: no finite entry in the chunk
       } else if (isfinite(sh.tau)) {
+        lower = sh.tau;
         const float Hc = rd32(sh.tau);
         int cnt = 0;
-        for (int p0 = 0; p0 < n; p0 += kWave) cnt += __popcll(ballot(p0 + lane < n && bv[p0 + lane] > Hc));
+        for (int p0 = 0; p0 < st.n; p0 += kWave) cnt += __popcll(ballot(p0 + lane < st.n && bv[p0 + lane] > Hc));
         if (lane == 0) s_base[wid] = cnt;
         __syncthreads();
         const int total = (s_base[0] + s_base[1]) + (s_base[2] + s_base[3]);
@@ -1613,9 +2233,9 @@ __global__ __launch_bounds__(kBlock) void fwl_split_chunks(const void* __restric
           int off = 0;
           for (int w = 0; w < wid; ++w) off += s_base[w];
           const int64_t slot = it * kSplitCap;
-          for (int p0 = 0; p0 < n; p0 += kWave) {
+          for (int p0 = 0; p0 < st.n; p0 += kWave) {
             const int p = p0 + lane;
-            const bool sel = p < n && bv[p] > Hc;
+            const bool sel = p < st.n && bv[p] > Hc;
             const uint64_t b = ballot(sel);
             if (sel) {
               sc.val[slot + off + rank_in(b)] = bv[p];
@@ -1625,10 +2245,27 @@ __global__ __launch_bounds__(kBlock) void fwl_split_chunks(const void* __restric
           }
         }
       }
+    } else {
+      double ls;
+      int lc;
+      float lB;
+      stream_lower_set(st, bv, lane, ls, lc, lB);
+      if (lane == 0) {
+        sh.wlo[wid] = st.t;
+        sh.wB[wid] = lB;
+        sh.red_s[wid] = ls;
+        sh.red_c[wid] = lc;
+      }
+      __syncthreads();
+      const double S = (sh.red_s[0] + sh.red_s[1]) + (sh.red_s[2] + sh.red_s[3]);
+      const int Cn = (sh.red_c[0] + sh.red_c[1]) + (sh.red_c[2] + sh.red_c[3]);
+      const float B = fmaxf(fmaxf(sh.wB[0], sh.wB[1]), fmaxf(sh.wB[2], sh.wB[3]));
+      lower = fmaxf(fmaxf(fmaxf(sh.wlo[0], sh.wlo[1]), fmaxf(sh.wlo[2], sh.wlo[3])), safe_lower32(S, Cn, B));
     }
     if (threadIdx.x == 0) {
       sc.count[it] = status;
-      sc.tau[it] = status > 0 ? sh.tau : -INFINITY;
+      sc.tau[it] = status > 0 || status < 0 ? lower : -INFINITY;
+      sc.mx[it] = Mc;
     }
     __syncthreads();
   }
@@ -1644,6 +2281,7 @@ __global__ __launch_bounds__(kBlock) void fwl_split_finish(const void* __restric
   constexpr int B = 8;   // support entries loaded per batch
   __shared__ BlockShared sh;
   __shared__ double s_lo[kWavesPerBlock];
+  __shared__ float s_mx[kWavesPerBlock];
   __shared__ int s_w[kWavesPerBlock];
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
@@ -1651,24 +2289,29 @@ __global__ __launch_bounds__(kBlock) void fwl_split_finish(const void* __restric
   float* cl = &sh.bval[0][0];
   int* cx = &sh.bidx[0][0];
   double lsum = 0.0;
+  const SelMem sm = {sh.hcnt, sh.hsum, sh.blist, kHistBlock, o.cap * 2 * kWavesPerBlock, sh.red_s, sh.red_c, &sh.ncol};
   for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
-    const void* row = static_cast<const char*>(z) + r * (int64_t)C * kElemBytes<T>;
+    const void* row = static_cast<const char*>(z) + r * o.ld * kElemBytes<T>;
     const int64_t y64 = tgt[r];
     // the chunks' lower bounds, and whether any chunk gave up
     const int64_t item = r * nch + t;
     const int cnt = t < nch ? sc.count[item] : 0;
     const double tc = t < nch ? sc.tau[item] : -INFINITY;
+    const float mc = t < nch ? sc.mx[item] : -INFINITY;
     const bool yok = y64 >= 0 && y64 < C;
     const int yr = yok ? (int)y64 : -1;
     const float zy = t == 0 && yok ? load_elem<T>(row, yr) : NAN;   // used by thread 0
     const double wlo = wave_max_f64(tc);
+    const float wmx = wave_max_f32(mc);
     const int wbad = ballot(cnt < 0) != 0;
     if (lane == 0) {
       s_lo[wid] = wlo;
+      s_mx[wid] = wmx;
       s_w[wid] = wbad;
     }
     __syncthreads();
     const double lo = fmax(fmax(s_lo[0], s_lo[1]), fmax(s_lo[2], s_lo[3]));
+    const float Mrow = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
     bool generic = ((s_w[0] | s_w[1]) | (s_w[2] | s_w[3])) != 0 || o.force_generic;
     __syncthreads();
     // chunk t's entries above lo: count them, then write them at their place in the row's list
@@ -1778,7 +2421,12 @@ __global__ __launch_bounds__(kBlock) void fwl_split_finish(const void* __restric
         }
       }
     } else {
-      generic_row<T, MODE>(row, r, C, yr, lane, wid, sh, o, tau, kappa);
+      // every chunk bound is a lower bound on tau (tau_c of a subset, or H of summed entries)
+      const float t1 = fmaxf(rd32(lo), bound_below_max(Mrow));
+      select_in_memory<kWavesPerBlock, T, V4>(row, C, t1, Mrow, sm, lane, wid, tau, kappa);
+      __syncthreads();
+      write_support<kWavesPerBlock, T, MODE, V4, true>(row, r, C, yr, rd32(tau), (float)(o.scale / (double)kappa), o,
+                                                       sh.wsel, lane, wid);
     }
     if (t == 0) {
       const float Hf = rd32(tau);
@@ -1787,9 +2435,11 @@ __global__ __launch_bounds__(kBlock) void fwl_split_finish(const void* __restric
         if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + yr, (zy > Hf ? inv : 0.0f) - o.scale_f);
         else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
       }
-      const float loss = (float)((1.0 - (double)zy) + tau);
+      const double l64 = (1.0 - (double)zy) + tau;
+      const float loss = (float)l64;
       if (o.H) o.H[r] = Hf;
       if (o.loss) o.loss[r] = loss;
+      if (o.loss64) o.loss64[r] = l64;
       if (o.kappa) o.kappa[r] = kappa;
       if constexpr (MODE == kCand) o.ccnt[r] = kappa;
       lsum += (double)loss;
@@ -1946,7 +2596,7 @@ __global__ __launch_bounds__(kBlock) void fwl_fill_zero(void* __restrict__ dst, 
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
-    const void* __restrict__ z, const int64_t* __restrict__ tgt, const float* __restrict__ Hin,
+    const void* __restrict__ z, int64_t ld, const int64_t* __restrict__ tgt, const float* __restrict__ Hin,
     const int32_t* __restrict__ kap_in, const int32_t* __restrict__ cidx, int64_t N, int C, double scale,
     float scale_f, void* __restrict__ grad, bool odd_tail) {
   const int lane = lane_id();
@@ -1958,7 +2608,7 @@ __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
     const int64_t y64 = tgt[r];
     const int yr = (y64 >= 0 && y64 < C) ? (int)y64 : -1;
     const float inv = (float)(scale / (double)kap);
-    const void* row = static_cast<const char*>(z) + r * (int64_t)C * kElemBytes<T>;
+    const void* row = static_cast<const char*>(z) + r * ld * kElemBytes<T>;
     const int64_t g0 = r * (int64_t)C;
     if (kap <= kTwoPassCap) {
       if (lane < kap) {
@@ -1966,13 +2616,14 @@ __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
         if (id != yr) store_elem<T>(grad, g0 + id, inv);
       }
     } else {
+      // a support longer than the list: its entries from the logits (the fill wrote the zeros)
       for (int j = lane; j < C; j += kWave)
-        if (j != yr) store_elem<T>(grad, g0 + j, load_elem<T>(row, j) > Hf ? inv : 0.0f);
+        if (j != yr && load_elem<T>(row, j) > Hf) store_elem<T>(grad, g0 + j, inv);
     }
     if (lane == 0) {
       if (yr >= 0) store_elem<T>(grad, g0 + yr, (load_elem<T>(row, yr) > Hf ? inv : 0.0f) - scale_f);
       // a 16-bit gradient of odd size: its last element lies past the fill's last whole dword
-      if (odd_tail && r == N - 1 && yr != C - 1 && kap <= kTwoPassCap) {
+      if (odd_tail && r == N - 1 && yr != C - 1) {
         const float zl = load_elem<T>(row, C - 1);
         store_elem<T>(grad, g0 + C - 1, zl > Hf ? inv : 0.0f);
       }
@@ -2011,9 +2662,35 @@ __global__ void fwl_empty_mean(float* mean, double reduce_div) {
 // ------------------------------------------------------------------------------------------------
 // host side
 
-int g_path = 0;
-int g_cap = kCapMax;
-bool g_no_window = false;   // path 8: path 1 without line-aligned windows
+// Dispatch switches of one call (fwl_options); the process-wide defaults are set by fwl_set_params.
+struct Params {
+  int path;         // 0 automatic; 1-8 forced (fwl_set_params)
+  int cap;          // LDS candidate capacity per wavefront of the streaming kernels
+  bool no_window;   // path 8: path 1 without line-aligned windows
+};
+
+std::atomic<int> g_path{0};
+std::atomic<int> g_cap{kCapMax};
+
+Params default_params() {
+  Params p;
+  p.path = g_path.load(std::memory_order_relaxed);
+  p.cap = g_cap.load(std::memory_order_relaxed);
+  p.no_window = p.path == 8;
+  return p;
+}
+
+// the call's switches: opt (validated) or the process defaults
+bool call_params(const fwl_options* opt, Params& p) {
+  p = default_params();
+  if (opt == nullptr) return true;
+  if (opt->path < 0 || opt->path > 8) return false;
+  if (opt->cand_cap != 0 && (opt->cand_cap < kWave || opt->cand_cap > kCapMax)) return false;
+  p.path = opt->path;
+  p.no_window = opt->path == 8;
+  p.cap = opt->cand_cap != 0 ? opt->cand_cap : kCapMax;
+  return true;
+}
 
 int blocks_row(int64_t N) { return (int)(N < kMaxBlocksRow ? (N > 0 ? N : 1) : kMaxBlocksRow); }
 
@@ -2080,23 +2757,26 @@ int wave_grid(int64_t N, int64_t row_bytes, int resident) {
   return (int)(g > min_blocks ? g : min_blocks);
 }
 
-
+// Every launcher returns the grid of the kernel that stores the mean's block partials.
 
 template <typename T, int MODE, int NV, bool V4, bool AW = false>
-void launch_wave(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+int launch_wave(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   const void* k = reinterpret_cast<const void*>(&fwl_wave_rows<T, MODE, NV, V4, AW>);
   const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
   hipLaunchKernelGGL((fwl_wave_rows<T, MODE, NV, V4, AW>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+  return grid;
 }
 
 // Whether line-aligned windows apply to a launch of the register-row kernel with `spare` unused
-// 16-byte units per lane row (64*NV minus the row's units): rows of 16-byte multiples from
-// 16-byte aligned logits and gradient that share their offset within a 128-byte line, with at
-// least one row starting inside a line whose window fits (shift <= spare).  Row starts repeat mod
-// 128 every 8 rows.
-bool windows_apply(const void* z, const void* g, int64_t N, int64_t row_bytes, int spare) {
+// 16-byte units per lane row (64*NV minus the row's units): contiguous rows (logits row stride C)
+// of 16-byte multiples from 16-byte aligned logits and gradient that share their offset within a
+// 128-byte line, with at least one row starting inside a line whose window fits (shift <= spare).
+// Row starts repeat mod 128 every 8 rows.
+bool windows_apply(const void* z, const void* g, int64_t N, int64_t row_bytes, int64_t ld_bytes, int spare) {
   const uintptr_t zp = reinterpret_cast<uintptr_t>(z), gp = reinterpret_cast<uintptr_t>(g);
-  if (g == nullptr || row_bytes % 16 != 0 || zp % 16 != 0 || gp % 16 != 0 || (zp - gp) % 128 != 0) return false;
+  if (g == nullptr || ld_bytes != row_bytes || row_bytes % 16 != 0 || zp % 16 != 0 || gp % 16 != 0 ||
+      (zp - gp) % 128 != 0)
+    return false;
   for (int64_t r = 0; r < 8 && r < N; ++r) {
     const int a = (int)(((zp + (uintptr_t)(r * row_bytes)) >> 4) & 7);
     if (a > 0 && a <= spare) return true;
@@ -2110,20 +2790,17 @@ inline int wave_tier(int units) {
 }
 
 template <typename T, int MODE, int NV>
-void launch_wave_v4(const void* z, const int64_t* y, int64_t N, int C, bool aw, const Outs& o, hipStream_t s) {
+int launch_wave_v4(const void* z, const int64_t* y, int64_t N, int C, bool aw, const Outs& o, hipStream_t s) {
   if constexpr (std::is_same<T, float>::value && MODE == kGrad) {
-    if (aw) {
-      launch_wave<T, MODE, NV, true, true>(z, y, N, C, o, s);
-      return;
-    }
+    if (aw) return launch_wave<T, MODE, NV, true, true>(z, y, N, C, o, s);
   }
-  launch_wave<T, MODE, NV, true>(z, y, N, C, o, s);
+  return launch_wave<T, MODE, NV, true>(z, y, N, C, o, s);
 }
 
 // register rows: NV units per lane, the smallest power of two that covers the row (E <= 32)
 template <typename T, int MODE>
-void dispatch_wave(const void* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o,
-                   hipStream_t s) {
+int dispatch_wave(const void* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o, const Params& p,
+                  hipStream_t s) {
   if (v4) {
     // per-lane work grows with NV whatever the row length: tiers at every 64 units up to 6
     constexpr int U = kUnit<T, true>;
@@ -2131,27 +2808,28 @@ void dispatch_wave(const void* z, const int64_t* y, int64_t N, int C, bool v4, c
     // line-aligned windows for the fp32 gradient rows whose window fits the row's own tier
     bool aw = false;
     if constexpr (std::is_same<T, float>::value && MODE == kGrad)
-      aw = !g_no_window && windows_apply(z, o.grad, N, (int64_t)C * kElemBytes<T>, kWave * wave_tier(units) - units);
-    if (units <= 64) launch_wave_v4<T, MODE, 1>(z, y, N, C, aw, o, s);
-    else if (units <= 128) launch_wave_v4<T, MODE, 2>(z, y, N, C, aw, o, s);
-    else if (units <= 192) launch_wave_v4<T, MODE, 3>(z, y, N, C, aw, o, s);
-    else if (units <= 256) launch_wave_v4<T, MODE, 4>(z, y, N, C, aw, o, s);
-    else if constexpr (U == 4) {
-      if (units <= 320) launch_wave_v4<T, MODE, 5>(z, y, N, C, aw, o, s);
-      else if (units <= 384) launch_wave_v4<T, MODE, 6>(z, y, N, C, aw, o, s);
-      else launch_wave_v4<T, MODE, 8>(z, y, N, C, aw, o, s);
+      aw = !p.no_window && windows_apply(z, o.grad, N, (int64_t)C * kElemBytes<T>, o.ld * kElemBytes<T>,
+                                         kWave * wave_tier(units) - units);
+    if (units <= 64) return launch_wave_v4<T, MODE, 1>(z, y, N, C, aw, o, s);
+    if (units <= 128) return launch_wave_v4<T, MODE, 2>(z, y, N, C, aw, o, s);
+    if (units <= 192) return launch_wave_v4<T, MODE, 3>(z, y, N, C, aw, o, s);
+    if (units <= 256) return launch_wave_v4<T, MODE, 4>(z, y, N, C, aw, o, s);
+    if constexpr (U == 4) {
+      if (units <= 320) return launch_wave_v4<T, MODE, 5>(z, y, N, C, aw, o, s);
+      if (units <= 384) return launch_wave_v4<T, MODE, 6>(z, y, N, C, aw, o, s);
+      return launch_wave_v4<T, MODE, 8>(z, y, N, C, aw, o, s);
     }
-  } else {
-    if (C <= 64) launch_wave<T, MODE, 1, false>(z, y, N, C, o, s);
-    else if (C <= 128) launch_wave<T, MODE, 2, false>(z, y, N, C, o, s);
-    else if (C <= 256) launch_wave<T, MODE, 4, false>(z, y, N, C, o, s);
-    else if (C <= 512) launch_wave<T, MODE, 8, false>(z, y, N, C, o, s);
-    else launch_wave<T, MODE, 16, false>(z, y, N, C, o, s);
+    return 0;   // not reached: the host keeps 16-bit register rows within 256 units
   }
+  if (C <= 64) return launch_wave<T, MODE, 1, false>(z, y, N, C, o, s);
+  if (C <= 128) return launch_wave<T, MODE, 2, false>(z, y, N, C, o, s);
+  if (C <= 256) return launch_wave<T, MODE, 4, false>(z, y, N, C, o, s);
+  if (C <= 512) return launch_wave<T, MODE, 8, false>(z, y, N, C, o, s);
+  return launch_wave<T, MODE, 16, false>(z, y, N, C, o, s);
 }
 
 template <typename T, int MODE, int L, int NV, bool V4>
-void launch_seg(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+int launch_seg(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   constexpr int R = kWave / L;
   const void* k = reinterpret_cast<const void*>(&fwl_seg_rows<T, MODE, L, NV, V4>);
   const int64_t groups = (N + R - 1) / R;
@@ -2170,53 +2848,68 @@ void launch_seg(const void* z, const int64_t* y, int64_t N, int C, const Outs& o
   int64_t g = persistent_grid(groups, kWavesPerBlock, target, cap);
   if (g < min_blocks) g = min_blocks;
   hipLaunchKernelGGL((fwl_seg_rows<T, MODE, L, NV, V4>), dim3((int)g), dim3(kBlock), 0, s, z, y, N, C, o);
+  return (int)g;
 }
 
-// short rows: segments of 16 or 32 lanes; returns false when the row is too long for them
+// short rows: segments of 16 or 32 lanes; returns 0 (nothing launched) when the row is too long
 template <typename T, int MODE>
-bool dispatch_seg(const void* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o, hipStream_t s) {
+int dispatch_seg(const void* z, const int64_t* y, int64_t N, int C, bool v4, const Outs& o, hipStream_t s) {
   if constexpr (MODE == kCand) {
-    return false;
+    return 0;
   } else {
     if (v4) {
       constexpr int U = kUnit<T, true>;
       const int units = C / U;
-      if (units <= 16) launch_seg<T, MODE, 16, 1, true>(z, y, N, C, o, s);
-      else if (units <= 32) launch_seg<T, MODE, 16, 2, true>(z, y, N, C, o, s);
-      else if (units <= 64) launch_seg<T, MODE, 32, 2, true>(z, y, N, C, o, s);
-      else return false;
-    } else {
-      if (C <= 16) launch_seg<T, MODE, 16, 1, false>(z, y, N, C, o, s);
-      else if (C <= 32) launch_seg<T, MODE, 16, 2, false>(z, y, N, C, o, s);
-      else if (C <= 64) launch_seg<T, MODE, 16, 4, false>(z, y, N, C, o, s);
-      else if (C <= 128) launch_seg<T, MODE, 32, 4, false>(z, y, N, C, o, s);
-      else return false;
+      if (units <= 16) return launch_seg<T, MODE, 16, 1, true>(z, y, N, C, o, s);
+      if (units <= 32) return launch_seg<T, MODE, 16, 2, true>(z, y, N, C, o, s);
+      if (units <= 64) return launch_seg<T, MODE, 32, 2, true>(z, y, N, C, o, s);
+      return 0;
     }
-    return true;
+    if (C <= 16) return launch_seg<T, MODE, 16, 1, false>(z, y, N, C, o, s);
+    if (C <= 32) return launch_seg<T, MODE, 16, 2, false>(z, y, N, C, o, s);
+    if (C <= 64) return launch_seg<T, MODE, 16, 4, false>(z, y, N, C, o, s);
+    if (C <= 128) return launch_seg<T, MODE, 32, 4, false>(z, y, N, C, o, s);
+    return 0;
   }
 }
 
+// The rows a streaming launch deferred (their lists overflowed): fwl_overflow_rows right after it,
+// its block partials after the streaming kernel's `grid1`.  Nothing to launch without the
+// workspace's overflow records (the streaming kernels then solve such rows themselves).
 template <typename T, int MODE, bool V4>
-void launch_block(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+int launch_overflow(const void* z, const int64_t* y, int64_t N, int C, Outs o, int grid1, hipStream_t s) {
+  if (o.ovf_lo == nullptr) return 0;
+  if (o.partials != nullptr) o.partials += grid1;
+  const void* k = reinterpret_cast<const void*>(&fwl_overflow_rows<T, MODE, V4>);
+  const int grid = persistent_grid(N, 1, resident_blocks(k), kMaxBlocksRow);
+  hipLaunchKernelGGL((fwl_overflow_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+  return grid;
+}
+
+template <typename T, int MODE, bool V4>
+int launch_block(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   const void* k = reinterpret_cast<const void*>(&fwl_block_rows<T, MODE, V4>);
   const int grid = persistent_grid(N, 1, resident_blocks(k), kMaxBlocksRow);
   hipLaunchKernelGGL((fwl_block_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+  return grid + launch_overflow<T, MODE, V4>(z, y, N, C, o, grid, s);
 }
 
 template <typename T, int MODE, bool V4>
-void launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
+int launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<T, MODE, V4>);
   const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
   hipLaunchKernelGGL((fwl_wave_stream_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+  return grid + launch_overflow<T, MODE, V4>(z, y, N, C, o, grid, s);
 }
 
 size_t mean_ws_bytes(int64_t N);
+size_t ovf_ws_bytes(int64_t N);
 
 // The fused op in two passes: the candidate-list kernel (lists cut at kTwoPassCap, kept in the
 // workspace after the mean's part), then fwl_fill_zero and fwl_scatter_support.
 template <typename T, bool V4>
-void launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, void* ws, hipStream_t s) {
-  char* base = static_cast<char*>(ws) + mean_ws_bytes(N);
+int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, void* ws, hipStream_t s) {
+  char* base = static_cast<char*>(ws) + mean_ws_bytes(N) + ovf_ws_bytes(N);
   const size_t L = (size_t)N * kTwoPassCap;
   Outs o1 = o;
   o1.cval = reinterpret_cast<float*>(base);
@@ -2230,13 +2923,15 @@ void launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Ou
   // The read pass streams one row per wavefront when there are rows for two wavefronts per SIMD
   // (8192 x 32000: 178 us against 206 us with one block per row; 2048 x 131072: equal), else one
   // row per block (520 x 128256: 181 us with one row per wavefront, 119 us per block).
-  if (N >= 2 * 4 * (int64_t)device_cus()) launch_wave_stream<T, kCand, V4>(z, y, N, C, o1, s);
-  else launch_block<T, kCand, V4>(z, y, N, C, o1, s);
+  int grid;
+  if (N >= 2 * 4 * (int64_t)device_cus()) grid = launch_wave_stream<T, kCand, V4>(z, y, N, C, o1, s);
+  else grid = launch_block<T, kCand, V4>(z, y, N, C, o1, s);
   const int64_t bytes = N * (int64_t)C * kElemBytes<T>;
   const int64_t fill_blocks = (bytes + kFillBytes - 1) / kFillBytes;
   hipLaunchKernelGGL(fwl_fill_zero, dim3((unsigned)fill_blocks), dim3(kBlock), 0, s, o.grad, bytes);
-  hipLaunchKernelGGL((fwl_scatter_support<T>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, y, o1.H, o1.ccnt, o1.cidx, N,
-                     C, o.scale, o.scale_f, o.grad, (bytes & 3) != 0);
+  hipLaunchKernelGGL((fwl_scatter_support<T>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, o.ld, y, o1.H, o1.ccnt,
+                     o1.cidx, N, C, o.scale, o.scale_f, o.grad, (bytes & 3) != 0);
+  return grid;
 }
 
 
@@ -2270,19 +2965,22 @@ bool split_rows(int64_t N, int64_t C, int64_t elem, int path) {
   return N >= 1 && N <= kSplitMaxRows && C >= 1 && (path == 7 || (path == 0 && C * elem >= kSplitMinBytes));
 }
 
-// fp64 partial sums of the mean: one per block of the largest grid any forward launches for N rows
+// fp64 partial sums of the mean: one per block of the two largest grids a forward launches for N
+// rows (a streaming kernel, then fwl_overflow_rows)
 int64_t partial_slots(int64_t N) {
   const int64_t wave_max = (N + (int64_t)kWavesPerBlock * kRowsPerWave - 1) / ((int64_t)kWavesPerBlock * kRowsPerWave);
   int64_t b = kMaxBlocksRow > kMaxBlocksWave ? kMaxBlocksRow : kMaxBlocksWave;
-  return wave_max > b ? wave_max : b;
+  if (b < kSplitMaxRows) b = kSplitMaxRows;
+  return 2 * (wave_max > b ? wave_max : b);
 }
 
-// the mean's part of the workspace: final ticket, block partials, group partials, group tickets
-size_t mean_ws_bytes(int64_t N) {
-  const size_t P = (size_t)partial_slots(N);
-  const size_t G = (P + kTicketGroup - 1) / kTicketGroup;
-  return kWsHeader + sizeof(double) * P + sizeof(unsigned) * kTicketStride * G;
-}
+inline size_t ws_round(size_t b) { return (b + kWsAlign - 1) / kWsAlign * kWsAlign; }
+
+// the mean's part of the workspace: the block partials
+size_t mean_ws_bytes(int64_t N) { return ws_round(sizeof(double) * (size_t)partial_slots(N)); }
+
+// the overflow records of the streaming kernels: a lower bound and the maximum per row
+size_t ovf_ws_bytes(int64_t N) { return ws_round(2 * sizeof(float) * (size_t)(N > 0 ? N : 0)); }
 
 // Whether the fused op may run in two passes (the long-row block path) under switch `path`.
 // Measured on MI355X against one pass (fp32): 8192 x 32000 423 -> 400 us, 2048 x 131072 378 ->
@@ -2323,50 +3021,72 @@ size_t two_pass_bytes(int64_t N) {
 
 size_t split_scratch_bytes(int64_t N, int64_t C) {
   const int64_t items = N * split_chunks_bound(N, C, kSplitMinChunk);
-  return (size_t)items * (sizeof(double) + sizeof(int) + (size_t)kSplitCap * (sizeof(float) + sizeof(int)));
+  return (size_t)items * (sizeof(double) + sizeof(int) + sizeof(float) + (size_t)kSplitCap * (sizeof(float) + sizeof(int)));
+}
+
+size_t workspace_bytes(int64_t N, int64_t C, int path) {
+  if (N < 0) N = 0;
+  // the fp64 partials of the mean, the overflow records, then the larger of the split rows' and
+  // the two passes' scratch
+  size_t extra = 0;
+  if (split_rows(N, C, 4, path)) extra = split_scratch_bytes(N, C);
+  if (two_pass_rows(N, C, 4, path) && two_pass_bytes(N) > extra) extra = two_pass_bytes(N);
+  return mean_ws_bytes(N) + ovf_ws_bytes(N) + extra;
 }
 
 template <typename T, int MODE, bool V4>
-void launch_split(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, void* ws, hipStream_t s) {
+int launch_split(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, void* ws, hipStream_t s) {
   constexpr int kRound = kWave * kWavesPerBlock * Round<T, V4>::kSlots;
   static_assert(kRound >= kSplitMinChunk, "the workspace bound assumes rounds of >= kSplitMinChunk elements");
   const SplitPlan pl = split_plan(N, C, kRound);
   const int64_t items = N * split_chunks_bound(N, C, kSplitMinChunk);   // the workspace layout
-  char* base = static_cast<char*>(ws) + mean_ws_bytes(N);
+  char* base = static_cast<char*>(ws) + mean_ws_bytes(N) + ovf_ws_bytes(N);
   SplitScratch sc;
   sc.tau = reinterpret_cast<double*>(base);
   sc.count = reinterpret_cast<int*>(base + sizeof(double) * items);
-  sc.val = reinterpret_cast<float*>(base + (sizeof(double) + sizeof(int)) * items);
-  sc.idx = reinterpret_cast<int*>(base + (sizeof(double) + sizeof(int) + sizeof(float) * kSplitCap) * items);
+  sc.mx = reinterpret_cast<float*>(base + (sizeof(double) + sizeof(int)) * items);
+  sc.val = reinterpret_cast<float*>(base + (sizeof(double) + sizeof(int) + sizeof(float)) * items);
+  sc.idx = reinterpret_cast<int*>(base + (sizeof(double) + sizeof(int) + sizeof(float) + sizeof(float) * kSplitCap) * items);
   const void* ka = reinterpret_cast<const void*>(&fwl_split_chunks<T, MODE, V4>);
   const int ga = persistent_grid(N * (int64_t)pl.nch, 1, resident_blocks(ka), kMaxBlocksRow);
   hipLaunchKernelGGL((fwl_split_chunks<T, MODE, V4>), dim3(ga), dim3(kBlock), 0, s, z, N, C, pl.CH, pl.nch, o, sc);
   const int gb = (int)N;   // N <= kSplitMaxRows
   hipLaunchKernelGGL((fwl_split_finish<T, MODE, V4>), dim3(gb), dim3(kBlock), 0, s, z, y, N, C, pl.nch, o, sc);
+  return gb;
 }
 
 // rows are addressed through buffer resources with 32-bit byte ranges and offsets (one round
 // past the row end included), hence the bound on C
 
-// shared forward driver; `out_v4_ok` says whether the mode's dense output allows 128-bit access
+// Shared forward driver; `out_v4_ok` says whether the mode's dense output allows 128-bit access.
+// ld is the logits' row stride in elements (>= C).  The mean's block partials go to the start of
+// the workspace and fwl_mean_finish adds them after the rows.
 template <typename T, int MODE>
-int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scale, double reduce_div,
-            Outs o, bool out_v4_ok, void* ws, size_t ws_bytes, hipStream_t s) {
-  if (bad_shape(N, C64) || (N > 0 && (z == nullptr || y == nullptr))) return FWL_ERR_INVALID_ARG;
+int forward(const void* z, int64_t ld, const int64_t* y, int64_t N, int64_t C64, double scale, double reduce_div,
+            Outs o, bool out_v4_ok, void* ws, size_t ws_bytes, const Params& p, hipStream_t s) {
+  if (bad_shape(N, C64) || ld < C64 || ld > kMaxC || (N > 0 && (z == nullptr || y == nullptr)))
+    return FWL_ERR_INVALID_ARG;
   if (!aligned(z, kElemBytes<T>) || !aligned(y, 8)) return FWL_ERR_ALIGNMENT;
   const int C = (int)C64;
+  // every row's byte range must fit the buffer resources' 32-bit offsets (checked on C by
+  // bad_shape); rows further apart than that are addressed from their own base
   o.scale = scale;
   o.reduce_div = reduce_div;
   o.scale_f = (float)scale;
-  o.cap = g_cap;
-  o.force_generic = g_path == 3 || g_path == 5;
+  o.ld = ld;
+  o.cap = p.cap;
+  o.force_generic = p.path == 3 || p.path == 5;
+  o.partials = nullptr;
+  o.ovf_lo = o.ovf_mx = nullptr;
+  const bool ws_ok = ws != nullptr && aligned(ws, 8);
   if (o.mean != nullptr) {
-    if (ws == nullptr || ws_bytes < fwl_workspace_bytes(N, C64) || !aligned(ws, 8)) return FWL_ERR_WORKSPACE;
-    const size_t P = (size_t)partial_slots(N);
-    char* wb = static_cast<char*>(ws);
-    o.ticket = reinterpret_cast<unsigned*>(wb);
-    o.partials = reinterpret_cast<double*>(wb + kWsHeader);
-    o.gtickets = reinterpret_cast<unsigned*>(wb + kWsHeader + sizeof(double) * P);
+    if (!ws_ok || ws_bytes < mean_ws_bytes(N)) return FWL_ERR_WORKSPACE;
+    o.partials = static_cast<double*>(ws);
+  }
+  const size_t ws_head = mean_ws_bytes(N) + ovf_ws_bytes(N);   // where the long rows' scratch starts
+  if (ws_ok && ws_bytes >= ws_head) {
+    o.ovf_lo = reinterpret_cast<float*>(static_cast<char*>(ws) + mean_ws_bytes(N));
+    o.ovf_mx = o.ovf_lo + N;
   }
   if (N == 0) {
     if (o.mean != nullptr) hipLaunchKernelGGL(fwl_empty_mean, dim3(1), dim3(1), 0, s, o.mean, reduce_div);
@@ -2376,52 +3096,56 @@ int forward(const void* z, const int64_t* y, int64_t N, int64_t C64, double scal
   // and 16-bit rows of even length also take them (the buffer range check is per dword: a last unit
   // that runs past the row loads zeros there and stores nothing there; unaligned starts are
   // supported)
-  const bool aligned_rows = (C % kUnit<T, true>) == 0 && aligned(z, 16) && out_v4_ok;
+  const bool aligned_rows = (C % kUnit<T, true>) == 0 && (ld % kUnit<T, true>) == 0 && aligned(z, 16) && out_v4_ok;
   // 16-bit rows of even length start on 4-byte boundaries: every dword holds two elements of one
   // row, so the per-dword range check serves them as it serves fp32 rows of any length (bf16,
   // against 16-bit accesses: 1002 elements 3.73 -> 4.44 TB/s, 8194 3.58 -> 4.10, 50002 2.29 ->
   // 3.48; rows of up to 256 elements keep the 16-bit accesses, which fill more lanes: 130
   // elements 1.20 against 1.03)
-  const bool even16 = kElemBytes<T> == 2 && MODE == kGrad && C % 2 == 0 && C > 256 && aligned(z, 4) &&
+  const bool even16 = kElemBytes<T> == 2 && MODE == kGrad && C % 2 == 0 && ld % 2 == 0 && C > 256 && aligned(z, 4) &&
                       aligned(o.grad, 4);
   const bool v4 = aligned_rows || (std::is_same<T, float>::value && MODE != kMask) || even16;
-  int path = g_path == 8 ? 1 : g_path;
+  int path = p.path == 8 ? 1 : p.path;
   // measured on MI355X: registers win up to 2048 for 128-bit rows, up to 1024 for rows accessed
   // one element at a time; one streaming wavefront per row up to 8192; one block per row beyond
   const int max_wave_c = v4 ? kMaxWaveC : kMaxWaveC1;
+  const size_t ws_have = ws_ok ? ws_bytes : 0;
+  int grid = 0;
   // few long rows: chunks of every row on their own blocks (needs the scratch of the workspace)
   if (path == 0 && split_rows(N, C, kElemBytes<T>, 0)) path = 7;
   if (path == 7) {
-    if (split_rows(N, C, kElemBytes<T>, 7) && ws != nullptr && ws_bytes >= fwl_workspace_bytes(N, C64) && aligned(ws, 8)) {
-      if (v4) launch_split<T, MODE, true>(z, y, N, C, o, ws, s);
-      else launch_split<T, MODE, false>(z, y, N, C, o, ws, s);
-      return launch_status();
+    if (split_rows(N, C, kElemBytes<T>, 7) && ws_have >= ws_head + split_scratch_bytes(N, C)) {
+      grid = v4 ? launch_split<T, MODE, true>(z, y, N, C, o, ws, s) : launch_split<T, MODE, false>(z, y, N, C, o, ws, s);
+      path = -1;
+    } else {
+      path = 2;
     }
-    path = 2;
   }
+  const bool two_pass_ok = MODE == kGrad && aligned(o.grad, 4) && ws_have >= ws_head + two_pass_bytes(N);
   if (path == 0 && !aligned_rows && C <= 128) path = 6;   // short unaligned rows: 32-bit segments
   if (path == 0) {
-    const bool two_pass = MODE == kGrad && two_pass_rows(N, C, kElemBytes<T>, 0) && aligned(o.grad, 4) &&
-                          ws != nullptr && aligned(ws, 8) && ws_bytes >= mean_ws_bytes(N) + two_pass_bytes(N);
+    const bool two_pass = two_pass_ok && two_pass_rows(N, C, kElemBytes<T>, 0);
     const bool stream = C <= kMaxStreamC || (kElemBytes<T> == 2 && C <= kMaxStreamC16 && N >= kStreamMinRows16);
     path = C <= max_wave_c ? 6 : (two_pass ? 2 : (stream ? 4 : 2));
   }
   if ((path == 1 || path == 6) && C > max_wave_c) path = 4;
-  if (path == 6 && dispatch_seg<T, MODE>(z, y, N, C, aligned_rows, o, s)) return launch_status();
-  if (path == 1 || path == 6) {
-    dispatch_wave<T, MODE>(z, y, N, C, v4, o, s);
-  } else if (path == 4 || path == 5) {
-    if (v4) launch_wave_stream<T, MODE, true>(z, y, N, C, o, s);
-    else launch_wave_stream<T, MODE, false>(z, y, N, C, o, s);
-  } else if (MODE == kGrad && two_pass_rows(N, C, kElemBytes<T>, g_path) && aligned(o.grad, 4) && ws != nullptr &&
-             aligned(ws, 8) &&
-             ws_bytes >= mean_ws_bytes(N) + two_pass_bytes(N)) {
-    if (v4) launch_two_pass<T, true>(z, y, N, C, o, ws, s);
-    else launch_two_pass<T, false>(z, y, N, C, o, ws, s);
-  } else {
-    if (v4) launch_block<T, MODE, true>(z, y, N, C, o, s);
-    else launch_block<T, MODE, false>(z, y, N, C, o, s);
+  if (path == 6) {
+    grid = dispatch_seg<T, MODE>(z, y, N, C, aligned_rows, o, s);
+    if (grid > 0) path = -1;
   }
+  if (path == 1 || path == 6) {
+    grid = dispatch_wave<T, MODE>(z, y, N, C, v4, o, p, s);
+  } else if (path == 4 || path == 5) {
+    grid = v4 ? launch_wave_stream<T, MODE, true>(z, y, N, C, o, s) : launch_wave_stream<T, MODE, false>(z, y, N, C, o, s);
+  } else if (path >= 0) {
+    if (two_pass_ok && two_pass_rows(N, C, kElemBytes<T>, p.path)) {
+      grid = v4 ? launch_two_pass<T, true>(z, y, N, C, o, ws, s) : launch_two_pass<T, false>(z, y, N, C, o, ws, s);
+    } else {
+      grid = v4 ? launch_block<T, MODE, true>(z, y, N, C, o, s) : launch_block<T, MODE, false>(z, y, N, C, o, s);
+    }
+  }
+  if (o.mean != nullptr)
+    hipLaunchKernelGGL(fwl_mean_finish, dim3(1), dim3(kWave), 0, s, o.partials, (unsigned)grid, reduce_div, o.mean);
   return launch_status();
 }
 
@@ -2441,6 +3165,37 @@ int scale_grad(void* grad, const float* grad_output, int64_t go_stride, int64_t 
   return launch_status();
 }
 
+// the fused op for any element type (fwl_forward_backward_ex and the entry points over it)
+int fused_forward(int dtype, const void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C,
+                  double scale, double reduce_div, float* H, float* losses, double* losses64, float* mean_loss,
+                  int32_t* kappa, void* grad, void* workspace, size_t workspace_bytes, const Params& p,
+                  hipStream_t stream) {
+  if (N > 0 && grad == nullptr) return FWL_ERR_INVALID_ARG;
+  Outs o = {};
+  o.H = H;
+  o.loss = losses;
+  o.loss64 = losses64;
+  o.mean = mean_loss;
+  o.kappa = kappa;
+  o.grad = grad;
+  switch (dtype) {
+    case FWL_FLOAT32:
+      if (!aligned(grad, 4)) return FWL_ERR_ALIGNMENT;
+      return forward<float, kGrad>(logits, ld, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
+                                   workspace_bytes, p, stream);
+    case FWL_BFLOAT16:
+      if (!aligned(grad, 2)) return FWL_ERR_ALIGNMENT;
+      return forward<bf16_t, kGrad>(logits, ld, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
+                                    workspace_bytes, p, stream);
+    case FWL_FLOAT16:
+      if (!aligned(grad, 2)) return FWL_ERR_ALIGNMENT;
+      return forward<f16_t, kGrad>(logits, ld, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
+                                   workspace_bytes, p, stream);
+    default:
+      return FWL_ERR_INVALID_ARG;
+  }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------------------------------------
@@ -2451,69 +3206,47 @@ extern "C" {
 const char* fwl_status_string(int status) {
   switch (status) {
     case FWL_OK: return "ok";
-    case FWL_ERR_INVALID_ARG: return "invalid argument (null pointer, N < 0, C < 1 or C too large)";
+    case FWL_ERR_INVALID_ARG: return "invalid argument (null pointer, N < 0, C < 1, C too large, ld < C, or an option out of range)";
     case FWL_ERR_WORKSPACE: return "workspace missing, misaligned or smaller than fwl_workspace_bytes(N, C)";
-    case FWL_ERR_ALIGNMENT: return "misaligned pointer (logits/grad need 4 bytes, targets 8 bytes)";
+    case FWL_ERR_ALIGNMENT: return "misaligned pointer (logits/grad need their element size, targets 8 bytes)";
     case FWL_ERR_LAUNCH: return "kernel launch failed (is the current device a gfx950?)";
     case FWL_ERR_DEVICE: return "no usable device";
     default: return "unknown fwloss status";
   }
 }
 
-size_t fwl_workspace_bytes(int64_t N, int64_t C) {
-  if (N < 0) N = 0;
-  // the completion counter, the fp64 partials of the mean, then the split rows' scratch
-  size_t b = mean_ws_bytes(N);
-  // the split rows' scratch and the two passes' scratch share the space after the mean's part
-  size_t extra = 0;
-  if (split_rows(N, C, 4, g_path)) extra = split_scratch_bytes(N, C);
-  if (two_pass_rows(N, C, 4, g_path) && two_pass_bytes(N) > extra) extra = two_pass_bytes(N);
-  return b + extra;
+size_t fwl_workspace_bytes(int64_t N, int64_t C) { return workspace_bytes(N, C, default_params().path); }
+
+size_t fwl_workspace_bytes_ex(int64_t N, int64_t C, const fwl_options* options) {
+  Params p;
+  if (!call_params(options, p)) return 0;
+  return workspace_bytes(N, C, p.path);
+}
+
+int fwl_forward_backward_ex(int dtype, const void* logits, int64_t ld, const int64_t* targets, int64_t N, int64_t C,
+                            double scale, double reduce_div, float* H, float* losses, double* losses64,
+                            float* mean_loss, int32_t* kappa, void* grad, void* workspace, size_t workspace_bytes,
+                            const fwl_options* options, hipStream_t stream) {
+  Params p;
+  if (!call_params(options, p)) return FWL_ERR_INVALID_ARG;
+  return fused_forward(dtype, logits, ld, targets, N, C, scale, reduce_div, H, losses, losses64, mean_loss, kappa,
+                       grad, workspace, workspace_bytes, p, stream);
 }
 
 int fwl_forward_backward(const float* logits, const int64_t* targets, int64_t N, int64_t C,
                          double scale, double reduce_div, float* H, float* losses,
                          float* mean_loss, int32_t* kappa, float* grad, void* workspace,
                          size_t workspace_bytes, hipStream_t stream) {
-  if (N > 0 && grad == nullptr) return FWL_ERR_INVALID_ARG;
-  if (!aligned(grad, 4)) return FWL_ERR_ALIGNMENT;
-  Outs o = {};
-  o.H = H;
-  o.loss = losses;
-  o.mean = mean_loss;
-  o.kappa = kappa;
-  o.grad = grad;
-  return forward<float, kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
-                        workspace_bytes, stream);
+  return fused_forward(FWL_FLOAT32, logits, C, targets, N, C, scale, reduce_div, H, losses, nullptr, mean_loss, kappa,
+                       grad, workspace, workspace_bytes, default_params(), stream);
 }
 
 int fwl_forward_backward_typed(int dtype, const void* logits, const int64_t* targets, int64_t N, int64_t C,
                                double scale, double reduce_div, float* H, float* losses, float* mean_loss,
                                int32_t* kappa, void* grad, void* workspace, size_t workspace_bytes,
                                hipStream_t stream) {
-  if (N > 0 && grad == nullptr) return FWL_ERR_INVALID_ARG;
-  Outs o = {};
-  o.H = H;
-  o.loss = losses;
-  o.mean = mean_loss;
-  o.kappa = kappa;
-  o.grad = grad;
-  switch (dtype) {
-    case FWL_FLOAT32:
-      if (!aligned(grad, 4)) return FWL_ERR_ALIGNMENT;
-      return forward<float, kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
-                                   workspace_bytes, stream);
-    case FWL_BFLOAT16:
-      if (!aligned(grad, 2)) return FWL_ERR_ALIGNMENT;
-      return forward<bf16_t, kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
-                                    workspace_bytes, stream);
-    case FWL_FLOAT16:
-      if (!aligned(grad, 2)) return FWL_ERR_ALIGNMENT;
-      return forward<f16_t, kGrad>(logits, targets, N, C, scale, reduce_div, o, aligned(grad, 16), workspace,
-                                   workspace_bytes, stream);
-    default:
-      return FWL_ERR_INVALID_ARG;
-  }
+  return fused_forward(dtype, logits, C, targets, N, C, scale, reduce_div, H, losses, nullptr, mean_loss, kappa, grad,
+                       workspace, workspace_bytes, default_params(), stream);
 }
 
 int fwl_forward_small(const float* logits, const int64_t* targets, int64_t N, int64_t C,
@@ -2527,8 +3260,8 @@ int fwl_forward_small(const float* logits, const int64_t* targets, int64_t N, in
   o.mean = mean_loss;
   o.kappa = kappa;
   o.mask = selected;
-  return forward<float, kMask>(logits, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o,
-                        aligned(selected, 4), workspace, workspace_bytes, stream);
+  return forward<float, kMask>(logits, C, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o,
+                               aligned(selected, 4), workspace, workspace_bytes, default_params(), stream);
 }
 
 int fwl_forward_large(const float* logits, const int64_t* targets, int64_t N, int64_t C,
@@ -2549,8 +3282,8 @@ int fwl_forward_large(const float* logits, const int64_t* targets, int64_t N, in
   o.ccnt = cand_counts;
   o.cstride = (int)(C > 0 && C <= kMaxC ? C : 0);   // whole rows (checked again by forward)
   o.ccap = o.cstride;
-  return forward<float, kCand>(logits, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o, true,
-                        workspace, workspace_bytes, stream);
+  return forward<float, kCand>(logits, C, targets, N, C, N > 0 ? 1.0 / (double)N : 1.0, (double)N, o, true,
+                               workspace, workspace_bytes, default_params(), stream);
 }
 
 int fwl_backward_small(const int64_t* targets, const uint8_t* selected, const int32_t* kappa,
@@ -2617,15 +3350,14 @@ int fwl_scale_grad_typed(int dtype, void* grad, const float* grad_output, int64_
 
 int fwl_set_params(int path, int cand_cap) {
   if (path < 0 || path > 8 || cand_cap < kWave || cand_cap > kCapMax) return FWL_ERR_INVALID_ARG;
-  g_path = path;
-  g_no_window = path == 8;
-  g_cap = cand_cap;
+  g_path.store(path, std::memory_order_relaxed);
+  g_cap.store(cand_cap, std::memory_order_relaxed);
   return FWL_OK;
 }
 
 int fwl_get_params(int* path, int* cand_cap) {
-  if (path) *path = g_path;
-  if (cand_cap) *cand_cap = g_cap;
+  if (path) *path = g_path.load(std::memory_order_relaxed);
+  if (cand_cap) *cand_cap = g_cap.load(std::memory_order_relaxed);
   return FWL_OK;
 }
 

@@ -50,7 +50,10 @@ class ReductionError(KeyError, ValueError):
 
 
 class FWFunction(torch.autograd.Function):
-    """Eager-gradient autograd Function (the GPU counterpart of fw_cpu.cpp:721-741)."""
+    """Eager-gradient autograd Function (the GPU counterpart of fw_cpu.cpp:721-741).  The backward
+    scales the stored gradient in place and hands it over, so it runs once per forward, like the
+    reference's, which erases the stored gradient (fw_cpu.cpp:734-740); a second backward through
+    the same graph raises instead of returning a gradient scaled twice."""
 
     @staticmethod
     def forward(ctx, logits, target, reduction):
@@ -61,15 +64,20 @@ class FWFunction(torch.autograd.Function):
             scale, rdiv = 1.0, 1.0
         _, losses, reduced, _, grad = _ext.fw_forward_backward(logits.detach(), target, scale, rdiv)
         ctx.save_for_backward(grad)
+        ctx.consumed = False
         # the loss has the logits' dtype, as in the reference (fw_cpu.cpp:732); computed in fp32/fp64
         out = losses if reduction == "none" else reduced
         return out if out.dtype == logits.dtype else out.to(logits.dtype)
 
     @staticmethod
     def backward(ctx, grad_output):
+        if ctx.consumed:
+            raise RuntimeError("familywise_loss: the backward of this loss already ran (its stored gradient was "
+                               "scaled in place and handed over); compute the loss again for another backward")
         (grad,) = ctx.saved_tensors
         if not ctx.needs_input_grad[0]:
             return None, None, None
+        ctx.consumed = True
         _ext.fw_scale_grad(grad, grad_output.detach())
         return grad, None, None
 
@@ -92,14 +100,14 @@ def familywise_loss(logits, target, reduction="mean"):
 
 
 def fw_loss_grad(Z, y, scale=1.0, flat_kmax=None, serial_below=None, use_chunked=None):
-    """(per-row loss [N] float64, scale * gradient [N, C] float32, kappa [N] int64), the outputs and
-    dtypes of fwcpp.fw_loss_grad (src/cpu/fwcpp.py:21-23).  flat_kmax, serial_below and use_chunked
-    tune the reference's CPU branches (fw_cpu.cpp:750-757); they are accepted and have no effect
-    here.  The losses are computed in fp64 and rounded to fp32 on the device, then widened."""
+    """(per-row loss [N] float64, scale * gradient [N, C] in Z's dtype, kappa [N] int64), the outputs
+    and dtypes of fwcpp.fw_loss_grad (src/cpu/fwcpp.py:21-23).  flat_kmax, serial_below and
+    use_chunked tune the reference's CPU branches (fw_cpu.cpp:750-757); they are accepted and have
+    no effect here.  The losses are the kernel's fp64 values (1 - z_y) + tau, not rounded to fp32."""
     if not Z.is_cuda:
         raise RuntimeError("fw_loss_grad: Z must be a CUDA (ROCm) tensor")
-    _, losses, _, kappa, grad = _ext.fw_forward_backward(Z, y, float(scale), 1.0)
-    return losses.double(), grad, kappa.long()
+    out = _ext.fw_forward_backward(Z, y, float(scale), 1.0, losses64=True)
+    return out[5], out[4], out[3].long()
 
 
 def linear_forward(hidden, weight, target, chunk=8192):

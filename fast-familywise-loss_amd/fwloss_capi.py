@@ -22,6 +22,9 @@ _D = ctypes.c_double
 SIGNATURES = {
     "fwl_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "fwl_workspace_bytes": ([_I64, _I64], ctypes.c_size_t),
+    "fwl_workspace_bytes_ex": ([_I64, _I64, _P], ctypes.c_size_t),
+    "fwl_forward_backward_ex": ([ctypes.c_int, _P, _I64, _P, _I64, _I64, _D, _D, _P, _P, _P, _P, _P, _P, _P,
+                                 ctypes.c_size_t, _P, _P], ctypes.c_int),
     "fwl_forward_backward": ([_P, _P, _I64, _I64, _D, _D, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], ctypes.c_int),
     "fwl_forward_small": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], ctypes.c_int),
     "fwl_backward_small": ([_P, _P, _P, _I64, _I64, _P, _P], ctypes.c_int),
@@ -86,16 +89,21 @@ def _check(rc, name):
         raise RuntimeError(f"{name}: {status_string(rc)} ({rc})")
 
 
+class Options(ctypes.Structure):
+    """struct fwl_options: the dispatch switches of one call."""
+    _fields_ = [("path", ctypes.c_int), ("cand_cap", ctypes.c_int)]
+
+
 class Workspace:
-    """Zero-filled device workspace; the library leaves it zero-filled after every call."""
+    """Device workspace (any contents: the library writes what it reads there first)."""
 
     def __init__(self, device, nbytes=1 << 16):
-        self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
 
-    def get(self, N, C):
-        need = lib().fwl_workspace_bytes(N, C)
+    def get(self, N, C, options=None):
+        need = lib().fwl_workspace_bytes_ex(N, C, None if options is None else ctypes.byref(options))
         if self.buf.numel() < need:
-            self.buf = torch.zeros(need, dtype=torch.uint8, device=self.buf.device)
+            self.buf = torch.empty(need, dtype=torch.uint8, device=self.buf.device)
         return self.buf
 
 
@@ -144,3 +152,31 @@ def forward_backward_typed(z, y, scale=None, reduce_div=None, ws=None, grad=None
 
 def set_params(path, cand_cap=512):
     _check(lib().fwl_set_params(path, cand_cap), "fwl_set_params")
+
+
+def forward_backward_ex(z, y, scale=None, reduce_div=None, ws=None, path=None, cand_cap=0, losses64=False,
+                        stream=None):
+    """fwl_forward_backward_ex: float32/bfloat16/float16 logits whose rows may lie any distance apart
+    (z.stride(1) == 1; ld = z.stride(0)), per-call options (path None: the process defaults), and the
+    fp64 per-row losses when `losses64`.  Returns dict(H, loss, loss64, mean, kappa, grad)."""
+    N, C = z.shape
+    if N > 1 and z.stride(1) != 1:
+        raise ValueError("the elements of a row must be adjacent (z.stride(1) == 1)")
+    ld = z.stride(0) if N > 1 else C
+    scale = (1.0 / N if N else 1.0) if scale is None else scale
+    reduce_div = float(N) if reduce_div is None else reduce_div
+    opt = None if path is None else Options(path, cand_cap)
+    ws = ws or Workspace(z.device)
+    buf = ws.get(N, C, opt)
+    dev = z.device
+    out = dict(H=torch.empty(N, device=dev), loss=torch.empty(N, device=dev),
+               loss64=torch.empty(N, dtype=torch.float64, device=dev) if losses64 else None,
+               mean=torch.empty((), device=dev), kappa=torch.empty(N, dtype=torch.int32, device=dev),
+               grad=torch.empty((N, C), dtype=z.dtype, device=dev))
+    s = ctypes.c_void_p((stream or torch.cuda.current_stream()).cuda_stream)
+    rc = lib().fwl_forward_backward_ex(DTYPES[z.dtype], _ptr(z), ld, _ptr(y), N, C, scale, reduce_div, _ptr(out["H"]),
+                                       _ptr(out["loss"]), _ptr(out["loss64"]), _ptr(out["mean"]), _ptr(out["kappa"]),
+                                       _ptr(out["grad"]), _ptr(buf), buf.numel(),
+                                       None if opt is None else ctypes.byref(opt), s)
+    _check(rc, "fwl_forward_backward_ex")
+    return out

@@ -54,6 +54,41 @@ def make(cfg, N=None, seed=0):
     return np.ascontiguousarray(z, dtype=np.float32), y
 
 
+DISTS = ("gauss", "laplace", "mixture")
+
+
+def make_dist(dist, N, C, sigma=1.0, seed=0):
+    """(z float32 [N, C], y int64 [N]) from the input distributions of the reference's GPU harness
+    (benchmarks/cuda_benchmarks/data_io.py:8-83), swept there over sigma in {0.001, 0.01, 0.1, 1,
+    10, 100} (CE_FW_perf.py:94-96):
+
+        gauss    sigma * N(0, 1)                                  (data_io.py:8-21)
+        laplace  Laplace(0, sigma / sqrt(2)), variance sigma^2    (data_io.py:23-42)
+        mixture  each entry N(0, 1) or N(0, sigma^2), with probability 1/2 each (data_io.py:44-83)
+
+    Labels are uniform in [0, C).  Drawn with numpy's PCG64 (float32 draws), so the CPU checkers
+    and the GPU see identical bytes; the distributions are the reference's, the streams are not
+    torch's."""
+    if dist not in DISTS:
+        raise KeyError(dist)
+    rng = np.random.default_rng(seed)
+    y = rng.integers(0, C, size=N, dtype=np.int64)
+    s = np.float32(sigma)
+    if dist == "gauss":
+        z = rng.standard_normal((N, C), dtype=np.float32)
+        z *= s
+    elif dist == "laplace":
+        # the difference of two standard exponentials is Laplace(0, 1)
+        z = rng.standard_exponential((N, C), dtype=np.float32)
+        z -= rng.standard_exponential((N, C), dtype=np.float32)
+        z *= np.float32(sigma / np.sqrt(2.0))
+    else:
+        first = rng.random((N, C), dtype=np.float32) < np.float32(0.5)
+        z = rng.standard_normal((N, C), dtype=np.float32)
+        z[~first] *= s
+    return np.ascontiguousarray(z, dtype=np.float32), y
+
+
 FAMILIES = ("gauss", "ties", "constant", "sorted", "two_level", "outlier", "flat", "heavy", "neginf")
 
 

@@ -22,13 +22,16 @@
  *   - all pointers are device pointers; logits and grad are row-major [N, C], contiguous;
  *   - every call is asynchronous on `stream` and allocates nothing;
  *   - `workspace` is caller-provided device memory of at least fwl_workspace_bytes(N, C) bytes,
- *     8-byte aligned and zero-filled before its first use.  It holds completion counters, which
- *     every call returns to zero, and scratch that every call writes before reading it (partial
- *     sums of the mean; for few long rows the chunk thresholds and supports).  Calls that run
- *     concurrently (different streams) must not share one workspace;
+ *     8-byte aligned, with any contents: every call writes what it reads there before reading it
+ *     (the mean's block partial sums, added by a one-block kernel after the rows; for few long rows
+ *     the chunk thresholds and supports; for many long rows the support lists between the two
+ *     passes).  No state survives from one call to the next.  Calls that run concurrently
+ *     (different streams) must not share one workspace;
  *   - targets outside [0, C) do not fault: that row gets loss = NaN and no label term in grad;
  *   - NaN logits are never selected; rows without a finite maximum give kappa = 0, H = NaN;
- *   - the return value is FWL_OK or an fwl_status (argument errors are detected before launch).
+ *   - the return value is FWL_OK or an fwl_status (argument errors are detected before launch);
+ *   - calls are re-entrant: the dispatch switches of a call come from its fwl_options argument (the
+ *     _ex entry points) or, for the others, from the process-wide defaults of fwl_set_params.
  */
 #ifndef FWLOSS_H
 #define FWLOSS_H
@@ -58,18 +61,30 @@ enum fwl_dtype {
   FWL_FLOAT16 = 2     /* IEEE binary16 */
 };
 
+/* Dispatch switches of one call (the _ex entry points); NULL means the process-wide defaults of
+ * fwl_set_params.  Each call reads only its own options, so calls with different options may run
+ * at the same time from different host threads. */
+typedef struct fwl_options {
+  int path;       /* as fwl_set_params: 0 = automatic dispatch, 1-8 = a forced kernel family */
+  int cand_cap;   /* LDS candidate capacity per wavefront of paths 2 and 4, in [64, 512]; 0 = 512 */
+} fwl_options;
+
 /* Human-readable text of a status code (static storage). */
 const char* fwl_status_string(int status);
 
-/* Bytes of device workspace the forward entry points need for an [N, C] problem: 256 bytes, one
- * fp64 per block of the largest grid (>= 4096 blocks), 64 bytes per group of 32 blocks, then the
- * larger of: 524 bytes per (row, chunk) for at most 128 rows of >= 24576 elements (the split
- * rows), and 520 bytes per row for >= 384 rows of >= 32000 elements or for batches of >= 48M
- * elements in rows of >= 8192 (the fused op in two passes).  The answer follows the current
- * fwl_set_params switches (forcing path 7 needs the chunk scratch, forcing path 2 or 3 the
- * two-pass scratch, for rows of any length).  A smaller workspace is accepted where no mean is
- * requested: the one-pass kernels then run. */
+/* Bytes of device workspace the forward entry points need for an [N, C] problem: one fp64 per
+ * block of the largest grid (>= 4096 blocks), rounded up to 256 bytes, then the larger of: 528
+ * bytes per (row, chunk) for at most 128 rows of >= 24576 elements (the split rows), and 520
+ * bytes per row for >= 384 rows of >= 32000 elements or for batches of >= 48M elements in rows of
+ * >= 8192 (the fused op in two passes).  The answer follows the current fwl_set_params switches
+ * (forcing path 7 needs the chunk scratch, forcing path 2 or 3 the two-pass scratch, for rows of
+ * any length).  A smaller workspace is accepted: the mean needs only its first part, and without
+ * room for the rest the one-pass kernels run. */
 size_t fwl_workspace_bytes(int64_t N, int64_t C);
+
+/* fwl_workspace_bytes for a call with these options (NULL: the process-wide defaults); 0 for
+ * options out of range. */
+size_t fwl_workspace_bytes_ex(int64_t N, int64_t C, const fwl_options* options);
 
 /* Fused forward + backward: the whole hot path in one launch, reading logits once and writing the
  * dense gradient once.  mean_loss receives (float)(sum_r losses[r] / reduce_div) (reduce_div = N
@@ -94,6 +109,20 @@ int fwl_forward_backward_typed(int dtype, const void* logits, const int64_t* tar
                                int64_t C, double scale, double reduce_div, float* H, float* losses,
                                float* mean_loss, int32_t* kappa, void* grad, void* workspace,
                                size_t workspace_bytes, hipStream_t stream);
+
+/* fwl_forward_backward_typed with a logits row stride and per-call options:
+ *   ld        elements from one row of logits to the next (>= C; C for contiguous rows), so a
+ *             column slice such as logits[:, 1:] needs no copy (grad stays contiguous [N, C]);
+ *   losses64  optional fp64 per-row losses (1 - z_y) + tau, the value `losses` rounds; the
+ *             reference CPU path returns its per-row losses in fp64 (src/cpu/fw_cpu.cpp:614,
+ *             :750-757, fw_loss_grad);
+ *   options   dispatch switches of this call (NULL: the fwl_set_params defaults).
+ * Outputs as fwl_forward_backward_typed; every pointer output may be NULL but grad. */
+int fwl_forward_backward_ex(int dtype, const void* logits, int64_t ld, const int64_t* targets, int64_t N,
+                            int64_t C, double scale, double reduce_div, float* H, float* losses,
+                            double* losses64, float* mean_loss, int32_t* kappa, void* grad,
+                            void* workspace, size_t workspace_bytes, const fwl_options* options,
+                            hipStream_t stream);
 
 /* fwl_forward_backward for float64 logits (the reference CPU path's second dtype,
  * src/cpu/fw_cpu.cpp:697-703, run_generic<double>; the reference GPU ops take float32 only).
@@ -198,17 +227,19 @@ int fwl_linear_dweight(int dtype, const void* hidden, int64_t N, int64_t V, int6
                        const int64_t* keys, const float* values, int64_t P, void* dweight,
                        hipStream_t stream);
 
-/* Process-wide dispatch switches, the GPU counterpart of the reference CPU path's set_params
- * (src/cpu/fw_cpu.cpp:758-763, used by its tests to force each branch).  Not thread-safe; meant
- * for tests and tuning.
+/* Process-wide default dispatch switches, the GPU counterpart of the reference CPU path's
+ * set_params (src/cpu/fw_cpu.cpp:758-763, used by its tests to force each branch).  A call reads
+ * the defaults once, at its start (atomically); a call that needs its own switches passes
+ * fwl_options to an _ex entry point instead.
  *   path:      0 = automatic (7 for at most 128 rows of at least 96 KiB, 6 for short rows, 1 for
  *              C <= 2048 or C <= 1024 when rows are not 16-byte aligned, 4 for C <= 8192, else 2),
  *              1 = one wavefront per row with the row in registers (C <= 2048, or 1024 for rows
  *              that are not 16-byte aligned; larger C runs path 4),
  *              2 = one block per row, streamed, with LDS candidate lists,
- *              3 = path 2 with the generic multi-pass solve forced,
+ *              3 = path 2 with the overflow solve forced (rows solved in memory: a histogram
+ *              pass, at most 4 refinements, a collect pass; a bounded bisection as last resort),
  *              4 = one wavefront per row, streamed, with an LDS candidate list,
- *              5 = path 4 with the generic multi-pass solve forced,
+ *              5 = path 4 with the overflow solve forced,
  *              6 = short rows: 16- or 32-lane segments of a wavefront, 4 or 2 rows per
  *              iteration (rows of up to 64 units; longer rows and candidate lists run path 1),
  *              7 = split rows: one block per (row, chunk of >= 4096 elements) streams the chunk
@@ -219,7 +250,8 @@ int fwl_linear_dweight(int dtype, const void* hidden, int64_t N, int64_t V, int6
  *              fp32 gradient rows through windows that start on the row's first 128-byte line
  *              boundary, where the logits and gradient share their offsets within a line).
  *   cand_cap:  LDS candidate capacity per wavefront of paths 2 and 4, in [64, 512] (512 =
- *              default); smaller values make rows overflow into the generic solve sooner.
+ *              default); smaller values make rows overflow into the overflow solve sooner and
+ *              shrink its LDS list, so that more rows take its refinement passes.
  * Returns FWL_ERR_INVALID_ARG for values out of range. */
 int fwl_set_params(int path, int cand_cap);
 int fwl_get_params(int* path, int* cand_cap);

@@ -31,7 +31,7 @@ def P(x):
 def test_library_exports_every_declared_function():
     L = capi.lib()
     declared = capi.declared_functions()
-    assert len(declared) == 22
+    assert len(declared) == 24
     for name in declared:
         assert hasattr(L, name), name
     # the ctypes signature table covers exactly the header
@@ -56,17 +56,30 @@ def test_status_strings():
     assert capi.status_string(99) == "unknown fwloss status"
 
 
+def ws_round(b):
+    return -(-b // 256) * 256
+
+
+def ws_expect(N, extra=0):
+    """The workspace layout: fp64 partials for the two largest grids of a call (>= 4096 blocks
+    each, one per 256 rows beyond), the overflow records (two floats per row), then the long rows'
+    scratch."""
+    slots = 2 * max(-(-N // 256), 4096)
+    return ws_round(8 * slots) + ws_round(8 * N) + extra
+
+
 def test_workspace_bytes():
     L = capi.lib()
-    base = L.fwl_workspace_bytes(0, 1)
-    assert base >= 256 + 8 * 4096
-    assert L.fwl_workspace_bytes(65536, 1000) == base
-    # grows with N once the row-per-wave grid exceeds the fixed caps: per block one fp64 partial,
-    # per group of 32 blocks one 64-byte ticket slot
-    big = L.fwl_workspace_bytes(1 << 22, 10)
-    blocks = (1 << 22) // 256
-    assert big == 256 + 8 * blocks + 64 * (blocks // 32)
+    assert L.fwl_workspace_bytes(0, 1) == ws_expect(0)
+    assert L.fwl_workspace_bytes(65536, 1000) == ws_expect(65536)
+    assert L.fwl_workspace_bytes(1 << 22, 10) == ws_expect(1 << 22)
     assert L.fwl_workspace_bytes(1 << 22, 10) >= L.fwl_workspace_bytes((1 << 22) - 1, 10)
+    # per-call options: the same sizes as the process-wide switches; out of range gives 0
+    assert L.fwl_workspace_bytes_ex(65536, 1000, None) == ws_expect(65536)
+    opt = capi.Options(2, 512)
+    assert L.fwl_workspace_bytes_ex(16, 1000, ctypes.byref(opt)) == ws_expect(16, 16 * (64 * 8 + 8))
+    for bad in (capi.Options(9, 512), capi.Options(-1, 0), capi.Options(2, 63), capi.Options(2, 513)):
+        assert L.fwl_workspace_bytes_ex(16, 1000, ctypes.byref(bad)) == 0
 
 
 def test_forward_backward_argument_errors():
@@ -87,8 +100,24 @@ def test_forward_backward_argument_errors():
     assert call(y=A4) == 3
     assert call(grad=A2) == 3
     assert call(ws=None) == 2
-    assert call(wsb=ws_need - 1) == 2
+    assert call(wsb=ws_round(8 * 2 * 4096) - 1) == 2     # the mean needs its partials
     assert call(ws=A4 + 2) == 2
+
+
+def test_ex_entry_point_argument_errors():
+    L = capi.lib()
+    ws_need = L.fwl_workspace_bytes(8, 16)
+
+    def call(dtype=0, z=A16, ld=16, N=8, C=16, l64=A16, grad=A16, opt=None):
+        return L.fwl_forward_backward_ex(dtype, P(z), ld, P(A16), N, C, 1.0, 1.0, P(A16), P(A16), P(l64), P(A16),
+                                         P(A16), P(grad), P(A16), ws_need, opt, None)
+    assert call(ld=15) == 1                     # rows overlap
+    assert call(ld=2 ** 29 + 1) == 1
+    assert call(dtype=3) == 1
+    assert call(grad=None) == 1
+    assert call(dtype=1, z=A16 + 1) == 3
+    for bad in (capi.Options(9, 0), capi.Options(-1, 0), capi.Options(3, 32), capi.Options(3, 1024)):
+        assert call(opt=ctypes.byref(bad)) == 1
 
 
 def test_other_entry_point_argument_errors():
@@ -202,40 +231,39 @@ def test_workspace_sizes():
     p, c = ctypes.c_int(-1), ctypes.c_int(-1)
     L.fwl_get_params(ctypes.byref(p), ctypes.byref(c))
     saved = (p.value, c.value)
+    W = L.fwl_workspace_bytes
     try:
         L.fwl_set_params(0, 512)
-        base = L.fwl_workspace_bytes(4096, 1000)
-        assert base >= 256 + 8 * 4096
-        assert L.fwl_workspace_bytes(16, 1000) == base           # short rows: no scratch
-        assert L.fwl_workspace_bytes(65536, 8191) == base
-        assert L.fwl_workspace_bytes(0, 131072) == base
+        assert W(16, 1000) == ws_expect(16)           # short rows: no scratch
+        assert W(65536, 8191) == ws_expect(65536)
+        assert W(0, 131072) == ws_expect(0)
         # >= 384 rows of >= 32000 elements, or batches of >= 48M elements in rows of >= 8192 (the
         # fp32 rules, which cover the 16-bit one) run the fused op in two passes: per row 64
         # support values and indices, kappa and H
         row = 64 * 8 + 4 + 4
-        assert L.fwl_workspace_bytes(2048, 131072) - base == 2048 * row
-        assert L.fwl_workspace_bytes(384, 32000) - base == 384 * row
-        assert L.fwl_workspace_bytes(383, 32000) == base
-        assert L.fwl_workspace_bytes(6144, 8192) - base == 6144 * row     # 48M elements
-        assert L.fwl_workspace_bytes(6143, 8192) == base
-        assert L.fwl_workspace_bytes(65536, 8192) - base == 65536 * row
-        assert L.fwl_workspace_bytes(1024, 31999) == base
-        assert L.fwl_workspace_bytes(129, 24576) == base
-        assert L.fwl_workspace_bytes(128, 24575) == base
+        assert W(2048, 131072) == ws_expect(2048, 2048 * row)
+        assert W(384, 32000) == ws_expect(384, 384 * row)
+        assert W(383, 32000) == ws_expect(383)
+        assert W(6144, 8192) == ws_expect(6144, 6144 * row)      # 48M elements
+        assert W(6143, 8192) == ws_expect(6143)
+        assert W(65536, 8192) == ws_expect(65536, 65536 * row)
+        assert W(1024, 31999) == ws_expect(1024)
+        assert W(129, 24576) == ws_expect(129)
+        assert W(128, 24575) == ws_expect(128)
         # (row, chunk) items: about 1024 in all, chunks of at least 4096 elements, <= 256 per row;
-        # 8 + 4 + 64 * 8 bytes per item
-        item = 8 + 4 + 64 * 8
-        assert L.fwl_workspace_bytes(16, 131072) - base == 16 * 32 * item
-        assert L.fwl_workspace_bytes(3, 131072) - base == 3 * 32 * item
-        assert L.fwl_workspace_bytes(1, 2 ** 29) - base == 1 * 256 * item
-        assert L.fwl_workspace_bytes(128, 24576) - base == 128 * 6 * item
-        assert L.fwl_workspace_bytes(100, 40000) - base == 100 * 10 * item
+        # per item tau_c (8), the support size (4), the chunk maximum (4), 64 values and indices
+        item = 8 + 4 + 4 + 64 * 8
+        assert W(16, 131072) == ws_expect(16, 16 * 32 * item)
+        assert W(3, 131072) == ws_expect(3, 3 * 32 * item)
+        assert W(1, 2 ** 29) == ws_expect(1, 1 * 256 * item)
+        assert W(128, 24576) == ws_expect(128, 128 * 6 * item)
+        assert W(100, 40000) == ws_expect(100, 100 * 10 * item)
         L.fwl_set_params(2, 512)                                  # forced block path: two passes
-        assert L.fwl_workspace_bytes(16, 1000) - base == 16 * row
+        assert W(16, 1000) == ws_expect(16, 16 * row)
         L.fwl_set_params(7, 512)
-        assert L.fwl_workspace_bytes(16, 1000) - base == 16 * 1 * item
-        assert L.fwl_workspace_bytes(4, 30000) - base == 4 * 8 * item
-        assert L.fwl_workspace_bytes(129, 30000) == base          # more rows than path 7 takes
+        assert W(16, 1000) == ws_expect(16, 16 * 1 * item)
+        assert W(4, 30000) == ws_expect(4, 4 * 8 * item)
+        assert W(129, 30000) == ws_expect(129)                    # more rows than path 7 takes
     finally:
         L.fwl_set_params(*saved)
 
