@@ -160,65 +160,113 @@ __device__ __forceinline__ void row_bias(int C, int lane, float* bias) {
   for (int i = 0; i < E; ++i) bias[i] = slot_index<T, VEC>(i, lane) < C ? -0.0f : -INFINITY;
 }
 
-// A register row with more than 64 candidates z > t0, all of them in its LDS list cl (n of them;
-// indices in ci_lds in candidate-list mode).  The tau of the 64 lane maxima, a subset of the row, is
-// a lower bound t1 on tau, usually close to it: the list is cut at t1, and a list of at most 64
-// entries is sorted (resolve_list); a longer one takes fixed-point steps t <- H({z > t}) from t1
-// (each iterate <= tau, the set shrinking every step until it is the support), and after
-// kListSteps of them a bisection over the keys of (t1, m], so that the passes over the list are
-// bounded.  Works on the LDS list only: the register row stays untouched for the outputs.
-constexpr int kListSteps = 32;
-template <int MODE>
-__device__ __forceinline__ void solve_many(float lm, float t0, float m, int lane, float* cl, int* ci_lds, int& n,
-                                           double& tau, int& kappa, uint64_t& support) {
+// fp64 sum and count of the register row's entries > thr, in a fixed order (slot order per lane,
+// then the wavefront tree); the empty asm keeps the compiler from hoisting the conversions of the
+// row out of the caller's loops (16-32 more VGPRs held across them)
+template <int E>
+__device__ __forceinline__ void reg_sum_count(const float* x, float thr, double& s, int& c) {
+  double acc = 0.0;
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    float v = x[i];
+    asm volatile("" : "+v"(v));
+    const bool k = v > thr;
+    acc += k ? (double)v : 0.0;
+    cnt += k ? 1 : 0;
+  }
+  s = wave_sum_f64(acc);
+  c = wave_sum_i32(cnt);
+}
+
+// the same with per-lane fp32 partial sums (for bounds: see safe_lower32)
+template <int E>
+__device__ __forceinline__ void reg_sum_count32(const float* x, float thr, double& s, int& c) {
+  float acc = 0.0f;
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    const bool k = x[i] > thr;
+    acc += k ? x[i] : 0.0f;
+    cnt += k ? 1 : 0;
+  }
+  s = wave_sum_f64((double)acc);
+  c = wave_sum_i32(cnt);
+}
+
+// A register row with more than 64 candidates z > t0 (its LDS list cl holds them, n of them;
+// indices in ci_lds in candidate-list mode).  The tau of the 64 lane maxima, a subset of the row,
+// is a lower bound t1 on tau, usually close to it.  At most 64 entries above t1 are staged again
+// and sorted (resolve_list).  Otherwise fixed-point steps t <- H({z > t}) run over the registers:
+// first with fp32 partial sums, each step a safe lower bound (safe_lower32), until they stall;
+// then exact fp64 steps from there (each iterate <= tau, the set shrinking until it is the
+// support), at most kRegSteps of them, and a bisection over the keys of (t1, m] after that, so
+// that the passes over the registers are bounded.  The list keeps the candidates > t0 for the
+// candidate-list output.
+constexpr int kRegSteps = 32;
+template <typename T, int MODE, int E, bool V4>
+__device__ __forceinline__ void solve_many(const float* x, float lm, float t0, float m, int lane, float* cl,
+                                           int* ci_lds, int& n, double& tau, int& kappa, uint64_t& support) {
   const double tl = select_tier<kWave>(lm, kWave, lane);
+  const float B = fmaxf(fabsf(m), fabsf(t0));
   float t1 = t0;
   if (tl == tl) {
-    const double B = (double)fabsf(m) + 1.0;
-    const float r = rd32(tl - ((double)kWave * B + fabs(tl) + 1.0) * 0x1p-51);
+    const float r = rd32(tl - ((double)kWave * (double)(fabsf(m) + 1.0f) + fabs(tl) + 1.0) * 0x1p-51);
     if (isfinite(r)) t1 = fmaxf(t0, prev_f32(r));
   }
-  // keep the list entries > t1 (order kept)
-  int w = 0;
-  for (int p0 = 0; p0 < n; p0 += kWave) {
-    const int p = p0 + lane;
-    const float v = p < n ? cl[p] : -INFINITY;
-    int id = 0;
-    if constexpr (MODE == kCand) id = p < n ? ci_lds[p] : 0;
-    const bool keep = v > t1;
-    const uint64_t b = ballot(keep);
+  int n1 = 0;
+#pragma unroll
+  for (int i = 0; i < E; ++i) n1 += __popcll(ballot(x[i] > t1));
+  if (n1 <= kWave) {
     __builtin_amdgcn_wave_barrier();
-    if (keep) {
-      cl[w + rank_in(b)] = v;
-      if constexpr (MODE == kCand) ci_lds[w + rank_in(b)] = id;
+    int at = 0;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const bool c = x[i] > t1;
+      const uint64_t b = ballot(c);
+      if (b != 0) {
+        if (c) {
+          cl[at + rank_in(b)] = x[i];
+          if constexpr (MODE == kCand) ci_lds[at + rank_in(b)] = slot_index<T, V4>(i, lane);
+        }
+        at += __popcll(b);
+      }
     }
-    w += __popcll(b);
+    n = n1;
     __builtin_amdgcn_wave_barrier();
-  }
-  n = w;
-  if (n <= kWave) {
     resolve_list(cl, n, t1, m, lane, tau, kappa, support);
     return;
   }
   support = 0;
-  double t = (double)t1, s;
+  // bound steps with fp32 partial sums
+  float t = t1;
+  for (int it = 0; it < kRegSteps; ++it) {
+    double s;
+    int c;
+    reg_sum_count32<E>(x, t, s, c);
+    const float nt = safe_lower32(s, c, B);
+    if (!(nt > t)) break;
+    t = nt;
+  }
+  // exact steps from the bound
+  double tt = (double)t, s;
   int c;
-  list_sum_count(cl, n, t1, lane, s, c);
+  reg_sum_count<E>(x, t, s, c);
   bool conv = false;
   tau = NAN;
   kappa = 0;
-  for (int it = 0; it < kListSteps; ++it) {
+  for (int it = 0; it < kRegSteps && c > 0; ++it) {
     const double tn = (s - 1.0) / (double)c;
     double s2;
     int c2;
-    list_sum_count(cl, n, rd32(tn), lane, s2, c2);
-    if (c2 == c || !(tn > t)) {
+    reg_sum_count<E>(x, rd32(tn), s2, c2);
+    if (c2 == c || !(tn > tt)) {
       tau = tn;
       kappa = c2;
       conv = true;
       break;
     }
-    t = tn;
+    tt = tn;
     s = s2;
     c = c2;
   }
@@ -230,13 +278,13 @@ __device__ __forceinline__ void solve_many(float lm, float t0, float m, int lane
       const float v = fkey_inv(km);
       double s3;
       int c3;
-      list_sum_count(cl, n, v, lane, s3, c3);
+      reg_sum_count<E>(x, v, s3, c3);
       if (s3 - (double)c3 * (double)v >= 1.0) ka = km;
       else kb = km;
     }
     double s3;
     int c3;
-    list_sum_count(cl, n, fkey_inv(ka), lane, s3, c3);
+    reg_sum_count<E>(x, fkey_inv(ka), s3, c3);
     kappa = c3;
     tau = c3 > 0 ? (s3 - 1.0) / (double)c3 : NAN;
   }
@@ -244,7 +292,7 @@ __device__ __forceinline__ void solve_many(float lm, float t0, float m, int lane
   if (tc != tau) {
     double s3;
     tau = tc;
-    list_sum_count(cl, n, rd32(tau), lane, s3, kappa);
+    reg_sum_count<E>(x, rd32(tau), s3, kappa);
   }
 }
 
@@ -309,7 +357,7 @@ __device__ __forceinline__ RowResult process_row(int64_t r, rsrc_t next, int64_t
   int kappa;
   uint64_t support;
   if (n <= kWave) resolve_list(cl, n, t0, m, lane, tau, kappa, support);
-  else solve_many<MODE>(lm, t0, m, lane, cl, ci_lds, n, tau, kappa, support);
+  else solve_many<T, MODE, E, V4>(x, lm, t0, m, lane, cl, ci_lds, n, tau, kappa, support);
   const float Hf = rd32(tau);
   __builtin_amdgcn_wave_barrier();
 
@@ -2594,7 +2642,7 @@ __global__ __launch_bounds__(kBlock) void fwl_fill_zero(void* __restrict__ dst, 
   __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, r, 16u * threadIdx.x, 0, 0);
 }
 
-template <typename T>
+template <typename T, bool V4>
 __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
     const void* __restrict__ z, int64_t ld, const int64_t* __restrict__ tgt, const float* __restrict__ Hin,
     const int32_t* __restrict__ kap_in, const int32_t* __restrict__ cidx, int64_t N, int C, double scale,
@@ -2616,9 +2664,11 @@ __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
         if (id != yr) store_elem<T>(grad, g0 + id, inv);
       }
     } else {
-      // a support longer than the list: its entries from the logits (the fill wrote the zeros)
-      for (int j = lane; j < C; j += kWave)
-        if (j != yr && load_elem<T>(row, j) > Hf) store_elem<T>(grad, g0 + j, inv);
+      // a support longer than the list: its entries from the logits (the fill wrote the zeros),
+      // the row streamed in 128-bit units with two rounds in flight
+      row_pass<1, T, V4, true>(row, C, lane, 0, [&](float zj, int j) {
+        if (zj > Hf && j != yr) store_elem<T>(grad, g0 + j, inv);
+      });
     }
     if (lane == 0) {
       if (yr >= 0) store_elem<T>(grad, g0 + yr, (load_elem<T>(row, yr) > Hf ? inv : 0.0f) - scale_f);
@@ -2929,7 +2979,7 @@ int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Out
   const int64_t bytes = N * (int64_t)C * kElemBytes<T>;
   const int64_t fill_blocks = (bytes + kFillBytes - 1) / kFillBytes;
   hipLaunchKernelGGL(fwl_fill_zero, dim3((unsigned)fill_blocks), dim3(kBlock), 0, s, o.grad, bytes);
-  hipLaunchKernelGGL((fwl_scatter_support<T>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, o.ld, y, o1.H, o1.ccnt,
+  hipLaunchKernelGGL((fwl_scatter_support<T, V4>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, o.ld, y, o1.H, o1.ccnt,
                      o1.cidx, N, C, o.scale, o.scale_f, o.grad, (bytes & 3) != 0);
   return grid;
 }
@@ -3199,6 +3249,36 @@ int fused_forward(int dtype, const void* logits, int64_t ld, const int64_t* targ
 }  // namespace
 
 // ------------------------------------------------------------------------------------------------
+// The workspace of fwl_forward_backward_noalloc: one array per device, in the code object, so that
+// the entry point allocates nothing.  In host code `scratch` is only a host-side stand-in for the
+// symbol; its device address (one per device) comes from hipGetSymbolAddress and is the only
+// address passed to kernels.  The library keeps no state in a workspace between calls, so nothing
+// in it needs clearing; calls that overlap on one device share it and race.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// the device address of `scratch` on the current device (looked up once per device)
+int scratch_address(void** out) {
+  static std::mutex mu;
+  static std::map<int, void*> addr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return FWL_ERR_DEVICE;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = addr.find(dev);
+  if (it == addr.end()) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return FWL_ERR_DEVICE;
+    it = addr.emplace(dev, ptr).first;
+  }
+  *out = it->second;
+  return FWL_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------
 // C ABI
 
 extern "C" {
@@ -3231,6 +3311,24 @@ int fwl_forward_backward_ex(int dtype, const void* logits, int64_t ld, const int
   if (!call_params(options, p)) return FWL_ERR_INVALID_ARG;
   return fused_forward(dtype, logits, ld, targets, N, C, scale, reduce_div, H, losses, losses64, mean_loss, kappa,
                        grad, workspace, workspace_bytes, p, stream);
+}
+
+size_t fwl_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+int fwl_forward_backward_noalloc(int dtype, const void* logits, int64_t ld, const int64_t* targets, int64_t N,
+                                 int64_t C, double scale, double reduce_div, float* H, float* losses,
+                                 double* losses64, float* mean_loss, int32_t* kappa, void* grad,
+                                 const fwl_options* options, hipStream_t stream) {
+  Params p;
+  if (!call_params(options, p)) return FWL_ERR_INVALID_ARG;
+  if (bad_shape(N, C)) return FWL_ERR_INVALID_ARG;
+  // every part of the workspace this call would use must fit the static scratch
+  if (workspace_bytes(N, C, p.path) > kNoAllocScratchBytes) return FWL_ERR_WORKSPACE;
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != FWL_OK) return rc;
+  return fused_forward(dtype, logits, ld, targets, N, C, scale, reduce_div, H, losses, losses64, mean_loss, kappa,
+                       grad, ws, kNoAllocScratchBytes, p, stream);
 }
 
 int fwl_forward_backward(const float* logits, const int64_t* targets, int64_t N, int64_t C,

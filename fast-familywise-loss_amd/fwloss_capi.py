@@ -23,6 +23,9 @@ SIGNATURES = {
     "fwl_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "fwl_workspace_bytes": ([_I64, _I64], ctypes.c_size_t),
     "fwl_workspace_bytes_ex": ([_I64, _I64, _P], ctypes.c_size_t),
+    "fwl_noalloc_scratch_bytes": ([], ctypes.c_size_t),
+    "fwl_forward_backward_noalloc": ([ctypes.c_int, _P, _I64, _P, _I64, _I64, _D, _D, _P, _P, _P, _P, _P, _P, _P, _P],
+                                     ctypes.c_int),
     "fwl_forward_backward_ex": ([ctypes.c_int, _P, _I64, _P, _I64, _I64, _D, _D, _P, _P, _P, _P, _P, _P, _P,
                                  ctypes.c_size_t, _P, _P], ctypes.c_int),
     "fwl_forward_backward": ([_P, _P, _I64, _I64, _D, _D, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P], ctypes.c_int),

@@ -124,6 +124,23 @@ int fwl_forward_backward_ex(int dtype, const void* logits, int64_t ld, const int
                             void* workspace, size_t workspace_bytes, const fwl_options* options,
                             hipStream_t stream);
 
+/* fwl_forward_backward_ex without the workspace arguments: it allocates nothing and takes no
+ * workspace, for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  No counterpart in the reference, whose ops
+ * allocate their outputs and scratch (src/cuda/fw_radix_argmax.cu:1390-1393, :1426-1453).  The
+ * caller passes the inputs and outputs; the workspace is a static device array of
+ * fwl_noalloc_scratch_bytes() bytes (16 MiB) in the library, one per device, looked up once per
+ * device.  Calls on one device share it: calls that overlap on one device (several streams or
+ * threads at once) race and give undefined results.  A call whose workspace (fwl_workspace_bytes_ex
+ * with the same options) exceeds the array returns FWL_ERR_WORKSPACE before any launch: the mean
+ * and overflow records need about 8 bytes per row, many long rows 520 more (about 2M rows of short
+ * rows, or 30000 rows of >= 32000 elements). */
+size_t fwl_noalloc_scratch_bytes(void);
+int fwl_forward_backward_noalloc(int dtype, const void* logits, int64_t ld, const int64_t* targets,
+                                 int64_t N, int64_t C, double scale, double reduce_div, float* H,
+                                 float* losses, double* losses64, float* mean_loss, int32_t* kappa,
+                                 void* grad, const fwl_options* options, hipStream_t stream);
+
 /* fwl_forward_backward for float64 logits (the reference CPU path's second dtype,
  * src/cpu/fw_cpu.cpp:697-703, run_generic<double>; the reference GPU ops take float32 only).
  * Every decision is taken in fp64: tau from fixed-point iterations t <- H({z > t}) with sums in a
