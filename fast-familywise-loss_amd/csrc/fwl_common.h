@@ -26,6 +26,7 @@ namespace {
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 // Raw buffer resources (GFX9 layout): the hardware range check drops stores and zero-fills loads
@@ -479,9 +480,10 @@ __device__ __forceinline__ float safe_lower(double s, int c, float B) {
   return isfinite(r) ? prev_f32(r) : -INFINITY;
 }
 
-// safe_lower for a sum s accumulated partly in fp32 (per-lane partial sums of up to 16 values of
-// magnitude <= B, rounded at most 16 times each, then added in fp64): the rounding of each term's
-// contribution is below B*2^-19, so the bound moves down by B*2^-19 more.
+// safe_lower for a sum s accumulated partly in fp32: per-lane partial sums of at most 63 values of
+// magnitude <= B each, then added in fp64.  Adding the j-th value rounds by at most j*B*2^-24, so
+// a lane of k values is off by at most k(k+1)/2 * B*2^-24, and the error of the sum divided by the
+// number c of values is at most (k_max + 1)/2 * B*2^-24 <= B*2^-19: the bound moves down by that.
 __device__ __forceinline__ float safe_lower32(double s, int c, float B) {
   if (c <= 0) return -INFINITY;
   const double h = (s - 1.0) / (double)c - (double)B * 0x1p-19;
@@ -542,13 +544,84 @@ __device__ __forceinline__ void list_sum_count(const float* bv, int n, float thr
   c = cnt;
 }
 
+// Padded lists: storage of a whole number of 4*64-entry groups, 16-byte aligned.  pad_list sets
+// the entries [n, n rounded up to 256) to -inf, after which a pass reads four entries per lane
+// with one 128-bit LDS load and needs no bound check (-inf is above no threshold).
+__device__ __forceinline__ void pad_list(float* bv, int n, int lane) {
+  const int end = (n + 4 * kWave - 1) & ~(4 * kWave - 1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int q = n + lane + kWave * j;
+    if (q < end) bv[q] = -INFINITY;
+  }
+}
+
+// this lane's sum (in A: float for bounds, at most n/64 terms; double for exact steps) and count
+// of the entries > thr of a padded list [0, n)
+template <typename A>
+__device__ __forceinline__ void list4_lane(const float* bv, int n, float thr, int lane, A& acc, int& cnt) {
+  acc = (A)0;
+  cnt = 0;
+#pragma unroll 2
+  for (int p0 = 0; p0 < n; p0 += 4 * kWave) {
+    const v4f v = *reinterpret_cast<const v4f*>(bv + p0 + 4 * lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool k = v[j] > thr;
+      acc += k ? (A)v[j] : (A)0;
+      cnt += k ? 1 : 0;
+    }
+  }
+}
+
+// list_sum_count over a padded list, fp64
+__device__ __forceinline__ void list4_sum_count(const float* bv, int n, float thr, int lane, double& s, int& c) {
+  double acc;
+  int cnt;
+  list4_lane<double>(bv, n, thr, lane, acc, cnt);
+  s = wave_sum_f64(acc);
+  c = wave_sum_i32(cnt);
+}
+
+// keep the entries > t of a padded list [0, n) in place (and their indices, unless noidx; bi is
+// then padded storage too); returns the number kept.  The order of the entries changes.
+__device__ __forceinline__ int list4_compact(float* bv, int* bi, int n, float t, bool noidx, int lane) {
+  int w = 0;
+  for (int p0 = 0; p0 < n; p0 += 4 * kWave) {
+    const int p = p0 + 4 * lane;
+    const v4f v = *reinterpret_cast<const v4f*>(bv + p);
+    v4i id = {-1, -1, -1, -1};
+    if (!noidx) id = *reinterpret_cast<const v4i*>(bi + p);
+    // every write below lands below p0 + 256: on entries this group has already read
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool keep = v[j] > t;
+      const uint64_t b = ballot(keep);
+      if (keep) {
+        const int pos = w + rank_in(b);
+        bv[pos] = v[j];
+        if (!noidx) bi[pos] = id[j];
+      }
+      w += __popcll(b);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  return w;
+}
+
 // tau, kappa and (for n <= 64) the support bits of a candidate list cl[0, n) that holds every row
 // entry > t0 (t0 <= tau, e.g. the largest float <= max - 1) and whose largest entry is the row
 // maximum m.  Up to 64 entries: one per lane, sorted across the wavefront, fp64 prefix sums,
 // tau = max_k (S_k - 1)/k.  Longer lists: fixed-point iterations t <- H({z > t}) from t0 (each
 // iterate is <= tau and the set shrinks every step until it is {z > tau}).
+// (PAD: cl is a padded list, see pad_list, whose passes use 128-bit loads)
+template <bool PAD = false>
 __device__ __forceinline__ void resolve_list(const float* cl, int n, float t0, float m, int lane, double& tau,
                                              int& kappa, uint64_t& support) {
+  auto sum_count = [&](float thr, double& s, int& c) {
+    if constexpr (PAD) list4_sum_count(cl, n, thr, lane, s, c);
+    else list_sum_count(cl, n, thr, lane, s, c);
+  };
   tau = NAN;
   kappa = 0;
   support = 0;
@@ -560,12 +633,12 @@ __device__ __forceinline__ void resolve_list(const float* cl, int n, float t0, f
   } else if (n > kWave) {
     double t = (double)t0, s;
     int c;
-    list_sum_count(cl, n, t0, lane, s, c);
+    sum_count(t0, s, c);
     for (int it = 0; it <= n + 1; ++it) {
       const double tn = (s - 1.0) / (double)c;
       double s2;
       int c2;
-      list_sum_count(cl, n, rd32(tn), lane, s2, c2);
+      sum_count(rd32(tn), s2, c2);
       if (c2 == c || !(tn > t)) {
         tau = tn;
         kappa = c2;
@@ -579,7 +652,7 @@ __device__ __forceinline__ void resolve_list(const float* cl, int n, float t0, f
     if (tc != tau) {
       double s3;
       tau = tc;
-      list_sum_count(cl, n, rd32(tau), lane, s3, kappa);
+      sum_count(rd32(tau), s3, kappa);
     }
   }
 }

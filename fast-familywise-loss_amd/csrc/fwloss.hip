@@ -948,13 +948,12 @@ __global__ __launch_bounds__(kBlock) void fwl_seg_rows(const void* __restrict__ 
 // fwl_block_rows: one block per row, streaming with LDS candidate lists
 
 constexpr int kHistBlock = 1024;    // bins of a block's histogram (select_in_memory, W = 4)
-constexpr int kHistWave = 256;      // bins of a wavefront's histogram (W = 1)
 constexpr int kTightenSteps = 12;   // fixed-point steps per tightening of a candidate list
 
 // LDS of the block kernels.  While a row streams, each wavefront keeps its candidate list (value,
 // index) in bval/bidx; the overflow solve (select_in_memory) reuses the same bytes, first as a
 // histogram, then as one list of values.
-struct BlockShared {
+struct alignas(16) BlockShared {
   union {
     struct {
       float bval[kWavesPerBlock][kCapMax];
@@ -982,22 +981,16 @@ struct BlockShared {
 static_assert(sizeof(unsigned) * kHistBlock + sizeof(double) * kHistBlock <= 8 * kWavesPerBlock * kCapMax,
               "the histogram reuses the candidate lists");
 
-// the same for one wavefront of fwl_wave_stream_rows
-struct WaveShared {
-  union {
-    struct {
-      float val[kCapMax];
-      int idx[kCapMax];
-    };
-    struct {
-      unsigned hcnt[kHistWave];
-      double hsum[kHistWave];
-    };
-    float list[2 * kCapMax];
-  };
+// The list of one wavefront of fwl_wave_stream_rows: up to kWaveVCap candidate values, the first
+// kCapMax of them with their indices.  A row whose list outgrows the indices keeps its values (tau
+// comes from them) and writes its support from one more pass over the row: rows of low-variance
+// logits (hundreds to thousands of support entries) then need no overflow solve.  56 KB of LDS
+// per block: the kernel runs two blocks per CU.
+constexpr int kWaveVCap = 3072;
+struct alignas(16) WaveShared {
+  float val[kWaveVCap];
+  int idx[kCapMax];
 };
-static_assert(sizeof(unsigned) * kHistWave + sizeof(double) * kHistWave <= 8 * kCapMax,
-              "the histogram reuses the candidate list");
 
 // Streaming rounds.  A row is shared by W wavefronts (W = 4: one block per row; W = 1: one
 // wavefront per row).  In round `round`, access group u of a lane covers unit
@@ -1053,6 +1046,7 @@ __device__ __forceinline__ void zero_round(rsrc_t out, int round, int wid, int l
 // One wavefront's state while a row (or a stretch of one) streams.
 struct StreamState {
   int n;          // entries in the wavefront's list: every entry seen so far that is > t
+  bool noidx;     // the list outgrew its indices: values only from then on
   float m;        // running maximum
   float t;        // running lower bound on tau
   bool ovf;       // the list could not hold the entries > t; from then on the scan only sums
@@ -1064,6 +1058,7 @@ struct StreamState {
 __device__ __forceinline__ StreamState stream_state(bool force) {
   StreamState st;
   st.n = 0;
+  st.noidx = false;
   st.m = -INFINITY;
   st.t = -INFINITY;
   st.ovf = force;   // forced: no list, only the sums (the overflow solve's path for every row)
@@ -1076,47 +1071,34 @@ __device__ __forceinline__ StreamState stream_state(bool force) {
 // Raise the wavefront's lower bound t with fixed-point steps t <- H({entries > t}) over its list
 // and the round held in registers (a subset of the row, so H of it is <= tau), then drop the list
 // entries <= t (not in the support: their output stays the zero written while streaming).
+// The list (bv, and bi unless noidx) is padded storage (pad_list): at most 64 entries per lane,
+// so its fp32 partial sums stay within what safe_lower32 allows.
 template <int S>
-__device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, const float* x, float m, int lane) {
+__device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, const float* x, float m, bool noidx,
+                                       int lane) {
   const float B = fmaxf(fabsf(m), fabsf(t));
+  pad_list(bv, n, lane);
   float tf = t;
   for (int it = 0; it < kTightenSteps; ++it) {
-    double s;
-    int c;
-    list_sum_count(bv, n, tf, lane, s, c);
-    // the round's entries: per-lane fp32 partial sums (a bound needs no exact sum)
+    // per-lane fp32 partial sums of the list and of the round (a bound needs no exact sum)
+    float ls;
+    int lc;
+    list4_lane<float>(bv, n, tf, lane, ls, lc);
     float rs = 0.0f;
-    int rc = 0;
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const bool k = x[i] > tf;
       rs += k ? x[i] : 0.0f;
-      rc += k ? 1 : 0;
+      lc += k ? 1 : 0;
     }
-    s += wave_sum_f64((double)rs);
-    c += wave_sum_i32(rc);
+    const double s = wave_sum_f64((double)ls + (double)rs);
+    const int c = wave_sum_i32(lc);
     const float nt = safe_lower32(s, c, B);
     if (!(nt > tf)) break;
     tf = nt;
   }
   t = fmaxf(t, tf);
-  int w = 0;
-  for (int p0 = 0; p0 < n; p0 += kWave) {
-    const int p = p0 + lane;
-    const float v = p < n ? bv[p] : -INFINITY;
-    const int id = p < n ? bi[p] : -1;
-    const bool keep = v > t;
-    const uint64_t b = ballot(keep);
-    __builtin_amdgcn_wave_barrier();
-    if (keep) {
-      const int pos = w + rank_in(b);
-      bv[pos] = v;
-      bi[pos] = id;
-    }
-    w += __popcll(b);
-    __builtin_amdgcn_wave_barrier();
-  }
-  n = w;
+  n = list4_compact(bv, bi, n, t, noidx, lane);
 }
 
 // Candidates of one round: the running maximum m gives the bound t (>= m - 1 rounded down), and
@@ -1124,9 +1106,10 @@ __device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, co
 // first used to tighten t; if they still do not fit, the list is abandoned: from then on the
 // entries above the bound of that moment (tov) are only summed (their H is a lower bound on tau
 // for the overflow solve).
+// (cap: the list's capacity in values; icap <= cap: entries that keep their indices)
 template <int W, typename T, bool VEC>
 __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, int wid, int lane, float* bv,
-                                           int* bi, int cap, StreamState& st) {
+                                           int* bi, int cap, int icap, StreamState& st) {
   constexpr int S = Round<T, VEC>::kSlots;
   constexpr int kRoundElems = kUnit<T, VEC> * kWave * W * Round<T, VEC>::kPer;
   float lm = -INFINITY;
@@ -1149,8 +1132,9 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
     int cnt = 0;
 #pragma unroll
     for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > st.t));
-    if (st.n + cnt > cap) {
-      tighten<S>(bv, bi, st.n, st.t, a.x, st.m, lane);
+    // a list that still has its indices is tightened before it gives them up
+    if (st.n + cnt > (st.noidx ? cap : icap)) {
+      tighten<S>(bv, bi, st.n, st.t, a.x, st.m, st.noidx, lane);
       cnt = 0;
 #pragma unroll
       for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > st.t));
@@ -1168,6 +1152,7 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
       }
     }
     if (!st.ovf) {
+      if (st.n + cnt > icap) st.noidx = true;
 #pragma unroll
       for (int i = 0; i < S; ++i) {
         const bool p = a.x[i] > st.t;
@@ -1175,7 +1160,7 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
         if (p) {
           const int pos = st.n + rank_in(b);
           bv[pos] = a.x[i];
-          bi[pos] = round_slot_index<W, T, VEC>(round, i, wid, lane);
+          if (!st.noidx) bi[pos] = round_slot_index<W, T, VEC>(round, i, wid, lane);
         }
         st.n += __popcll(b);
       }
@@ -1206,7 +1191,8 @@ __device__ __forceinline__ void stream_first(const void* __restrict__ row, int C
 // the first round, from stream_first.
 template <int W, typename T, int MODE, bool VEC>
 __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* out_row, int C, int lane, int wid,
-                                            float* bv, int* bi, int cap, StreamState& st, Round<T, VEC>& a) {
+                                            float* bv, int* bi, int cap, int icap, StreamState& st,
+                                            Round<T, VEC>& a) {
   constexpr int per_round = kWave * W * Round<T, VEC>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
@@ -1224,11 +1210,11 @@ __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* 
   while (true) {
     load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
-    scan_round<W, T, VEC>(a, k, C, wid, lane, bv, bi, cap, st);
+    scan_round<W, T, VEC>(a, k, C, wid, lane, bv, bi, cap, icap, st);
     if (++k >= rounds) break;
     load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
-    scan_round<W, T, VEC>(b, k, C, wid, lane, bv, bi, cap, st);
+    scan_round<W, T, VEC>(b, k, C, wid, lane, bv, bi, cap, icap, st);
     if (++k >= rounds) break;
   }
 }
@@ -1881,7 +1867,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, o.cap, st, first);
+    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, o.cap, o.cap, st, first);
     if (lane == 0) {
       sh.wmax[wid] = st.m;
       sh.wn[wid] = st.n;
@@ -2020,6 +2006,9 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
   float* bv = s_w[wid].val;
   int* bi = s_w[wid].idx;
   const SelMem sm = {nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr};
+  // the default capacity takes the whole value list; a smaller one (fwl_options) shrinks both
+  const int vcap = o.cap >= kCapMax ? kWaveVCap : o.cap;
+  const int icap = o.cap < kCapMax ? o.cap : kCapMax;
   const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
   float my_H = 0.0f, my_loss = 0.0f;
   double my_l64 = 0.0;
@@ -2042,7 +2031,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-    stream_span<1, T, MODE, V4>(row, out_row, C, lane, 0, bv, bi, o.cap, st, first);
+    stream_span<1, T, MODE, V4>(row, out_row, C, lane, 0, bv, bi, vcap, icap, st, first);
     if (k + 1 < nrows) stream_first<1, T, V4>(row_at(k + 1), C, lane, 0, first);
     double tau;
     int kappa;
@@ -2050,23 +2039,11 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     if (!st.ovf) {
       // keep the entries above the final bound (every support entry is among them)
       const float tb = bound_below_max(st.m);
-      int kept = 0;
-      for (int p0 = 0; p0 < st.n; p0 += kWave) {
-        const int p = p0 + lane;
-        const float v = p < st.n ? bv[p] : -INFINITY;
-        const int id = p < st.n ? bi[p] : -1;
-        const bool keep = v > tb;
-        const uint64_t b = ballot(keep);
-        __builtin_amdgcn_wave_barrier();
-        if (keep) {
-          bv[kept + rank_in(b)] = v;
-          bi[kept + rank_in(b)] = id;
-        }
-        kept += __popcll(b);
-        __builtin_amdgcn_wave_barrier();
-      }
-      st.n = kept;
-      resolve_list(bv, st.n, tb, st.m, lane, tau, kappa, support);
+      pad_list(bv, st.n, lane);
+      st.n = list4_compact(bv, bi, st.n, tb, st.noidx, lane);
+      pad_list(bv, st.n, lane);
+      // every list entry is > st.t (<= tau): the fixed-point steps of a long list start there
+      resolve_list<true>(bv, st.n, fmaxf(tb, st.t), st.m, lane, tau, kappa, support);
     } else {
       double ls;
       int lc;
@@ -2090,7 +2067,11 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     const float inv = (float)(o.scale / (double)kappa);
     // this wavefront's zero placeholders have landed before any entry is rewritten
     wait_vmem();
-    if (!st.ovf) {
+    if (st.noidx && !st.ovf) {
+      // the list kept values only: the support from one more pass over the row (candidate lists
+      // cut at ccap leave a longer support to fwl_scatter_support, which reads the row itself)
+      if (MODE != kCand || kappa <= o.ccap) write_support<1, T, MODE, V4, true>(row, r, C, yr, Hf, inv, o, nullptr, lane, 0);
+    } else if (!st.ovf) {
       if constexpr (MODE == kGrad || MODE == kMask) {
         for (int p = lane; p < st.n; p += kWave) {
           const int id = bi[p];
@@ -2248,7 +2229,7 @@ __global__ __launch_bounds__(kBlock) void fwl_split_chunks(const void* __restric
     StreamState st = stream_state(o.force_generic != 0);
     Round<T, V4> first;
     stream_first<kWavesPerBlock, T, V4>(span, len, lane, wid, first);
-    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, st, first);
+    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, o.cap, st, first);
     if (lane == 0) {
       sh.wmax[wid] = st.m;
       sh.wn[wid] = st.n;
@@ -2632,21 +2613,43 @@ __global__ __launch_bounds__(kBlock) void fwl_cand_to_grad(
 constexpr int kTwoPassCap = 64;          // support entries kept per row between the passes
 constexpr int kFillBytes = 4096;         // bytes per block of the fill
 
-__global__ __launch_bounds__(kBlock) void fwl_fill_zero(void* __restrict__ dst, int64_t bytes) {
+// kap (optional): per row its kappa; rows whose kappa exceeds `cap` are left alone (the scatter
+// writes them whole).  Needs rows of a whole number of dwords and of >= kFillBytes bytes, so that a
+// block's bytes lie in at most two rows and no dword straddles two rows.
+__global__ __launch_bounds__(kBlock) void fwl_fill_zero(void* __restrict__ dst, int64_t bytes, int64_t row_bytes,
+                                                         const int32_t* __restrict__ kap, int cap) {
   const int64_t b0 = (int64_t)blockIdx.x * kFillBytes;
   const int64_t left = bytes - b0;
   const rsrc_t r = make_rsrc(static_cast<char*>(dst) + b0, (uint32_t)(left < kFillBytes ? left : kFillBytes));
+  const uint32_t off = 16u * threadIdx.x;
+  if (kap != nullptr) {
+    // the block's first row and where the next one starts (block-uniform)
+    const int64_t ra = b0 / row_bytes;
+    const int64_t next = (ra + 1) * row_bytes - b0;   // bytes into the block
+    const bool fa = kap[ra] <= cap;
+    const bool fb = next < kFillBytes && next < left ? kap[ra + 1] <= cap : fa;
+    if (!fa && !fb) return;
+    if (!(fa && fb)) {
+      // dwords of the rows to fill only
+#pragma unroll
+      for (uint32_t d = 0; d < 4; ++d) {
+        const uint32_t o4 = off + 4u * d;
+        if ((int64_t)o4 < next ? fa : fb) __builtin_amdgcn_raw_buffer_store_b32(0u, r, o4, 0, 0);
+      }
+      return;
+    }
+  }
   // 16 bytes per thread; the range check drops what lies past the end (per dword; the caller
   // pads nothing, so a gradient whose size is not a multiple of 4 bytes gets its last 2 bytes
   // from fwl_scatter_support)
-  __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, r, 16u * threadIdx.x, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, r, off, 0, 0);
 }
 
 template <typename T, bool V4>
 __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
     const void* __restrict__ z, int64_t ld, const int64_t* __restrict__ tgt, const float* __restrict__ Hin,
     const int32_t* __restrict__ kap_in, const int32_t* __restrict__ cidx, int64_t N, int C, double scale,
-    float scale_f, void* __restrict__ grad, bool odd_tail) {
+    float scale_f, void* __restrict__ grad, bool odd_tail, bool dense) {
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
@@ -2663,6 +2666,36 @@ __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
         const int id = cidx[r * (int64_t)kTwoPassCap + lane];
         if (id != yr) store_elem<T>(grad, g0 + id, inv);
       }
+    } else if (dense) {
+      // a support longer than the list, on a row the fill left alone: the whole row from the
+      // logits (z > H ? inv : 0) in 128-bit units, each line written once, two rounds in flight
+      constexpr int PER = Round<T, V4>::kPer;
+      constexpr int U = kUnit<T, V4>;
+      constexpr int per_round = kWave * Round<T, V4>::kSlots;
+      const int rounds = (C + per_round - 1) / per_round;
+      const rsrc_t in = make_rsrc(row, (uint32_t)(kElemBytes<T> * C));
+      const rsrc_t none = make_rsrc(row, 0u);
+      const rsrc_t out = make_rsrc(static_cast<char*>(grad) + g0 * kElemBytes<T>, (uint32_t)(kElemBytes<T> * C));
+      const uint32_t b_inv = encode<T>(inv);
+      auto emit = [&](const Round<T, V4>& a, int k) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          uint32_t bits[U];
+#pragma unroll
+          for (int e = 0; e < U; ++e) bits[e] = a.x[U * u + e] > Hf ? b_inv : 0u;
+          store_unit_bits<T, V4>(out, (uint32_t)lane_unit<1, PER>(k, u, 0, lane), bits);
+        }
+      };
+      Round<T, V4> a, b;
+      load_round<1, T, V4>(in, 0, 0, lane, a);
+      for (int k = 0; k < rounds; k += 2) {
+        load_round<1, T, V4>(k + 1 < rounds ? in : none, k + 1, 0, lane, b);
+        emit(a, k);
+        if (k + 1 >= rounds) break;
+        load_round<1, T, V4>(k + 2 < rounds ? in : none, k + 2, 0, lane, a);
+        emit(b, k + 1);
+      }
+      wait_vmem();   // the label element below is stored over its value here
     } else {
       // a support longer than the list: its entries from the logits (the fill wrote the zeros),
       // the row streamed in 128-bit units with two rounds in flight
@@ -2978,9 +3011,14 @@ int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Out
   else grid = launch_block<T, kCand, V4>(z, y, N, C, o1, s);
   const int64_t bytes = N * (int64_t)C * kElemBytes<T>;
   const int64_t fill_blocks = (bytes + kFillBytes - 1) / kFillBytes;
-  hipLaunchKernelGGL(fwl_fill_zero, dim3((unsigned)fill_blocks), dim3(kBlock), 0, s, o.grad, bytes);
+  // rows whose support outgrew the lists are written whole by the scatter kernel, and the fill
+  // leaves them alone, where rows are whole dwords and at least a fill block long
+  const int64_t row_bytes = (int64_t)C * kElemBytes<T>;
+  const bool dense = row_bytes % 4 == 0 && row_bytes >= kFillBytes;
+  hipLaunchKernelGGL(fwl_fill_zero, dim3((unsigned)fill_blocks), dim3(kBlock), 0, s, o.grad, bytes, row_bytes,
+                     dense ? o1.ccnt : nullptr, kTwoPassCap);
   hipLaunchKernelGGL((fwl_scatter_support<T, V4>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, o.ld, y, o1.H, o1.ccnt,
-                     o1.cidx, N, C, o.scale, o.scale_f, o.grad, (bytes & 3) != 0);
+                     o1.cidx, N, C, o.scale, o.scale_f, o.grad, (bytes & 3) != 0, dense);
   return grid;
 }
 
