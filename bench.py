@@ -9,8 +9,10 @@ rotated between steps so the 256 MB Infinity Cache cannot hold a step's data fro
 
 Prints one JSON line.  ``roofline.achieved`` = algorithmic bytes per launch (read logits once,
 write the gradient once, read labels, write H/loss/kappa: 8*N*C + 20*N bytes) / the mean duration
-of a launch, measured with one HIP event pair around the timed region on the stream the kernels run
-on (region GPU time / K).  ``roofline.traffic`` is the
+of the op's row kernels, measured with one HIP event pair on their stream around K more launches of
+the same op through the C ABI without the mean (whose one-block finishing kernel, about 2-5 us, the
+timed steps add after the row kernels; region GPU time / K).  ``kernel_ms`` is the same for the
+timed steps themselves.  ``roofline.traffic`` is the
 HBM bytes per launch measured with rocprofv3 counters (profiles/<kernel>_<config>.md), or null.
 ``cpu_baseline`` times the reference's own CPU path (compiled into oracle/_ref) on this host's cores,
 on the same host-generated inputs, as loss + full gradient per call (benchmarks/cpu_benchmarks/
@@ -242,6 +244,44 @@ def bench_linear(args):
     }), flush=True)
 
 
+def row_kernels_ms(sets, N, C, tdt, steps, stream):
+    """Mean GPU time of the fused op's row kernels alone: K launches through the C ABI
+    (fwl_forward_backward_ex) on the same rotated inputs with no mean requested, so that the op
+    launches no finishing kernel; one HIP event pair around them on `stream`.  None for float64
+    (another entry point)."""
+    import torch
+    import fwloss_capi as capi
+    if tdt not in capi.DTYPES:
+        return None
+    dev = sets[0][0].device
+    ws = capi.Workspace(dev)
+    buf = ws.get(N, C)
+    outs = [dict(H=torch.empty(N, device=dev), loss=torch.empty(N, device=dev),
+                 kappa=torch.empty(N, dtype=torch.int32, device=dev),
+                 grad=torch.empty((N, C), dtype=tdt, device=dev)) for _ in sets]
+    P = capi._ptr
+    s = capi.ctypes.c_void_p(stream.cuda_stream)
+
+    def launch(i):
+        zt, yt = sets[i % len(sets)]
+        o = outs[i % len(sets)]
+        rc = capi.lib().fwl_forward_backward_ex(capi.DTYPES[tdt], P(zt), C, P(yt), N, C, 1.0 / N, float(N), P(o["H"]),
+                                                P(o["loss"]), None, None, P(o["kappa"]), P(o["grad"]), P(buf),
+                                                buf.numel(), None, s)
+        if rc != 0:
+            raise RuntimeError(f"fwl_forward_backward_ex returned {rc}")
+    for i in range(min(steps, 20)):
+        launch(i)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for i in range(steps):
+        launch(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps
+
+
 def main():
     args = parse()
     if args.op == "linear":
@@ -310,7 +350,8 @@ def main():
     kern_ms = ev0.elapsed_time(ev1) / args.steps
     ms_per_step = wall * 1e3 / args.steps
     nbytes = alg_bytes(N, C, ELEM_BYTES[args.dtype])
-    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    row_ms = row_kernels_ms(sets, N, C, tdt, args.steps, stream)
+    achieved = nbytes / ((kern_ms if row_ms is None else row_ms) * 1e-3) / 1e9
 
     # the reference harness's two-op sequence (fp32 only), for comparison: the small ops below
     # K = 10000, the candidate-list ops above (benchmarks/cuda_benchmarks/CE_FW_perf.py:76-88)
@@ -371,6 +412,7 @@ def main():
         "gbps": nbytes / (ms_per_step * 1e-3) / 1e9,
         "hbm_frac": nbytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "kernel_ms": kern_ms,
+        "row_kernels_ms": row_ms,
         "two_op_ms_per_step": two_op_ms,
         "roofline": {"bound": "hbm", "kernel": tag, "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "alg_bytes": nbytes,
