@@ -194,10 +194,6 @@ struct Outs {
   int cap;             // LDS candidate capacity per wavefront (<= kCapMax)
   int cstride;         // candidate-list mode: row stride of cval/cidx (C for the drop-in op)
   int ccap;            // candidate-list mode: entries kept per row (further ones are dropped)
-  // the two-pass op's read pass (one wavefront per row, candidate-list mode): every row's
-  // candidate bits in memory for the write pass (null: none)
-  uint8_t* gmask;      // [N, gmstride bytes]: per streaming round, S bits per lane
-  int gmstride;
 };
 
 // ------------------------------------------------------------------------------------------------

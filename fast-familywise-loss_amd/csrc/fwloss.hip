@@ -1110,20 +1110,11 @@ __device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, co
 // for the overflow solve).
 // (cap: the list's capacity in values; icap <= cap: entries that keep their indices)
 //
-// GL: the row's candidate bits go to memory (one wavefront per row): per round, S bits per lane,
-// bit i set where slot i held an entry above the bound of that round.  Each bound is <= tau, so
-// every support entry has its bit set, and a later pass over the row need only look at the
-// elements whose bits are set.
-struct GList {
-  rsrc_t mask;    // the row's candidate bits (null resource: none kept)
-};
-
-template <int W, typename T, bool VEC, bool GL>
+template <int W, typename T, bool VEC>
 __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, int wid, int lane, float* bv,
-                                           int* bi, int cap, int icap, StreamState& st, GList& gl) {
+                                           int* bi, int cap, int icap, StreamState& st) {
   constexpr int S = Round<T, VEC>::kSlots;
   constexpr int kRoundElems = kUnit<T, VEC> * kWave * W * Round<T, VEC>::kPer;
-  static_assert(!GL || W == 1, "candidate lists in memory: one wavefront per row");
   float lm = -INFINITY;
   if ((round + 1) * kRoundElems <= C) {
     // a round inside the row: nothing to mask
@@ -1139,7 +1130,6 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
   }
   st.m = fmaxf(st.m, wave_max_f32(lm));
   st.t = fmaxf(st.t, bound_below_max(st.m));
-  uint32_t bits = 0;   // GL: this lane's candidates of the round
   bool done = false;
   if (!st.ovf) {
     if (ballot(lm > st.t) == 0) {
@@ -1178,7 +1168,6 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
             bv[pos] = a.x[i];
             if (!st.noidx) bi[pos] = round_slot_index<W, T, VEC>(round, i, wid, lane);
           }
-          if constexpr (GL) bits |= p ? 1u << i : 0u;
           st.n += __popcll(b);
         }
         done = true;
@@ -1194,17 +1183,10 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
       const bool k = a.x[i] > st.tov;
       rs += k ? a.x[i] : 0.0f;
       st.acc_c += k ? 1 : 0;
-      if constexpr (GL) bits |= k ? 1u << i : 0u;
     }
     st.acc_s += (double)rs;
   }
-  if constexpr (GL) {
-    if constexpr (S == 16) __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bits, gl.mask, 2u * (kWave * round + lane), 0, 0);
-    else __builtin_amdgcn_raw_buffer_store_b32(bits, gl.mask, 4u * (kWave * round + lane), 0, 0);
-  }
 }
-
-__device__ __forceinline__ GList no_glist() { return GList{make_rsrc(nullptr, 0u)}; }
 
 // the first round of a row (or stretch), loaded ahead of stream_span (C = 0: no row, no traffic)
 template <int W, typename T, bool VEC>
@@ -1216,10 +1198,10 @@ __device__ __forceinline__ void stream_first(const void* __restrict__ row, int C
 // to it) once: loads run one round ahead of the candidate scan, and every dense output element
 // (gradient or mask; `out_row` null in candidate-list mode) gets its zero placeholder.  `a` holds
 // the first round, from stream_first.
-template <int W, typename T, int MODE, bool VEC, bool GL = false>
+template <int W, typename T, int MODE, bool VEC>
 __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* out_row, int C, int lane, int wid,
                                             float* bv, int* bi, int cap, int icap, StreamState& st,
-                                            Round<T, VEC>& a, GList& gl) {
+                                            Round<T, VEC>& a) {
   constexpr int per_round = kWave * W * Round<T, VEC>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
@@ -1237,11 +1219,11 @@ __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* 
   while (true) {
     load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
-    scan_round<W, T, VEC, GL>(a, k, C, wid, lane, bv, bi, cap, icap, st, gl);
+    scan_round<W, T, VEC>(a, k, C, wid, lane, bv, bi, cap, icap, st);
     if (++k >= rounds) break;
     load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
-    scan_round<W, T, VEC, GL>(b, k, C, wid, lane, bv, bi, cap, icap, st, gl);
+    scan_round<W, T, VEC>(b, k, C, wid, lane, bv, bi, cap, icap, st);
     if (++k >= rounds) break;
   }
 }
@@ -1894,8 +1876,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-    GList gl = no_glist();
-    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, o.cap, o.cap, st, first, gl);
+    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, o.cap, o.cap, st, first);
     if (lane == 0) {
       sh.wmax[wid] = st.m;
       sh.wn[wid] = st.n;
@@ -2034,7 +2015,6 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
   int* bi = reinterpret_cast<int*>(s_w[wid].val + (kWaveVCap - kCapMax));
   const SelMem sm = {nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr};
   // the default capacity takes the whole value list; a smaller one (fwl_options) shrinks both
-  constexpr bool GL = MODE == kCand;
   const int vcap = o.cap >= kCapMax ? kWaveVCap : o.cap;
   const int icap = o.cap < kCapMax ? o.cap : kCapMax;
   const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
@@ -2056,13 +2036,10 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     const int yr = yok ? (int)y64 : -1;
 
     StreamState st = stream_state(o.force_generic != 0);
-    st.noidx = icap == 0;
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-    GList gl = no_glist();
-    if (GL && o.gmask != nullptr) gl.mask = make_rsrc(o.gmask + r * (int64_t)o.gmstride, (uint32_t)o.gmstride);
-    stream_span<1, T, MODE, V4, GL>(row, out_row, C, lane, 0, bv, bi, vcap, icap, st, first, gl);
+    stream_span<1, T, MODE, V4>(row, out_row, C, lane, 0, bv, bi, vcap, icap, st, first);
     if (k + 1 < nrows) stream_first<1, T, V4>(row_at(k + 1), C, lane, 0, first);
     double tau;
     int kappa;
@@ -2284,8 +2261,7 @@ __global__ __launch_bounds__(kBlock) void fwl_split_chunks(const void* __restric
     StreamState st = stream_state(o.force_generic != 0);
     Round<T, V4> first;
     stream_first<kWavesPerBlock, T, V4>(span, len, lane, wid, first);
-    GList gl = no_glist();
-    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, o.cap, st, first, gl);
+    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, o.cap, st, first);
     if (lane == 0) {
       sh.wmax[wid] = st.m;
       sh.wn[wid] = st.n;
@@ -2776,31 +2752,24 @@ __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
   }
 }
 
-// fwl_write_flat: the first kernel of the two-pass op's write pass when the read pass kept every
-// row's candidate bits (Outs::gmask), for rows of a whole number of 128-bit units.  One block per
-// 4 KB of the [N, C] gradient, one 128-bit unit per thread, stored once.  Measured on MI355X over
-// 1 GiB: zero stores reach 6.85 TB/s in 4 KB blocks of 256 threads (6.80 with a load from a small
-// cached array before them), against 5.5-5.8 TB/s from resident wavefronts looping over items;
-// loading the candidate bits from memory first costs 4.6 TB/s, and loading the logits under them
-// 6.3 TB/s of read and write traffic together.  Hence:
+// fwl_write_flat: the two-pass op's gradient for rows of a whole number of 128-bit units, one
+// block per 4 KB of the [N, C] gradient, one 128-bit unit per thread, stored once:
 //   * rows of at most kTwoPassCap support entries: zeros (fwl_scatter_support then stores the
 //     listed support entries and the label element);
-//   * longer supports: a unit none of whose elements has its bit set (each such element is <= a
-//     lower bound on tau, outside the support) stores zeros without reading the logits; the other
-//     units load their logits and store inv where z > H; the label element gets its scale
-//     subtracted in the same store.
-constexpr int kWriteBytes = 4096;            // gradient bytes per block
-constexpr uint32_t kUnitNone = 0x0FFFFFFFu;  // a unit index whose offset lies past every row
+//   * longer supports: the unit's logits are loaded and inv stored where z > H; the label element
+//     gets its scale subtracted in the same store.
+// Measured on MI355X over 1 GiB: zero stores reach 6.85 TB/s in 4 KB blocks of 256 threads, 6.80
+// with a load from a small cached array before them, against 5.5-5.8 TB/s from resident
+// wavefronts looping over items; stores that first load the logits under them move 6.1 TB/s of
+// read and write traffic together (8 KB and 16 KB blocks: less).  A row's kappa comes through the
+// scalar cache, so a block's only wait on memory before its stores is that of its logits.
+constexpr int kWriteBytes = 4096;   // gradient bytes per block
 
 template <typename T>
 __global__ __launch_bounds__(kBlock) void fwl_write_flat(
     const void* __restrict__ z, int64_t ld, const int64_t* __restrict__ tgt, const float* __restrict__ Hin,
-    const int32_t* __restrict__ kap_in, const uint8_t* __restrict__ gmask, int gmstride, int64_t N, int C,
-    double scale, float scale_f, void* __restrict__ grad) {
+    const int32_t* __restrict__ kap_in, int64_t N, int C, double scale, float scale_f, void* __restrict__ grad) {
   constexpr int U = kUnit<T, true>;
-  constexpr int PER = Round<T, true>::kPer;
-  constexpr int S = Round<T, true>::kSlots;
-  constexpr uint32_t kUnitBits = (1u << U) - 1u;
   const int64_t units = N * (int64_t)(C / U);
   const int64_t u0 = (int64_t)blockIdx.x * (kWriteBytes / 16);   // the block's first unit
   const int64_t ug = u0 + threadIdx.x;
@@ -2811,10 +2780,6 @@ __global__ __launch_bounds__(kBlock) void fwl_write_flat(
   const int du = (int)(ug - rb * upr);
   const int64_t r = rb + du / upr;
   const int q = du % upr;
-  // its candidate bits: round q / (64 PER), access group (q / 64) % PER, lane q % 64
-  const int k = q / (kWave * PER);
-  const int u = (q / kWave) % PER;
-  const int ln = q % kWave;
   // kappa of the block's first two rows through the scalar cache (a block spans at most two rows
   // of >= 4 KB), of others per thread
   const int kap0 = kap_in[rb];
@@ -2825,14 +2790,9 @@ __global__ __launch_bounds__(kBlock) void fwl_write_flat(
     store_zero_unit<T, true>(out, threadIdx.x);
     return;
   }
-  const uint8_t* mrow = gmask + r * (int64_t)gmstride;
-  uint32_t m;
-  if constexpr (S == 16) m = reinterpret_cast<const uint16_t*>(mrow)[kWave * k + ln];
-  else m = reinterpret_cast<const uint32_t*>(mrow)[kWave * k + ln];
-  m = (m >> (U * u)) & kUnitBits;
   float x[U];
   const rsrc_t in = make_rsrc(static_cast<const char*>(z) + r * ld * kElemBytes<T>, (uint32_t)(kElemBytes<T> * C));
-  load_unit<T, true>(in, m ? (uint32_t)q : kUnitNone, x);
+  load_unit<T, true>(in, (uint32_t)q, x);
   const float Hf = Hin[r];
   const int64_t y64 = tgt[r];
   const int yr = (y64 >= 0 && y64 < C) ? (int)y64 : -1;
@@ -2841,7 +2801,7 @@ __global__ __launch_bounds__(kBlock) void fwl_write_flat(
   uint32_t bits[U];
 #pragma unroll
   for (int e = 0; e < U; ++e) {
-    const bool sup = ((m >> e) & 1u) && x[e] > Hf;
+    const bool sup = x[e] > Hf;
     bits[e] = sup ? b_inv : 0u;
     if (U * q + e == yr) bits[e] = encode<T>((sup ? inv : 0.0f) - scale_f);
   }
@@ -3119,18 +3079,12 @@ int launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const 
   return grid + launch_overflow<T, MODE, V4>(z, y, N, C, o, grid, s);
 }
 
-inline size_t ws_round(size_t b) { return (b + kWsAlign - 1) / kWsAlign * kWsAlign; }
 size_t mean_ws_bytes(int64_t N);
 size_t ovf_ws_bytes(int64_t N);
 size_t two_pass_bytes(int64_t N);
-size_t list_bytes(int64_t N, int64_t C);
-bool list_rows(int64_t N);
-int list_mask_stride(int64_t C);
-
-// The fused op in two passes.  With room in the workspace for every row's candidate bits
-// (list_rows): the candidate-list kernel one wavefront per row, keeping the bits, then
-// fwl_write_rows.  Otherwise the candidate-list kernel with its lists cut at kTwoPassCap, then
-// fwl_fill_zero and fwl_scatter_support.  The lists go to the workspace after the mean's part.
+// The fused op in two passes: the candidate-list kernel (lists cut at kTwoPassCap, kept in the
+// workspace after the mean's part), then the write pass: fwl_write_flat and fwl_scatter_support
+// for rows of whole 128-bit units, else fwl_fill_zero and fwl_scatter_support.
 template <typename T, bool V4>
 int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, void* ws, size_t ws_bytes,
                     hipStream_t s) {
@@ -3145,25 +3099,21 @@ int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Out
   o1.ccap = kTwoPassCap;
   if (o1.H == nullptr) o1.H = Hs;
   o1.grad = nullptr;
-  const size_t head = mean_ws_bytes(N) + ovf_ws_bytes(N) + two_pass_bytes(N);
-  const int64_t row_bytes = (int64_t)C * kElemBytes<T>;
-  if (V4 && row_bytes % 16 == 0 && list_rows(N) && ws_bytes >= head + list_bytes(N, C)) {
-    o1.gmstride = list_mask_stride(C);
-    o1.gmask = reinterpret_cast<uint8_t*>(static_cast<char*>(ws) + head);
-    const int grid = launch_wave_stream<T, kCand, V4>(z, y, N, C, o1, s);
-    const int64_t wb = (N * row_bytes + kWriteBytes - 1) / kWriteBytes;
-    hipLaunchKernelGGL((fwl_write_flat<T>), dim3((unsigned)wb), dim3(kBlock), 0, s, z, o.ld, y, o1.H, o1.ccnt,
-                       o1.gmask, o1.gmstride, N, C, o.scale, o.scale_f, o.grad);
-    hipLaunchKernelGGL((fwl_scatter_support<T, V4>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, o.ld, y, o1.H,
-                       o1.ccnt, o1.cidx, N, C, o.scale, o.scale_f, o.grad, false, kLongDone);
-    return grid;
-  }
   // The read pass streams one row per wavefront when there are rows for two wavefronts per SIMD
   // (8192 x 32000: 178 us against 206 us with one block per row; 2048 x 131072: equal), else one
   // row per block (520 x 128256: 181 us with one row per wavefront, 119 us per block).
   int grid;
   if (N >= 2 * 4 * (int64_t)device_cus()) grid = launch_wave_stream<T, kCand, V4>(z, y, N, C, o1, s);
   else grid = launch_block<T, kCand, V4>(z, y, N, C, o1, s);
+  const int64_t row_bytes = (int64_t)C * kElemBytes<T>;
+  if (V4 && row_bytes % 16 == 0) {
+    const int64_t wb = (N * row_bytes + kWriteBytes - 1) / kWriteBytes;
+    hipLaunchKernelGGL((fwl_write_flat<T>), dim3((unsigned)wb), dim3(kBlock), 0, s, z, o.ld, y, o1.H, o1.ccnt, N, C,
+                       o.scale, o.scale_f, o.grad);
+    hipLaunchKernelGGL((fwl_scatter_support<T, V4>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, o.ld, y, o1.H,
+                       o1.ccnt, o1.cidx, N, C, o.scale, o.scale_f, o.grad, false, kLongDone);
+    return grid;
+  }
   const int64_t bytes = N * (int64_t)C * kElemBytes<T>;
   const int64_t fill_blocks = (bytes + kFillBytes - 1) / kFillBytes;
   // rows whose support outgrew the lists are written whole by the scatter kernel, and the fill
@@ -3217,6 +3167,8 @@ int64_t partial_slots(int64_t N) {
 }
 
 
+inline size_t ws_round(size_t b) { return (b + kWsAlign - 1) / kWsAlign * kWsAlign; }
+
 // the mean's part of the workspace: the block partials
 size_t mean_ws_bytes(int64_t N) { return ws_round(sizeof(double) * (size_t)partial_slots(N)); }
 
@@ -3260,32 +3212,19 @@ size_t two_pass_bytes(int64_t N) {
   return (size_t)N * (kTwoPassCap * (sizeof(float) + sizeof(int32_t)) + sizeof(int32_t) + sizeof(float));
 }
 
-// The two passes' candidate bits in memory (Outs::gmask): from kListMinRows rows on (the read pass
-// then streams one row per wavefront), when the workspace holds them: per row one bit per element,
-// in streaming rounds of 1024 (fp32, and 16-bit rows accessed one element at a time) or 2048
-// elements (16-bit 128-bit rows).
-constexpr int64_t kListMinRows = 2048;
-bool list_rows(int64_t N) { return N >= kListMinRows; }
-int list_mask_stride(int64_t C) { return (int)ws_round((size_t)(128 * ((C + 1023) / 1024) + 128)); }
-size_t list_bytes(int64_t N, int64_t C) { return N <= 0 ? 0 : (size_t)N * list_mask_stride(C); }
 
 size_t split_scratch_bytes(int64_t N, int64_t C) {
   const int64_t items = N * split_chunks_bound(N, C, kSplitMinChunk);
   return (size_t)items * (sizeof(double) + sizeof(int) + sizeof(float) + (size_t)kSplitCap * (sizeof(float) + sizeof(int)));
 }
 
-// (lists: with the two passes' candidate lists in memory, where they apply; a workspace of the
-// size without them runs every path, the two-pass op then with its cut lists)
-size_t workspace_bytes(int64_t N, int64_t C, int path, bool lists = true) {
+size_t workspace_bytes(int64_t N, int64_t C, int path) {
   if (N < 0) N = 0;
   // the fp64 partials of the mean, the overflow records, then the larger of the split rows' and
   // the two passes' scratch
   size_t extra = 0;
   if (split_rows(N, C, 4, path)) extra = split_scratch_bytes(N, C);
-  if (two_pass_rows(N, C, 4, path)) {
-    const size_t tp = two_pass_bytes(N) + (lists && list_rows(N) ? list_bytes(N, C) : 0);
-    if (tp > extra) extra = tp;
-  }
+  if (two_pass_rows(N, C, 4, path) && two_pass_bytes(N) > extra) extra = two_pass_bytes(N);
   return mean_ws_bytes(N) + ovf_ws_bytes(N) + extra;
 }
 
@@ -3528,9 +3467,8 @@ int fwl_forward_backward_noalloc(int dtype, const void* logits, int64_t ld, cons
   Params p;
   if (!call_params(options, p)) return FWL_ERR_INVALID_ARG;
   if (bad_shape(N, C)) return FWL_ERR_INVALID_ARG;
-  // every part of the workspace this call needs must fit the static scratch (the two-pass op's
-  // candidate lists in memory are used only where they fit)
-  if (workspace_bytes(N, C, p.path, false) > kNoAllocScratchBytes) return FWL_ERR_WORKSPACE;
+  // every part of the workspace this call would use must fit the static scratch
+  if (workspace_bytes(N, C, p.path) > kNoAllocScratchBytes) return FWL_ERR_WORKSPACE;
   void* ws = nullptr;
   const int rc = scratch_address(&ws);
   if (rc != FWL_OK) return rc;

@@ -169,12 +169,12 @@ def test_dist_full_size(ext, dev, dist, shape):
     torch.cuda.empty_cache()
 
 
-# ---------------------------------------------------------------- the two passes' candidate bits
+# ---------------------------------------------------------------- the two-pass op's write pass
 
 def list_mix(N, C, seed):
-    """Rows for the two-pass op with its candidate bits in memory: N(0, sigma) rows over sigma
-    (supports from a handful of entries to most of the row), ascending rows (every element is a
-    candidate), constant rows and dyadic ties."""
+    """Rows for the two-pass op: N(0, sigma) rows over sigma (supports from a handful of entries to
+    most of the row), ascending rows (every element is a candidate), constant rows and dyadic
+    ties."""
     rng = np.random.default_rng(seed)
     z, y = data.make_dist("gauss", N, C, 1.0, seed=seed)
     sig = np.array([1.0, 0.1, 0.01, 0.001, 5e-4, 1e-4, 100.0, 1.0], np.float32)
@@ -188,11 +188,10 @@ def list_mix(N, C, seed):
 @pytest.mark.parametrize("path", [2, 3])
 @pytest.mark.parametrize("C", [4096, 4099, 20000])
 def test_two_pass_lists(ext, dev, reset_params, path, C):
-    """2048 rows: the forced two-pass paths keep every row's candidate bits (rows of whole 128-bit
-    units: C = 4096, 20000); the write pass zero-fills rows of <= 64 support entries (the scatter
-    kernel adds their support) and builds longer supports from the bits and the logits under them.
-    C = 4099 takes the fill and scatter kernels.  Path 3 sends every row through the overflow
-    solve."""
+    """2048 rows through the forced two-pass paths.  Rows of whole 128-bit units (C = 4096, 20000)
+    take the 4 KB-block write pass: zeros for rows of <= 64 support entries (the scatter kernel adds
+    their support), longer supports from the logits.  C = 4099 takes the fill and scatter kernels.
+    Path 3 sends every row through the overflow solve."""
     z, y = list_mix(2048, C, seed=C + path)
     ext.set_params(path, 512)
     print(f"two-pass lists path={path} C={C}", flush=True)
@@ -203,8 +202,8 @@ def test_two_pass_lists(ext, dev, reset_params, path, C):
 @pytest.mark.parametrize("path", [2, 3])
 @pytest.mark.parametrize("C", [4096, 4097])
 def test_two_pass_lists_16bit(ext, dev, reset_params, dtype, path, C):
-    """The same in 16-bit logits: 128-bit rows (32 candidate bits per lane and round) and odd rows
-    (the fill and scatter kernels)."""
+    """The same in 16-bit logits: rows of whole 128-bit units (the 4 KB-block write pass) and odd
+    rows (the fill and scatter kernels)."""
     z, y = list_mix(2048, C, seed=C + 7 * path)
     z16 = torch.from_numpy(z).to(dtype)
     z32 = z16.float().numpy()

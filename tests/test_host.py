@@ -68,15 +68,6 @@ def ws_expect(N, extra=0):
     return ws_round(8 * slots) + ws_round(8 * N) + extra
 
 
-def list_bytes(N, C):
-    """From 2048 rows on the two passes keep every row's candidate bits in memory: one bit per
-    element in rounds of 1024 elements (128 bytes) or 2048, and 128 bytes more, rounded to 256 bytes
-    per row."""
-    if N < 2048:
-        return 0
-    return N * ws_round(128 * -(-C // 1024) + 128)
-
-
 def test_workspace_bytes():
     L = capi.lib()
     assert L.fwl_workspace_bytes(0, 1) == ws_expect(0)
@@ -248,17 +239,14 @@ def test_workspace_sizes():
         assert W(0, 131072) == ws_expect(0)
         # >= 384 rows of >= 32000 elements, or batches of >= 48M elements in rows of >= 8192 (the
         # fp32 rules, which cover the 16-bit one) run the fused op in two passes: per row 64
-        # support values and indices, kappa and H, and from 2048 rows on the lists in memory
+        # support values and indices, kappa and H
         row = 64 * 8 + 4 + 4
-        assert W(2048, 131072) == ws_expect(2048, 2048 * row + list_bytes(2048, 131072))
-        assert list_bytes(2048, 131072) == 2048 * 16640
-        assert W(2047, 131072) == ws_expect(2047, 2047 * row)
+        assert W(2048, 131072) == ws_expect(2048, 2048 * row)
         assert W(384, 32000) == ws_expect(384, 384 * row)
         assert W(383, 32000) == ws_expect(383)
-        assert W(6144, 8192) == ws_expect(6144, 6144 * row + list_bytes(6144, 8192))   # 48M elements
+        assert W(6144, 8192) == ws_expect(6144, 6144 * row)      # 48M elements
         assert W(6143, 8192) == ws_expect(6143)
-        assert W(65536, 8192) == ws_expect(65536, 65536 * row + list_bytes(65536, 8192))
-        assert W(8192, 32000) == ws_expect(8192, 8192 * row + list_bytes(8192, 32000))
+        assert W(65536, 8192) == ws_expect(65536, 65536 * row)
         assert W(1024, 31999) == ws_expect(1024)
         assert W(129, 24576) == ws_expect(129)
         assert W(128, 24575) == ws_expect(128)
