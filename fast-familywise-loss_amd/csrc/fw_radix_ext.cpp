@@ -377,11 +377,19 @@ std::vector<at::Tensor> fw_linear_grads(at::Tensor hidden, at::Tensor weight, at
     at::Tensor lab_ok = (y >= 0) & (y < V);
     at::Tensor cnt = (kap.clamp_min(0).to(torch::kInt64) + (live & lab_ok & lab_in.logical_not()).to(torch::kInt64));
     at::Tensor incl = cnt.cumsum(0);
-    const int64_t P = N > 0 ? incl[N - 1].item<int64_t>() : 0;
+    at::Tensor offsets = incl - cnt;
+    // The number of entries sizes the sort.  Eagerly it is read back (one wait for the device);
+    // under HIP graph capture, where the host cannot wait, the key array has room for every row's
+    // largest count instead, and the slots past the entries hold a key of column V, which sorts
+    // last and dweight skips (measured at N = 8192, V = 128256: about 0.4 ms more per backward).
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    TORCH_CHECK(hipStreamIsCapturing(s, &cs) == hipSuccess, "fw_linear_grads: hipStreamIsCapturing failed");
+    const bool padded = cs != hipStreamCaptureStatusNone;
+    const int64_t P = padded ? N * (cap + 1) : (N > 0 ? incl[N - 1].item<int64_t>() : 0);
     if (P > 0) {
-      at::Tensor offsets = incl - cnt;
-      at::Tensor keys = torch::empty({P}, y.options());
-      at::Tensor vals = torch::empty({P}, y.options().dtype(torch::kFloat32));
+      at::Tensor keys = padded ? torch::full({P}, V * 2 * N, y.options()) : torch::empty({P}, y.options());
+      at::Tensor vals = padded ? torch::zeros({P}, y.options().dtype(torch::kFloat32))
+                               : torch::empty({P}, y.options().dtype(torch::kFloat32));
       check_status(fwl_linear_coo(y.data_ptr<int64_t>(), N, V, kap.data_ptr<int32_t>(), sup.data_ptr<int32_t>(),
                                   offsets.data_ptr<int64_t>(), rs.data_ptr<float>(), rs_stride,
                                   keys.data_ptr<int64_t>(), vals.data_ptr<float>(), s),

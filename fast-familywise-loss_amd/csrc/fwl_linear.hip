@@ -354,7 +354,10 @@ __global__ __launch_bounds__(kBlock) void fwl_lin_coo(const int64_t* __restrict_
 }
 
 // dweight[j] = sum of g * hidden[row] over column j's entries, in key order (keys sorted).  One
-// wavefront per entry; the wavefront at the first entry of a column does the column.
+// wavefront per entry (strided over the grid); the wavefront at the first entry of a column does
+// the column.  Keys of column >= V (padding after the entries) are skipped.
+constexpr int64_t kLinDweightBlocks = 65536;
+
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kBlock) void fwl_lin_dweight(const void* __restrict__ hid, int64_t N, int64_t V, int d,
                                                           const int64_t* __restrict__ keys,
@@ -363,30 +366,31 @@ __global__ __launch_bounds__(kBlock) void fwl_lin_dweight(const void* __restrict
   constexpr int U = kUnit<T, VEC>;
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
-  const int64_t p0 = (int64_t)blockIdx.x * kWavesPerBlock + wid;
-  if (p0 >= P) return;
   const int64_t twoN = 2 * N;
-  const int64_t j = keys[p0] / twoN;
-  if (j < 0 || j >= V) return;   // not a column of weight
-  if (p0 > 0 && keys[p0 - 1] / twoN == j) return;
-  int64_t p1 = p0 + 1;
-  while (p1 < P && keys[p1] / twoN == j) ++p1;
   const uint32_t row_bytes = (uint32_t)(d * kElemBytes<T>);
-  const rsrc_t out = make_rsrc(static_cast<char*>(dW) + j * d * kElemBytes<T>, row_bytes);
   const int units = (d + U - 1) / U;
-  for (int u = lane; u - lane < units; u += kWave) {
-    float acc[U];
+  for (int64_t p0 = (int64_t)blockIdx.x * kWavesPerBlock + wid; p0 < P; p0 += (int64_t)gridDim.x * kWavesPerBlock) {
+    const int64_t j = keys[p0] / twoN;
+    if (j >= V) break;                                       // padding: sorted after every entry
+    if (j < 0) continue;                                     // not a column of weight
+    if (p0 > 0 && keys[p0 - 1] / twoN == j) continue;        // not the column's first entry
+    int64_t p1 = p0 + 1;
+    while (p1 < P && keys[p1] / twoN == j) ++p1;
+    const rsrc_t out = make_rsrc(static_cast<char*>(dW) + j * d * kElemBytes<T>, row_bytes);
+    for (int u = lane; u - lane < units; u += kWave) {
+      float acc[U];
 #pragma unroll
-    for (int e = 0; e < U; ++e) acc[e] = 0.0f;
-    for (int64_t p = p0; p < p1; ++p) {
-      const int64_t n = (keys[p] % twoN) / 2;   // keys >= 0: 0 <= n < N
-      const float gv = vals[p];
-      float h[U];
-      load_unit<T, VEC>(make_rsrc(static_cast<const char*>(hid) + n * d * kElemBytes<T>, row_bytes), (uint32_t)u, h);
+      for (int e = 0; e < U; ++e) acc[e] = 0.0f;
+      for (int64_t p = p0; p < p1; ++p) {
+        const int64_t n = (keys[p] % twoN) / 2;   // keys >= 0: 0 <= n < N
+        const float gv = vals[p];
+        float h[U];
+        load_unit<T, VEC>(make_rsrc(static_cast<const char*>(hid) + n * d * kElemBytes<T>, row_bytes), (uint32_t)u, h);
 #pragma unroll
-      for (int e = 0; e < U; ++e) acc[e] = fmaf(gv, h[e], acc[e]);
+        for (int e = 0; e < U; ++e) acc[e] = fmaf(gv, h[e], acc[e]);
+      }
+      store_unit<T, VEC>(out, (uint32_t)u, acc);
     }
-    store_unit<T, VEC>(out, (uint32_t)u, acc);
   }
 }
 
@@ -429,7 +433,8 @@ template <typename T>
 int lin_dweight(const void* hid, int64_t N, int64_t V, int64_t d, const int64_t* keys, const float* vals, int64_t P,
                 void* dW, hipStream_t s) {
   if (!aligned(hid, kElemBytes<T>) || !aligned(dW, kElemBytes<T>)) return FWL_ERR_ALIGNMENT;
-  const int64_t blocks = (P + kWavesPerBlock - 1) / kWavesPerBlock;
+  int64_t blocks = (P + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (blocks > kLinDweightBlocks) blocks = kLinDweightBlocks;   // the entries are strided over the grid
   if (lin_vec_ok<T>(hid, dW, d))
     hipLaunchKernelGGL((fwl_lin_dweight<T, true>), dim3((unsigned)blocks), dim3(kBlock), 0, s, hid, N, V, (int)d,
                        keys, vals, P, dW);

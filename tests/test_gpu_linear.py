@@ -248,3 +248,37 @@ def test_lm_head_scale_against_unfused(dev, spread):
     assert abs(l1.float().item() - l2.float().item()) <= 1e-2 * max(1.0, abs(l2.float().item()))
     close(h1.grad, h2.grad.double().cpu().numpy(), 2e-2)
     close(w1.grad, w2.grad.double().cpu().numpy(), 2e-2)
+
+
+def test_backward_graph_capture(dev):
+    """The layer's backward (fw_linear_grads) holds no host synchronisation: captured in a HIP
+    graph and replayed, with eager work and synchronisations between the replays, every replay
+    gives the eager gradients bit for bit (the key array is sized for every row's largest count;
+    the entries' count stays on the device)."""
+    import fwloss
+    ext = fwloss._ext
+    N = 300
+    h, w, y = make(dev, N, 64, 5000, "f32", seed=11)
+    res = fwloss.linear_forward(h, w, y, chunk=1000)
+    assert res["dense"] is None
+    rs = torch.full((1,), 1.0 / N, device=dev)
+    args = (h, w, y, res["kappa_sparse"], res["support"], rs, True, True)
+    dh0, dw0 = ext.fw_linear_grads(*args)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            ext.fw_linear_grads(*args)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        dh, dw = ext.fw_linear_grads(*args)
+    for i in range(3):
+        a = torch.randn(512, 512, device=dev)
+        (a @ a).sum().item()
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"replay {i}", flush=True)
+        assert torch.equal(dh, dh0) and torch.equal(dw, dw0), f"replay {i} differs from the eager gradients"
