@@ -974,6 +974,7 @@ struct alignas(16) BlockShared {
   int ovf[kWavesPerBlock];
   double red_s[kWavesPerBlock];
   int red_c[kWavesPerBlock];
+  int wnx[kWavesPerBlock];         // the wavefront's list outgrew its indices (long lists only)
   uint64_t defm[kWavesPerBlock];   // fwl_overflow_rows: the deferred rows among the next kBlock
   int ncol;
   double tau;
@@ -992,6 +993,33 @@ constexpr int kWaveVCap = 3072;
 static_assert(kWaveVCap >= 2 * kCapMax && kWaveVCap % (4 * kWave) == 0, "indices share the value list");
 struct alignas(16) WaveShared {
   float val[kWaveVCap];
+};
+
+// fwl_block_rows with long lists (the two-pass op's read pass on few rows): each wavefront's list
+// holds kWaveVCap values, the first kCapMax with their indices in the list's last kCapMax slots
+// (as in fwl_wave_stream_rows); 48 KB of lists per block.
+struct alignas(16) BlockSharedBig {
+  union {
+    float bval[kWavesPerBlock][kWaveVCap];
+    struct {
+      unsigned hcnt[kHistBlock];
+      double hsum[kHistBlock];
+    };
+    float blist[2 * kWavesPerBlock * kCapMax];
+  };
+  float sel[kWave];
+  float wmax[kWavesPerBlock];
+  float wlo[kWavesPerBlock];
+  float wB[kWavesPerBlock];
+  int wn[kWavesPerBlock];
+  int wsel[kWavesPerBlock];
+  int ovf[kWavesPerBlock];
+  int wnx[kWavesPerBlock];         // the wavefront's list outgrew its indices
+  double red_s[kWavesPerBlock];
+  int red_c[kWavesPerBlock];
+  int ncol;
+  double tau;
+  int kappa;
 };
 
 // Streaming rounds.  A row is shared by W wavefronts (W = 4: one block per row; W = 1: one
@@ -1247,7 +1275,11 @@ __device__ __forceinline__ void stream_lower_set(const StreamState& st, const fl
 // The wavefronts' candidate lists of a row (or of a stretch of one) in `sh` hold every entry above
 // each wavefront's final bound; cut them at the block maximum and resolve tau and kappa into
 // sh.tau / sh.kappa (valid after the caller's next barrier).
-__device__ __forceinline__ void block_merge_resolve(BlockShared& sh, int n, int wid, int lane) {
+// (SH = BlockSharedBig: the lists are padded (pad_list) and the fixed-point steps of a long merged
+// list run on all four wavefronts, each summing its own list)
+template <typename SH>
+__device__ __forceinline__ void block_merge_resolve(SH& sh, int n, int wid, int lane) {
+  constexpr bool kBig = std::is_same<SH, BlockSharedBig>::value;
   const float* bv = sh.bval[wid];
   const float M = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
   const float tb = bound_below_max(M);
@@ -1279,6 +1311,51 @@ __device__ __forceinline__ void block_merge_resolve(BlockShared& sh, int n, int 
         sh.tau = tt;
         sh.kappa = kk;
       }
+    }
+  } else if (ntot > kWave && kBig) {
+    // fixed-point iterations over the four lists, each wavefront summing its own, the partials
+    // added in a fixed order (every wavefront takes the same steps)
+    auto all_sum_count = [&](float thr, double& s, int& c) {
+      double sw;
+      int cw;
+      list4_sum_count(sh.bval[wid], n, thr, lane, sw, cw);
+      __syncthreads();
+      if (lane == 0) {
+        sh.red_s[wid] = sw;
+        sh.red_c[wid] = cw;
+      }
+      __syncthreads();
+      s = (sh.red_s[0] + sh.red_s[1]) + (sh.red_s[2] + sh.red_s[3]);
+      c = (sh.red_c[0] + sh.red_c[1]) + (sh.red_c[2] + sh.red_c[3]);
+    };
+    double tt = (double)tb, s;
+    int c;
+    all_sum_count(tb, s, c);
+    double res_t = NAN;
+    int res_k = 0;
+    for (int it = 0; it <= ntot + 1; ++it) {
+      const double tn = (s - 1.0) / (double)c;
+      double s2;
+      int c2;
+      all_sum_count(rd32(tn), s2, c2);
+      if (c2 == c || !(tn > tt)) {
+        res_t = tn;
+        res_k = c2;
+        break;
+      }
+      tt = tn;
+      s = s2;
+      c = c2;
+    }
+    const double tc = clamp_below_max(res_t, M);
+    if (tc != res_t) {
+      double s3;
+      res_t = tc;
+      all_sum_count(rd32(res_t), s3, res_k);
+    }
+    if (threadIdx.x == 0) {
+      sh.tau = res_t;
+      sh.kappa = res_k;
     }
   } else if (ntot > kWave) {
     if (wid == 0) {
@@ -1850,11 +1927,16 @@ __device__ void write_support(const void* row, int64_t r, int C, int yr, float H
   }
 }
 
-template <typename T, int MODE, bool V4>
+// (BIG: the long lists of BlockSharedBig, in candidate-list mode; a row one of whose wavefronts'
+// lists outgrew its indices has its support, where the caller wants it listed, written from one
+// more pass over the row)
+template <typename T, int MODE, bool V4, bool BIG = false>
 __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict__ z,
                                                          const int64_t* __restrict__ tgt, int64_t N,
                                                          int C, Outs o) {
-  __shared__ BlockShared sh;
+  static_assert(!BIG || MODE == kCand, "long block lists: candidate-list mode only");
+  using SH = std::conditional_t<BIG, BlockSharedBig, BlockShared>;
+  __shared__ SH sh;
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
   double bsum = 0.0;
@@ -1870,17 +1952,22 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
     const bool yok = y64 >= 0 && y64 < C;
     const int yr = yok ? (int)y64 : -1;
     float* bv = sh.bval[wid];
-    int* bi = sh.bidx[wid];
+    int* bi;
+    if constexpr (BIG) bi = reinterpret_cast<int*>(sh.bval[wid] + (kWaveVCap - kCapMax));
+    else bi = sh.bidx[wid];
+    const int vcap = BIG && o.cap >= kCapMax ? kWaveVCap : o.cap;
 
     StreamState st = stream_state(o.force_generic != 0);
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, o.cap, o.cap, st, first);
+    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, vcap, o.cap, st, first);
+    if constexpr (BIG) pad_list(bv, st.n, lane);
     if (lane == 0) {
       sh.wmax[wid] = st.m;
       sh.wn[wid] = st.n;
       sh.ovf[wid] = st.ovf;
+      if constexpr (BIG) sh.wnx[wid] = st.noidx;
     }
     const int64_t rn = r + gridDim.x;
     if constexpr (MODE == kGrad || MODE == kMask) {
@@ -1909,6 +1996,9 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
           if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + id, inv);
           else o.mask[r * (int64_t)C + id] = 1;
         }
+      } else if (BIG && (sh.wnx[0] | sh.wnx[1] | sh.wnx[2] | sh.wnx[3])) {
+        // some list kept values only: the support from the row, where it is listed at all
+        if (kappa <= o.ccap) write_support<kWavesPerBlock, T, MODE, V4, true>(row, r, C, yr, Hf, inv, o, sh.wsel, lane, wid);
       } else {
         int ns = 0;
         for (int p0 = 0; p0 < st.n; p0 += kWave) {
@@ -2643,6 +2733,7 @@ __global__ __launch_bounds__(kBlock) void fwl_cand_to_grad(
 // on MI355X: a 1 GiB fill writes at 6.8 TB/s in 4 KB blocks but at 6.1 TB/s in 16 KB blocks, and
 // a block that must first load its row's data before storing is bound by that latency.
 constexpr int kTwoPassCap = 64;          // support entries kept per row between the passes
+constexpr int kTwoPassWaveRowsPerCU = 8;    // rows per CU from which the read pass takes a wavefront per row
 constexpr int kFillBytes = 4096;         // bytes per block of the fill
 
 // kap (optional): per row its kappa; rows whose kappa exceeds `cap` are left alone (the scatter
@@ -3063,11 +3154,11 @@ int launch_overflow(const void* z, const int64_t* y, int64_t N, int C, Outs o, i
   return grid;
 }
 
-template <typename T, int MODE, bool V4>
+template <typename T, int MODE, bool V4, bool BIG = false>
 int launch_block(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
-  const void* k = reinterpret_cast<const void*>(&fwl_block_rows<T, MODE, V4>);
+  const void* k = reinterpret_cast<const void*>(&fwl_block_rows<T, MODE, V4, BIG>);
   const int grid = persistent_grid(N, 1, resident_blocks(k), kMaxBlocksRow);
-  hipLaunchKernelGGL((fwl_block_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+  hipLaunchKernelGGL((fwl_block_rows<T, MODE, V4, BIG>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
   return grid + launch_overflow<T, MODE, V4>(z, y, N, C, o, grid, s);
 }
 
@@ -3099,12 +3190,13 @@ int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Out
   o1.ccap = kTwoPassCap;
   if (o1.H == nullptr) o1.H = Hs;
   o1.grad = nullptr;
-  // The read pass streams one row per wavefront when there are rows for two wavefronts per SIMD
-  // (8192 x 32000: 178 us against 206 us with one block per row; 2048 x 131072: equal), else one
-  // row per block (520 x 128256: 181 us with one row per wavefront, 119 us per block).
+  // The read pass streams one row per wavefront when there are rows for kTwoPassWaveRowsPerCU
+  // wavefronts per CU (8192 x 32000: 178 us against 206 us with one block per row), else one row
+  // per block (520 x 128256: 181 us with one row per wavefront, 119 us per block), both with long
+  // lists.
   int grid;
-  if (N >= 2 * 4 * (int64_t)device_cus()) grid = launch_wave_stream<T, kCand, V4>(z, y, N, C, o1, s);
-  else grid = launch_block<T, kCand, V4>(z, y, N, C, o1, s);
+  if (N >= kTwoPassWaveRowsPerCU * (int64_t)device_cus()) grid = launch_wave_stream<T, kCand, V4>(z, y, N, C, o1, s);
+  else grid = launch_block<T, kCand, V4, true>(z, y, N, C, o1, s);
   const int64_t row_bytes = (int64_t)C * kElemBytes<T>;
   if (V4 && row_bytes % 16 == 0) {
     const int64_t wb = (N * row_bytes + kWriteBytes - 1) / kWriteBytes;
