@@ -286,6 +286,21 @@ __device__ __forceinline__ float select_lanes(uint64_t mask, float if_set, float
 }
 
 // maximum over the wavefront, returned in every lane (wavefront-uniform)
+// fp32 sum over the wavefront in a fixed order (for bounds: each value takes part in at most 6
+// roundings of the tree, see safe_lower32)
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v += __int_as_float(dpp_mov<kQuadXor1>(__float_as_int(v)));
+  v += __int_as_float(dpp_mov<kQuadXor2>(__float_as_int(v)));
+  v += __int_as_float(dpp_mov<kRowHalfMirror>(__float_as_int(v)));
+  v += __int_as_float(dpp_mov<kRowMirror>(__float_as_int(v)));
+  const int x = __float_as_int(v);
+  const float a = __int_as_float(__builtin_amdgcn_readlane(x, 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(x, 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(x, 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(x, 48));
+  return (a + b) + (c + d);
+}
+
 __device__ __forceinline__ float wave_max_f32(float v) {
   v = fmaxf(v, __int_as_float(dpp_mov<kQuadXor1>(__float_as_int(v))));
   v = fmaxf(v, __int_as_float(dpp_mov<kQuadXor2>(__float_as_int(v))));
@@ -484,6 +499,9 @@ __device__ __forceinline__ float safe_lower(double s, int c, float B) {
 // magnitude <= B each, then added in fp64.  Adding the j-th value rounds by at most j*B*2^-24, so
 // a lane of k values is off by at most k(k+1)/2 * B*2^-24, and the error of the sum divided by the
 // number c of values is at most (k_max + 1)/2 * B*2^-24 <= B*2^-19: the bound moves down by that.
+// Lanes of at most 48 values may also be added by wave_sum_f32 instead: each of its 6 levels
+// rounds by at most 2^-24 times the sum of the magnitudes below it (<= c*B), 6*B*2^-24 per value,
+// and 24.5 + 6 < 32.
 __device__ __forceinline__ float safe_lower32(double s, int c, float B) {
   if (c <= 0) return -INFINITY;
   const double h = (s - 1.0) / (double)c - (double)B * 0x1p-19;

@@ -179,19 +179,21 @@ __device__ __forceinline__ void reg_sum_count(const float* x, float thr, double&
   c = wave_sum_i32(cnt);
 }
 
-// the same with per-lane fp32 partial sums (for bounds: see safe_lower32)
+// the same for bounds (see safe_lower32): per-lane fp32 partial sums added by an fp32 tree, the
+// count from ballots (on the scalar unit, beside the tree's chain of dependent steps)
 template <int E>
 __device__ __forceinline__ void reg_sum_count32(const float* x, float thr, double& s, int& c) {
+  static_assert(E <= 48, "safe_lower32 allows at most 48 values per lane with an fp32 tree");
   float acc = 0.0f;
   int cnt = 0;
 #pragma unroll
   for (int i = 0; i < E; ++i) {
     const bool k = x[i] > thr;
     acc += k ? x[i] : 0.0f;
-    cnt += k ? 1 : 0;
+    cnt += __popcll(ballot(k));
   }
-  s = wave_sum_f64((double)acc);
-  c = wave_sum_i32(cnt);
+  s = (double)wave_sum_f32(acc);
+  c = cnt;
 }
 
 // A register row with more than 64 candidates z > t0 (its LDS list cl holds them, n of them;
