@@ -444,6 +444,17 @@ __device__ __forceinline__ double scan_f64(double v) {
   return v;
 }
 
+// inclusive prefix sum of an int over the wavefront's 64 lanes
+__device__ __forceinline__ int scan_i32(int v) {
+  v += __builtin_amdgcn_mov_dpp(v, 0x111, 0xF, 0xF, true);   // row_shr:1 (past the row edge: 0)
+  v += __builtin_amdgcn_mov_dpp(v, 0x112, 0xF, 0xF, true);   // row_shr:2
+  v += __builtin_amdgcn_mov_dpp(v, 0x114, 0xF, 0xF, true);   // row_shr:4
+  v += __builtin_amdgcn_mov_dpp(v, 0x118, 0xF, 0xF, true);   // row_shr:8
+  v += dpp_or0<kRowBcast15, 0xA>(v);                          // rows 1, 3 += last lane of 0, 2
+  v += dpp_or0<kRowBcast31, 0xC>(v);                          // rows 2, 3 += lane 31
+  return v;
+}
+
 // largest float <= t (so that x > t <=> x > rd32(t) for every float x; fw_cpu.cpp:96-101)
 __device__ __forceinline__ float rd32(double t) {
   float r = (float)t;
@@ -599,6 +610,37 @@ __device__ __forceinline__ void list4_sum_count(const float* bv, int n, float th
   list4_lane<double>(bv, n, thr, lane, acc, cnt);
   s = wave_sum_f64(acc);
   c = wave_sum_i32(cnt);
+}
+
+// list4_compact that also returns this lane's fp32 sum and count of the entries kept (at most n/64
+// terms: a bound's partial sum, see safe_lower32)
+__device__ __forceinline__ int list4_compact_sum(float* bv, int* bi, int n, float t, bool noidx, int lane,
+                                                 float& ks, int& kc) {
+  int w = 0;
+  ks = 0.0f;
+  kc = 0;
+  for (int p0 = 0; p0 < n; p0 += 4 * kWave) {
+    const int p = p0 + 4 * lane;
+    const v4f v = *reinterpret_cast<const v4f*>(bv + p);
+    v4i id = {-1, -1, -1, -1};
+    if (!noidx) id = *reinterpret_cast<const v4i*>(bi + p);
+    // every write below lands below p0 + 256: on entries this group has already read
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool keep = v[j] > t;
+      ks += keep ? v[j] : 0.0f;
+      kc += keep ? 1 : 0;
+      const uint64_t b = ballot(keep);
+      if (keep) {
+        const int pos = w + rank_in(b);
+        bv[pos] = v[j];
+        if (!noidx) bi[pos] = id[j];
+      }
+      w += __popcll(b);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  return w;
 }
 
 // keep the entries > t of a padded list [0, n) in place (and their indices, unless noidx; bi is

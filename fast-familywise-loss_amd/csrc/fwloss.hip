@@ -967,6 +967,7 @@ struct alignas(16) BlockShared {
     };
     float blist[2 * kWavesPerBlock * kCapMax];
   };
+  float trash[kWavesPerBlock][kWave];   // each lane's sink for the list appends it does not make
   float sel[kWave];
   float wmax[kWavesPerBlock];
   float wlo[kWavesPerBlock];      // each wavefront's lower bound on tau
@@ -988,13 +989,14 @@ static_assert(sizeof(unsigned) * kHistBlock + sizeof(double) * kHistBlock <= 8 *
 // The list of one wavefront of fwl_wave_stream_rows: up to kWaveVCap candidate values, the first
 // kCapMax of them with their indices, which live in the list's last kCapMax slots while the list
 // holds at most kCapMax entries.  A row whose list outgrows the indices keeps its values (tau
-// comes from them) and writes its support from one more pass over the row (the two-pass op: from
-// the candidate bits in memory): rows of low-variance logits (hundreds to thousands of support
-// entries) then need no overflow solve.  48 KB of LDS per block: three blocks per CU.
+// comes from them) and writes its support from one more pass over the row (the two-pass op's
+// write pass): rows of low-variance logits (hundreds to thousands of support entries) then need
+// no overflow solve.  49 KB of LDS per block (lists and trash slots): three blocks per CU.
 constexpr int kWaveVCap = 3072;
 static_assert(kWaveVCap >= 2 * kCapMax && kWaveVCap % (4 * kWave) == 0, "indices share the value list");
 struct alignas(16) WaveShared {
   float val[kWaveVCap];
+  float trash[kWave];   // each lane's sink for the list appends it does not make
 };
 
 // fwl_block_rows with long lists (the two-pass op's read pass on few rows): each wavefront's list
@@ -1009,6 +1011,7 @@ struct alignas(16) BlockSharedBig {
     };
     float blist[2 * kWavesPerBlock * kCapMax];
   };
+  float trash[kWavesPerBlock][kWave];
   float sel[kWave];
   float wmax[kWavesPerBlock];
   float wlo[kWavesPerBlock];
@@ -1102,7 +1105,9 @@ __device__ __forceinline__ StreamState stream_state(bool force) {
 
 // Raise the wavefront's lower bound t with fixed-point steps t <- H({entries > t}) over its list
 // and the round held in registers (a subset of the row, so H of it is <= tau), then drop the list
-// entries <= t (not in the support: their output stays the zero written while streaming).
+// entries <= the last step's start (not in the support: their output stays the zero written while
+// streaming).  The last step's sum comes from the compaction itself, so the list may keep entries
+// in (that start, t]: every reader of a list filters by its bound.
 // The list (bv, and bi unless noidx) is padded storage (pad_list): at most 64 entries per lane,
 // so its fp32 partial sums stay within what safe_lower32 allows.
 template <int S>
@@ -1110,27 +1115,32 @@ __device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, co
                                        int lane) {
   const float B = fmaxf(fabsf(m), fabsf(t));
   pad_list(bv, n, lane);
-  float tf = t;
-  for (int it = 0; it < kTightenSteps; ++it) {
-    // per-lane fp32 partial sums of the list and of the round (a bound needs no exact sum)
-    float ls;
-    int lc;
-    list4_lane<float>(bv, n, tf, lane, ls, lc);
-    float rs = 0.0f;
+  auto round_part = [&](float thr, float& rs, int& rc) {
+    rs = 0.0f;
 #pragma unroll
     for (int i = 0; i < S; ++i) {
-      const bool k = x[i] > tf;
+      const bool k = x[i] > thr;
       rs += k ? x[i] : 0.0f;
-      lc += k ? 1 : 0;
+      rc += k ? 1 : 0;
     }
-    const double s = wave_sum_f64((double)ls + (double)rs);
-    const int c = wave_sum_i32(lc);
-    const float nt = safe_lower32(s, c, B);
+  };
+  float tf = t;
+  for (int it = 0; it + 1 < kTightenSteps; ++it) {
+    // per-lane fp32 partial sums of the list and of the round (a bound needs no exact sum)
+    float ls, rs;
+    int lc;
+    list4_lane<float>(bv, n, tf, lane, ls, lc);
+    round_part(tf, rs, lc);
+    const float nt = safe_lower32(wave_sum_f64((double)ls + (double)rs), wave_sum_i32(lc), B);
     if (!(nt > tf)) break;
     tf = nt;
   }
-  t = fmaxf(t, tf);
-  n = list4_compact(bv, bi, n, t, noidx, lane);
+  float ks, rs;
+  int kc;
+  n = list4_compact_sum(bv, bi, n, tf, noidx, lane, ks, kc);
+  round_part(tf, rs, kc);
+  const float nt = safe_lower32(wave_sum_f64((double)ks + (double)rs), wave_sum_i32(kc), B);
+  t = fmaxf(t, fmaxf(tf, nt));
 }
 
 // Candidates of one round: the running maximum m gives the bound t (>= m - 1 rounded down), and
@@ -1142,7 +1152,7 @@ __device__ __forceinline__ void tighten(float* bv, int* bi, int& n, float& t, co
 //
 template <int W, typename T, bool VEC>
 __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, int wid, int lane, float* bv,
-                                           int* bi, int cap, int icap, StreamState& st) {
+                                           int* bi, float* tr, int cap, int icap, StreamState& st) {
   constexpr int S = Round<T, VEC>::kSlots;
   constexpr int kRoundElems = kUnit<T, VEC> * kWave * W * Round<T, VEC>::kPer;
   float lm = -INFINITY;
@@ -1165,15 +1175,22 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
     if (ballot(lm > st.t) == 0) {
       done = true;   // no candidate in this round (the common case)
     } else {
-      int cnt = 0;
+      // per-lane counts and their prefix sum place each lane's entries: lane L appends its k-th
+      // entry at n + (entries of lanes < L) + k, and an entry not appended is written to the
+      // lane's trash slot (tr) instead, so the appends need no per-slot ballot or branch
+      int lc = 0;
 #pragma unroll
-      for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > st.t));
+      for (int i = 0; i < S; ++i) lc += a.x[i] > st.t ? 1 : 0;
+      int incl = scan_i32(lc);
+      int cnt = __builtin_amdgcn_readlane(incl, kWave - 1);
       // a list that still has its indices is tightened before it gives them up
       if (st.n + cnt > (st.noidx ? cap : icap)) {
         tighten<S>(bv, bi, st.n, st.t, a.x, st.m, st.noidx, lane);
-        cnt = 0;
+        lc = 0;
 #pragma unroll
-        for (int i = 0; i < S; ++i) cnt += __popcll(ballot(a.x[i] > st.t));
+        for (int i = 0; i < S; ++i) lc += a.x[i] > st.t ? 1 : 0;
+        incl = scan_i32(lc);
+        cnt = __builtin_amdgcn_readlane(incl, kWave - 1);
         if (st.n + cnt > cap) {
           // the list cannot hold every entry above the bound: keep its sum and go on summing
           st.ovf = true;
@@ -1189,17 +1206,24 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
       }
       if (!st.ovf) {
         if (st.n + cnt > icap) st.noidx = true;
+        int pos = st.n + incl - lc;
+        if (st.noidx) {
 #pragma unroll
-        for (int i = 0; i < S; ++i) {
-          const bool p = a.x[i] > st.t;
-          const uint64_t b = ballot(p);
-          if (p) {
-            const int pos = st.n + rank_in(b);
-            bv[pos] = a.x[i];
-            if (!st.noidx) bi[pos] = round_slot_index<W, T, VEC>(round, i, wid, lane);
+          for (int i = 0; i < S; ++i) {
+            const bool p = a.x[i] > st.t;
+            *(p ? bv + pos : tr) = a.x[i];
+            pos += p ? 1 : 0;
           }
-          st.n += __popcll(b);
+        } else {
+#pragma unroll
+          for (int i = 0; i < S; ++i) {
+            const bool p = a.x[i] > st.t;
+            *(p ? bv + pos : tr) = a.x[i];
+            *(p ? bi + pos : reinterpret_cast<int*>(tr)) = round_slot_index<W, T, VEC>(round, i, wid, lane);
+            pos += p ? 1 : 0;
+          }
         }
+        st.n += cnt;
         done = true;
       }
     }
@@ -1230,8 +1254,8 @@ __device__ __forceinline__ void stream_first(const void* __restrict__ row, int C
 // the first round, from stream_first.
 template <int W, typename T, int MODE, bool VEC>
 __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* out_row, int C, int lane, int wid,
-                                            float* bv, int* bi, int cap, int icap, StreamState& st,
-                                            Round<T, VEC>& a) {
+                                            float* bv, int* bi, float* tr, int cap, int icap,
+                                            StreamState& st, Round<T, VEC>& a) {
   constexpr int per_round = kWave * W * Round<T, VEC>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
@@ -1249,11 +1273,11 @@ __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* 
   while (true) {
     load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
-    scan_round<W, T, VEC>(a, k, C, wid, lane, bv, bi, cap, icap, st);
+    scan_round<W, T, VEC>(a, k, C, wid, lane, bv, bi, tr, cap, icap, st);
     if (++k >= rounds) break;
     load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
-    scan_round<W, T, VEC>(b, k, C, wid, lane, bv, bi, cap, icap, st);
+    scan_round<W, T, VEC>(b, k, C, wid, lane, bv, bi, tr, cap, icap, st);
     if (++k >= rounds) break;
   }
 }
@@ -1963,7 +1987,8 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, vcap, o.cap, st, first);
+    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, sh.trash[wid] + lane, vcap, o.cap, st,
+                                             first);
     if constexpr (BIG) pad_list(bv, st.n, lane);
     if (lane == 0) {
       sh.wmax[wid] = st.m;
@@ -2131,7 +2156,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-    stream_span<1, T, MODE, V4>(row, out_row, C, lane, 0, bv, bi, vcap, icap, st, first);
+    stream_span<1, T, MODE, V4>(row, out_row, C, lane, 0, bv, bi, s_w[wid].trash + lane, vcap, icap, st, first);
     if (k + 1 < nrows) stream_first<1, T, V4>(row_at(k + 1), C, lane, 0, first);
     double tau;
     int kappa;
@@ -2353,7 +2378,8 @@ __global__ __launch_bounds__(kBlock) void fwl_split_chunks(const void* __restric
     StreamState st = stream_state(o.force_generic != 0);
     Round<T, V4> first;
     stream_first<kWavesPerBlock, T, V4>(span, len, lane, wid, first);
-    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, o.cap, o.cap, st, first);
+    stream_span<kWavesPerBlock, T, MODE, V4>(span, out_span, len, lane, wid, bv, bi, sh.trash[wid] + lane, o.cap,
+                                             o.cap, st, first);
     if (lane == 0) {
       sh.wmax[wid] = st.m;
       sh.wn[wid] = st.n;
