@@ -194,6 +194,8 @@ struct Outs {
   int cap;             // LDS candidate capacity per wavefront (<= kCapMax)
   int cstride;         // candidate-list mode: row stride of cval/cidx (C for the drop-in op)
   int ccap;            // candidate-list mode: entries kept per row (further ones are dropped)
+  int mark_unlisted;   // candidate-list mode: a row whose list kept values only gets ccnt = -kappa
+                       // (support not listed) instead of one more pass over the row to list it
 };
 
 // ------------------------------------------------------------------------------------------------

@@ -1088,6 +1088,8 @@ struct StreamState {
   float tov;      // the bound at the overflow: acc_s/acc_c hold the entries > tov seen since
   double acc_s;   // (per lane)
   int acc_c;      // (per lane)
+  int ylab;       // an element index of the span whose value is kept in zy as it streams by (-1: none)
+  float zy;
 };
 
 __device__ __forceinline__ StreamState stream_state(bool force) {
@@ -1100,6 +1102,8 @@ __device__ __forceinline__ StreamState stream_state(bool force) {
   st.tov = NAN;     // set at the overflow (forced: at the first round)
   st.acc_s = 0.0;
   st.acc_c = 0;
+  st.ylab = -1;
+  st.zy = NAN;
   return st;
 }
 
@@ -1155,6 +1159,19 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
                                            int* bi, float* tr, int cap, int icap, StreamState& st) {
   constexpr int S = Round<T, VEC>::kSlots;
   constexpr int kRoundElems = kUnit<T, VEC> * kWave * W * Round<T, VEC>::kPer;
+  if (st.ylab >= round * kRoundElems && st.ylab < (round + 1) * kRoundElems) {
+    // the round that holds element ylab: its value, from the lane that has it
+    float v = 0.0f;
+    bool f = false;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const bool h = round_slot_index<W, T, VEC>(round, i, wid, lane) == st.ylab;
+      v = h ? a.x[i] : v;
+      f = f || h;
+    }
+    const uint64_t b = ballot(f);
+    if (b != 0) st.zy = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)__builtin_ctzll(b)));
+  }
   float lm = -INFINITY;
   if ((round + 1) * kRoundElems <= C) {
     // a round inside the row: nothing to mask
@@ -1915,7 +1932,7 @@ __device__ void write_support(const void* row, int64_t r, int C, int yr, float H
     constexpr int per_round = kWave * W * S;
     const int rounds = (C + per_round - 1) / per_round;
     const rsrc_t in = make_rsrc(row, (uint32_t)(kElemBytes<T> * C));
-    float* cv = o.cval + r * (int64_t)o.cstride;
+    float* cv = o.cval != nullptr ? o.cval + r * (int64_t)o.cstride : nullptr;   // null: indices only
     int32_t* ci = o.cidx + r * (int64_t)o.cstride;
     int base = 0;
     for (int k = 0; k < rounds; ++k) {
@@ -1944,7 +1961,7 @@ __device__ void write_support(const void* row, int64_t r, int C, int yr, float H
         const uint64_t b = ballot(sel);
         const int pos = off + rank_in(b);
         if (sel && pos < o.ccap) {
-          cv[pos] = a.x[i];
+          if (cv != nullptr) cv[pos] = a.x[i];
           ci[pos] = j;
         }
         off += __popcll(b);
@@ -2008,6 +2025,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
     double tau = NAN;
     int kappa = 0;
     bool deferred = false;
+    bool unlisted = false;   // candidate-list mode: support left unlisted (mark_unlisted)
     if (!overflow) {
       block_merge_resolve(sh, st.n, wid, lane);
       __syncthreads();
@@ -2025,7 +2043,9 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
         }
       } else if (BIG && (sh.wnx[0] | sh.wnx[1] | sh.wnx[2] | sh.wnx[3])) {
         // some list kept values only: the support from the row, where it is listed at all
-        if (kappa <= o.ccap) write_support<kWavesPerBlock, T, MODE, V4, true>(row, r, C, yr, Hf, inv, o, sh.wsel, lane, wid);
+        unlisted = o.mark_unlisted != 0;
+        if (kappa <= o.ccap && !unlisted)
+          write_support<kWavesPerBlock, T, MODE, V4, true>(row, r, C, yr, Hf, inv, o, sh.wsel, lane, wid);
       } else {
         int ns = 0;
         for (int p0 = 0; p0 < st.n; p0 += kWave) {
@@ -2037,7 +2057,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
         __syncthreads();
         int off = 0;
         for (int w = 0; w < wid; ++w) off += sh.wsel[w];
-        float* cv = o.cval + r * (int64_t)o.cstride;
+        float* cv = o.cval != nullptr ? o.cval + r * (int64_t)o.cstride : nullptr;
         int32_t* ci = o.cidx + r * (int64_t)o.cstride;
         for (int p0 = 0; p0 < st.n; p0 += kWave) {
           const int p = p0 + lane;
@@ -2046,7 +2066,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
           const uint64_t b = ballot(k);
           if (k && off + rank_in(b) < o.ccap) {
             const int pos = off + rank_in(b);
-            cv[pos] = v;
+            if (cv != nullptr) cv[pos] = v;
             ci[pos] = bi[p];
           }
           off += __popcll(b);
@@ -2103,7 +2123,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
       if (o.loss) o.loss[r] = loss;
       if (o.loss64) o.loss64[r] = l64;
       if (o.kappa) o.kappa[r] = kappa;
-      if constexpr (MODE == kCand) o.ccnt[r] = kappa;
+      if constexpr (MODE == kCand) o.ccnt[r] = unlisted ? -kappa : kappa;
       bsum += (double)loss;
     }
     __syncthreads();
@@ -2139,6 +2159,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
   double my_l64 = 0.0;
   int my_kappa = 0;
   bool my_def = false;   // this lane's row was deferred to fwl_overflow_rows
+  bool my_unl = false;   // candidate-list mode: this lane's row left unlisted (mark_unlisted)
   double lsum = 0.0;
   auto row_at = [&](int k) { return static_cast<const char*>(z) + (w + (int64_t)k * stride) * o.ld * kElemBytes<T>; };
   // the next row's first round is loaded before this row is resolved (see fwl_block_rows)
@@ -2153,6 +2174,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     const int yr = yok ? (int)y64 : -1;
 
     StreamState st = stream_state(o.force_generic != 0);
+    st.ylab = yr;   // the label's logit, taken from the stream (no dependent load at the row's end)
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
@@ -2190,12 +2212,14 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     if (lane == 0 && !st.ovf && o.ovf_lo != nullptr) o.ovf_lo[r] = NAN;
     const float Hf = rd32(tau);
     const float inv = (float)(o.scale / (double)kappa);
-    // this wavefront's zero placeholders have landed before any entry is rewritten
-    wait_vmem();
+    // this wavefront's zero placeholders have landed before any entry is rewritten (candidate
+    // lists have none: the next row's first loads stay in flight)
+    if constexpr (MODE != kCand) wait_vmem();
     if (st.noidx && !st.ovf) {
       // the list kept values only: the support from one more pass over the row (candidate lists
       // cut at ccap leave a longer support to fwl_scatter_support, which reads the row itself)
-      if (MODE != kCand || kappa <= o.ccap) write_support<1, T, MODE, V4, true>(row, r, C, yr, Hf, inv, o, nullptr, lane, 0);
+      if (MODE != kCand || (kappa <= o.ccap && !o.mark_unlisted))
+        write_support<1, T, MODE, V4, true>(row, r, C, yr, Hf, inv, o, nullptr, lane, 0);
     } else if (!st.ovf) {
       if constexpr (MODE == kGrad || MODE == kMask) {
         for (int p = lane; p < st.n; p += kWave) {
@@ -2212,7 +2236,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
           const bool sel = v > Hf;
           const uint64_t b = ballot(sel);
           if (sel && out + rank_in(b) < o.ccap) {
-            o.cval[r * (int64_t)o.cstride + out + rank_in(b)] = v;
+            if (o.cval != nullptr) o.cval[r * (int64_t)o.cstride + out + rank_in(b)] = v;
             o.cidx[r * (int64_t)o.cstride + out + rank_in(b)] = bi[p];
           }
           out += __popcll(b);
@@ -2221,7 +2245,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     } else {
       write_support<1, T, MODE, V4, false>(row, r, C, yr, Hf, inv, o, nullptr, lane, 0);
     }
-    const float zy = yok ? load_elem<T>(row, yr) : NAN;
+    const float zy = yok ? st.zy : NAN;
     if (lane == 0 && yok) {
       if constexpr (MODE == kGrad) store_elem<T>(o.grad, r * (int64_t)C + yr, (zy > Hf ? inv : 0.0f) - o.scale_f);
       else if constexpr (MODE == kMask) o.mask[r * (int64_t)C + yr] = (uint8_t)(zy > Hf);
@@ -2234,6 +2258,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
       my_loss = loss;
       my_l64 = l64;
       my_kappa = kappa;
+      my_unl = MODE == kCand && st.noidx && !st.ovf && o.mark_unlisted != 0;
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -2243,7 +2268,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     if (o.loss) o.loss[r] = my_loss;
     if (o.loss64) o.loss64[r] = my_l64;
     if (o.kappa) o.kappa[r] = my_kappa;
-    if constexpr (MODE == kCand) o.ccnt[r] = my_kappa;
+    if constexpr (MODE == kCand) o.ccnt[r] = my_unl ? -my_kappa : my_kappa;
   }
   // each wavefront's loss sum in the first bytes of its own (now unused) list
   __builtin_amdgcn_wave_barrier();
@@ -2753,22 +2778,28 @@ __global__ __launch_bounds__(kBlock) void fwl_cand_to_grad(
 }
 
 // Write pass of the fused op for long rows.  A read pass over the logits (the candidate-list
-// kernel, with its lists cut at kTwoPassCap entries in the workspace) leaves every row's H, kappa
-// and support.  The gradient is then written by two kernels: fwl_fill_zero streams zeros over the
-// whole [N, C] gradient in 4 KB blocks, a plain fill that needs nothing from the read pass; then
-// fwl_scatter_support writes each row's few support entries and its label element (one wavefront
-// per row).  Rows whose support exceeds the list are rewritten from the logits (z > H).  Measured
-// on MI355X: a 1 GiB fill writes at 6.8 TB/s in 4 KB blocks but at 6.1 TB/s in 16 KB blocks, and
-// a block that must first load its row's data before storing is bound by that latency.
-constexpr int kTwoPassCap = 64;          // support entries kept per row between the passes
+// kernel, its lists cut at kTwoPassCap indices in the workspace) leaves every row's H, kappa and,
+// where its list kept the indices, its support.  The gradient is then written by two kernels:
+// fwl_fill_zero streams zeros over the whole [N, C] gradient in 4 KB blocks, a plain fill that
+// needs nothing from the read pass; then fwl_scatter_support writes each row's listed support
+// entries and its label element (one wavefront per row).  Rows whose support is not listed are
+// rewritten from the logits (z > H).  Measured on MI355X: a 1 GiB fill writes at 6.8 TB/s in
+// 4 KB blocks but at 6.1 TB/s in 16 KB blocks, and a block that must first load its row's data
+// before storing is bound by that latency.
+constexpr int kTwoPassCap = kCapMax;     // support indices kept per row between the passes
+
+// the read pass's per-row count: kappa where the support is listed, -kappa (or a kappa above
+// kTwoPassCap) where it is not
+__device__ __forceinline__ bool two_pass_listed(int k) { return k > 0 && k <= kTwoPassCap; }
+__device__ __forceinline__ int two_pass_kappa(int k) { return k < 0 ? -k : k; }
 constexpr int kTwoPassWaveRowsPerCU = 8;    // rows per CU from which the read pass takes a wavefront per row
 constexpr int kFillBytes = 4096;         // bytes per block of the fill
 
-// kap (optional): per row its kappa; rows whose kappa exceeds `cap` are left alone (the scatter
-// writes them whole).  Needs rows of a whole number of dwords and of >= kFillBytes bytes, so that a
+// kap (optional): per row the read pass's count; rows whose support is not listed are left alone
+// (the scatter writes them whole).  Needs rows of a whole number of dwords and of >= kFillBytes bytes, so that a
 // block's bytes lie in at most two rows and no dword straddles two rows.
 __global__ __launch_bounds__(kBlock) void fwl_fill_zero(void* __restrict__ dst, int64_t bytes, int64_t row_bytes,
-                                                         const int32_t* __restrict__ kap, int cap) {
+                                                         const int32_t* __restrict__ kap) {
   const int64_t b0 = (int64_t)blockIdx.x * kFillBytes;
   const int64_t left = bytes - b0;
   const rsrc_t r = make_rsrc(static_cast<char*>(dst) + b0, (uint32_t)(left < kFillBytes ? left : kFillBytes));
@@ -2777,8 +2808,8 @@ __global__ __launch_bounds__(kBlock) void fwl_fill_zero(void* __restrict__ dst, 
     // the block's first row and where the next one starts (block-uniform)
     const int64_t ra = b0 / row_bytes;
     const int64_t next = (ra + 1) * row_bytes - b0;   // bytes into the block
-    const bool fa = kap[ra] <= cap;
-    const bool fb = next < kFillBytes && next < left ? kap[ra + 1] <= cap : fa;
+    const bool fa = two_pass_listed(kap[ra]);
+    const bool fb = next < kFillBytes && next < left ? two_pass_listed(kap[ra + 1]) : fa;
     if (!fa && !fb) return;
     if (!(fa && fb)) {
       // dwords of the rows to fill only
@@ -2796,7 +2827,7 @@ __global__ __launch_bounds__(kBlock) void fwl_fill_zero(void* __restrict__ dst, 
   __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, r, off, 0, 0);
 }
 
-// how fwl_scatter_support treats rows of more than kTwoPassCap support entries
+// how fwl_scatter_support treats rows whose support is not listed
 constexpr int kLongScan = 0;    // the fill wrote their zeros: their support entries from the logits
 constexpr int kLongDense = 1;   // the fill left them alone: rewritten whole from the logits
 constexpr int kLongDone = 2;    // fwl_write_flat wrote them whole
@@ -2810,17 +2841,18 @@ __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
   const int wid = uniform((int)(threadIdx.x >> 6));
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
   for (int64_t r = (int64_t)blockIdx.x * kWavesPerBlock + wid; r < N; r += stride) {
-    const int kap = kap_in[r];
-    if (kap > kTwoPassCap && dense == kLongDone) continue;   // written whole by fwl_write_flat
+    const bool listed = two_pass_listed(kap_in[r]);
+    const int kap = two_pass_kappa(kap_in[r]);
+    if (!listed && dense == kLongDone) continue;   // written whole by fwl_write_flat
     const float Hf = Hin[r];
     const int64_t y64 = tgt[r];
     const int yr = (y64 >= 0 && y64 < C) ? (int)y64 : -1;
     const float inv = (float)(scale / (double)kap);
     const void* row = static_cast<const char*>(z) + r * ld * kElemBytes<T>;
     const int64_t g0 = r * (int64_t)C;
-    if (kap <= kTwoPassCap) {
-      if (lane < kap) {
-        const int id = cidx[r * (int64_t)kTwoPassCap + lane];
+    if (listed) {
+      for (int p = lane; p < kap; p += kWave) {
+        const int id = cidx[r * (int64_t)kTwoPassCap + p];
         if (id != yr) store_elem<T>(grad, g0 + id, inv);
       }
     } else if (dense) {
@@ -2873,9 +2905,9 @@ __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
 
 // fwl_write_flat: the two-pass op's gradient for rows of a whole number of 128-bit units, one
 // block per 4 KB of the [N, C] gradient, one 128-bit unit per thread, stored once:
-//   * rows of at most kTwoPassCap support entries: zeros (fwl_scatter_support then stores the
-//     listed support entries and the label element);
-//   * longer supports: the unit's logits are loaded and inv stored where z > H; the label element
+//   * rows whose support the read pass listed: zeros (fwl_scatter_support then stores the listed
+//     support entries and the label element);
+//   * other rows: the unit's logits are loaded and inv stored where z > H; the label element
 //     gets its scale subtracted in the same store.
 // Measured on MI355X over 1 GiB: zero stores reach 6.85 TB/s in 4 KB blocks of 256 threads, 6.80
 // with a load from a small cached array before them, against 5.5-5.8 TB/s from resident
@@ -2903,12 +2935,13 @@ __global__ __launch_bounds__(kBlock) void fwl_write_flat(
   // of >= 4 KB), of others per thread
   const int kap0 = kap_in[rb];
   const int kap1 = rb + 1 < N ? kap_in[rb + 1] : 0;
-  const int kap = r == rb ? kap0 : (r == rb + 1 ? kap1 : kap_in[r]);
+  const int kc = r == rb ? kap0 : (r == rb + 1 ? kap1 : kap_in[r]);
   const rsrc_t out = make_rsrc(static_cast<char*>(grad) + u0 * 16, (uint32_t)kWriteBytes);
-  if (kap <= kTwoPassCap) {
+  if (two_pass_listed(kc)) {
     store_zero_unit<T, true>(out, threadIdx.x);
     return;
   }
+  const int kap = two_pass_kappa(kc);
   float x[U];
   const rsrc_t in = make_rsrc(static_cast<const char*>(z) + r * ld * kElemBytes<T>, (uint32_t)(kElemBytes<T> * C));
   load_unit<T, true>(in, (uint32_t)q, x);
@@ -3201,21 +3234,23 @@ int launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const 
 size_t mean_ws_bytes(int64_t N);
 size_t ovf_ws_bytes(int64_t N);
 size_t two_pass_bytes(int64_t N);
-// The fused op in two passes: the candidate-list kernel (lists cut at kTwoPassCap, kept in the
-// workspace after the mean's part), then the write pass: fwl_write_flat and fwl_scatter_support
-// for rows of whole 128-bit units, else fwl_fill_zero and fwl_scatter_support.
+// The fused op in two passes: the candidate-list kernel (support indices of rows whose lists kept
+// them, at most kTwoPassCap per row, in the workspace after the mean's part), then the write
+// pass: fwl_write_flat and fwl_scatter_support for rows of whole 128-bit units, else
+// fwl_fill_zero and fwl_scatter_support.
 template <typename T, bool V4>
 int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, void* ws, size_t ws_bytes,
                     hipStream_t s) {
   char* base = static_cast<char*>(ws) + mean_ws_bytes(N) + ovf_ws_bytes(N);
   const size_t L = (size_t)N * kTwoPassCap;
   Outs o1 = o;
-  o1.cval = reinterpret_cast<float*>(base);
-  o1.cidx = reinterpret_cast<int32_t*>(base + sizeof(float) * L);
-  o1.ccnt = reinterpret_cast<int32_t*>(base + (sizeof(float) + sizeof(int32_t)) * L);
-  float* Hs = reinterpret_cast<float*>(base + (sizeof(float) + sizeof(int32_t)) * L + sizeof(int32_t) * (size_t)N);
+  o1.cval = nullptr;   // indices only
+  o1.cidx = reinterpret_cast<int32_t*>(base);
+  o1.ccnt = reinterpret_cast<int32_t*>(base + sizeof(int32_t) * L);
+  float* Hs = reinterpret_cast<float*>(base + sizeof(int32_t) * L + sizeof(int32_t) * (size_t)N);
   o1.cstride = kTwoPassCap;
   o1.ccap = kTwoPassCap;
+  o1.mark_unlisted = 1;
   if (o1.H == nullptr) o1.H = Hs;
   o1.grad = nullptr;
   // The read pass streams one row per wavefront when there are rows for kTwoPassWaveRowsPerCU
@@ -3240,7 +3275,7 @@ int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Out
   // leaves them alone, where rows are whole dwords and at least a fill block long
   const bool dense = row_bytes % 4 == 0 && row_bytes >= kFillBytes;
   hipLaunchKernelGGL(fwl_fill_zero, dim3((unsigned)fill_blocks), dim3(kBlock), 0, s, o.grad, bytes, row_bytes,
-                     dense ? o1.ccnt : nullptr, kTwoPassCap);
+                     dense ? o1.ccnt : nullptr);
   hipLaunchKernelGGL((fwl_scatter_support<T, V4>), dim3(blocks_wave(N)), dim3(kBlock), 0, s, z, o.ld, y, o1.H, o1.ccnt,
                      o1.cidx, N, C, o.scale, o.scale_f, o.grad, (bytes & 3) != 0, dense ? kLongDense : kLongScan);
   return grid;
@@ -3329,7 +3364,7 @@ constexpr int64_t kStreamMinRows16 = 1024;
 
 // the two passes' scratch: cut candidate lists (values, indices), kappa and H per row
 size_t two_pass_bytes(int64_t N) {
-  return (size_t)N * (kTwoPassCap * (sizeof(float) + sizeof(int32_t)) + sizeof(int32_t) + sizeof(float));
+  return (size_t)N * (kTwoPassCap * sizeof(int32_t) + sizeof(int32_t) + sizeof(float));
 }
 
 
@@ -3519,7 +3554,7 @@ int fused_forward(int dtype, const void* logits, int64_t ld, const int64_t* targ
 // symbol; its device address (one per device) comes from hipGetSymbolAddress and is the only
 // address passed to kernels.  The library keeps no state in a workspace between calls, so nothing
 // in it needs clearing; calls that overlap on one device share it and race.
-constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {

@@ -129,12 +129,12 @@ int fwl_forward_backward_ex(int dtype, const void* logits, int64_t ld, const int
  * serving loops, harnesses that forbid allocation).  No counterpart in the reference, whose ops
  * allocate their outputs and scratch (src/cuda/fw_radix_argmax.cu:1390-1393, :1426-1453).  The
  * caller passes the inputs and outputs; the workspace is a static device array of
- * fwl_noalloc_scratch_bytes() bytes (16 MiB) in the library, one per device, looked up once per
+ * fwl_noalloc_scratch_bytes() bytes (64 MiB) in the library, one per device, looked up once per
  * device.  Calls on one device share it: calls that overlap on one device (several streams or
  * threads at once) race and give undefined results.  A call whose workspace (fwl_workspace_bytes_ex
  * with the same options) exceeds the array returns FWL_ERR_WORKSPACE before any launch: the mean
- * and overflow records need about 8 bytes per row, many long rows 520 more (about 2M rows of short
- * rows, or 30000 rows of >= 32000 elements). */
+ * and overflow records need about 8 bytes per row, many long rows 2056 more (about 8M rows of short
+ * rows, or 32000 rows of >= 32000 elements). */
 size_t fwl_noalloc_scratch_bytes(void);
 int fwl_forward_backward_noalloc(int dtype, const void* logits, int64_t ld, const int64_t* targets,
                                  int64_t N, int64_t C, double scale, double reduce_div, float* H,

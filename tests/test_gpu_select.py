@@ -189,13 +189,17 @@ def list_mix(N, C, seed):
 @pytest.mark.parametrize("C", [4096, 4099, 20000])
 def test_two_pass_lists(ext, dev, reset_params, path, C):
     """2048 rows through the forced two-pass paths.  Rows of whole 128-bit units (C = 4096, 20000)
-    take the 4 KB-block write pass: zeros for rows of <= 64 support entries (the scatter kernel adds
-    their support), longer supports from the logits.  C = 4099 takes the fill and scatter kernels.
-    Path 3 sends every row through the overflow solve."""
+    take the 4 KB-block write pass: zeros for rows whose support the read pass listed (at most 512
+    entries, from a list that kept its indices; the scatter kernel adds them), the others from the
+    logits.  C = 4099 takes the fill and scatter kernels.  Path 3 sends every row through the
+    overflow solve.  The rows cover supports of a few, of 65-512 and of more than 512 entries."""
     z, y = list_mix(2048, C, seed=C + path)
     ext.set_params(path, 512)
     print(f"two-pass lists path={path} C={C}", flush=True)
-    assert_parity(fused(ext, *to_dev(dev, z, y)), oracle.definition(z, y), z)
+    ref = oracle.definition(z, y)
+    k = ref["kappa"]
+    assert (k <= 64).any() and ((k > 64) & (k <= 512)).any() and (k > 512).any()
+    assert_parity(fused(ext, *to_dev(dev, z, y)), ref, z)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -77,7 +77,7 @@ def test_workspace_bytes():
     # per-call options: the same sizes as the process-wide switches; out of range gives 0
     assert L.fwl_workspace_bytes_ex(65536, 1000, None) == ws_expect(65536)
     opt = capi.Options(2, 512)
-    assert L.fwl_workspace_bytes_ex(16, 1000, ctypes.byref(opt)) == ws_expect(16, 16 * (64 * 8 + 8))
+    assert L.fwl_workspace_bytes_ex(16, 1000, ctypes.byref(opt)) == ws_expect(16, 16 * (512 * 4 + 8))
     for bad in (capi.Options(9, 512), capi.Options(-1, 0), capi.Options(2, 63), capi.Options(2, 513)):
         assert L.fwl_workspace_bytes_ex(16, 1000, ctypes.byref(bad)) == 0
 
@@ -238,9 +238,9 @@ def test_workspace_sizes():
         assert W(65536, 8191) == ws_expect(65536)
         assert W(0, 131072) == ws_expect(0)
         # >= 384 rows of >= 32000 elements, or batches of >= 48M elements in rows of >= 8192 (the
-        # fp32 rules, which cover the 16-bit one) run the fused op in two passes: per row 64
-        # support values and indices, kappa and H
-        row = 64 * 8 + 4 + 4
+        # fp32 rules, which cover the 16-bit one) run the fused op in two passes: per row 512
+        # support indices, the read pass's count and H
+        row = 512 * 4 + 4 + 4
         assert W(2048, 131072) == ws_expect(2048, 2048 * row)
         assert W(384, 32000) == ws_expect(384, 384 * row)
         assert W(383, 32000) == ws_expect(383)

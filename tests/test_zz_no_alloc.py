@@ -81,8 +81,8 @@ def test_noalloc_16bit_and_strided(dev):
 def test_noalloc_refuses_sizes_beyond_the_scratch(dev):
     L = fwloss_capi.lib()
     cap = L.fwl_noalloc_scratch_bytes()
-    assert cap == 16 << 20
-    N = 3 << 20                                  # overflow records alone exceed 16 MiB
+    assert cap == 64 << 20
+    N = 12 << 20                                 # overflow records alone exceed 64 MiB
     assert L.fwl_workspace_bytes(N, 16) > cap
     rc = L.fwl_forward_backward_noalloc(0, P(0x10000), 16, P(0x10000), N, 16, 1.0, 1.0, None, None, None,
                                         P(0x10000), None, P(0x10000), None, None)
