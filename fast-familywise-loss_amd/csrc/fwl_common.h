@@ -207,6 +207,15 @@ __device__ __forceinline__ int lane_id() {
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// a 64-bit value the whole wavefront holds, in scalar registers (for row addresses that the
+// compiler cannot prove uniform, e.g. ones derived from LDS loads: buffer instructions with a
+// resource in vector registers are wrapped in loops over the distinct values)
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
 // number of set bits of b in lanes below this one

@@ -1192,12 +1192,12 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
     if (ballot(lm > st.t) == 0) {
       done = true;   // no candidate in this round (the common case)
     } else {
-      // per-lane counts and their prefix sum place each lane's entries: lane L appends its k-th
-      // entry at n + (entries of lanes < L) + k, and an entry not appended is written to the
-      // lane's trash slot (tr) instead, so the appends need no per-slot ballot or branch
       int lc = 0;
 #pragma unroll
       for (int i = 0; i < S; ++i) lc += a.x[i] > st.t ? 1 : 0;
+      // per-lane counts and their prefix sum place each lane's entries: lane L appends its k-th
+      // entry at n + (entries of lanes < L) + k, and an entry not appended is written to the
+      // lane's trash slot (tr) instead, so the appends need no per-slot ballot or branch
       int incl = scan_i32(lc);
       int cnt = __builtin_amdgcn_readlane(incl, kWave - 1);
       // a list that still has its indices is tightened before it gives them up
@@ -1224,17 +1224,30 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
       if (!st.ovf) {
         if (st.n + cnt > icap) st.noidx = true;
         int pos = st.n + incl - lc;
-        if (st.noidx) {
+        // the bound again, as a value the compiler does not match with the count's compares: the
+        // appends then compare into VCC rather than keep 16 lane masks in scalar registers
+        const float tw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(st.t)));
+        if (ballot(lc > 1) == 0) {
+          // a sparse round: no lane has more than one entry, which is then its maximum lm
+          const bool p = lc == 1;
+          *(p ? bv + pos : tr) = lm;
+          if (!st.noidx) {
+            int id = 0;
+#pragma unroll
+            for (int i = 0; i < S; ++i) id = a.x[i] == lm ? round_slot_index<W, T, VEC>(round, i, wid, lane) : id;
+            *(p ? bi + pos : reinterpret_cast<int*>(tr)) = id;
+          }
+        } else if (st.noidx) {
 #pragma unroll
           for (int i = 0; i < S; ++i) {
-            const bool p = a.x[i] > st.t;
+            const bool p = a.x[i] > tw;
             *(p ? bv + pos : tr) = a.x[i];
             pos += p ? 1 : 0;
           }
         } else {
 #pragma unroll
           for (int i = 0; i < S; ++i) {
-            const bool p = a.x[i] > st.t;
+            const bool p = a.x[i] > tw;
             *(p ? bv + pos : tr) = a.x[i];
             *(p ? bi + pos : reinterpret_cast<int*>(tr)) = round_slot_index<W, T, VEC>(round, i, wid, lane);
             pos += p ? 1 : 0;
@@ -2166,8 +2179,9 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
   Round<T, V4> first;
   if (nrows > 0) stream_first<1, T, V4>(row_at(0), C, lane, 0, first);
   for (int k = 0; k < nrows; ++k) {
-    const int64_t r = w + (int64_t)k * stride;
-    const void* row = row_at(k);
+    const int ku = uniform(k);   // (the compiler keeps the counter in a vector register)
+    const int64_t r = w + (int64_t)ku * stride;
+    const void* row = row_at(ku);
     const int64_t y64 = ((int64_t)__builtin_amdgcn_readlane((int)(my_y >> 32), k) << 32) |
                         (uint32_t)__builtin_amdgcn_readlane((int)my_y, k);
     const bool yok = y64 >= 0 && y64 < C;
@@ -2179,7 +2193,7 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
     stream_span<1, T, MODE, V4>(row, out_row, C, lane, 0, bv, bi, s_w[wid].trash + lane, vcap, icap, st, first);
-    if (k + 1 < nrows) stream_first<1, T, V4>(row_at(k + 1), C, lane, 0, first);
+    if (k + 1 < nrows) stream_first<1, T, V4>(row_at(ku + 1), C, lane, 0, first);
     double tau;
     int kappa;
     uint64_t support = 0;
@@ -2347,7 +2361,7 @@ __global__ __launch_bounds__(kBlock) void fwl_overflow_rows(const void* __restri
       while (pend[q] != 0) {
         const int64_t j = j0 + kWave * q + __builtin_ctzll(pend[q]);
         pend[q] &= pend[q] - 1;
-        solve(blockIdx.x + j * gridDim.x);
+        solve(uniform64(blockIdx.x + j * gridDim.x));   // (pend comes from LDS)
       }
     }
   }
