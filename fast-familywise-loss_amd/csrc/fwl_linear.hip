@@ -353,10 +353,18 @@ __global__ __launch_bounds__(kBlock) void fwl_lin_coo(const int64_t* __restrict_
   }
 }
 
-// dweight[j] = sum of g * hidden[row] over column j's entries, in key order (keys sorted).  One
-// wavefront per entry (strided over the grid); the wavefront at the first entry of a column does
-// the column.  Keys of column >= V (padding after the entries) are skipped.
+// dweight[j] = sum of g * hidden[row] over column j's entries, in key order (keys sorted): every
+// output element is one fma chain over the column's entries in that order.  The grid strides
+// over the entries.  The wavefront at a column's first entry finds the column's end (a galloping
+// then binary search over the keys) and, for a column of at most kLinShortColumn entries, does
+// the whole column.  A longer column (a frequent label, or many rows sharing support entries) is
+// split over the hidden dimension instead: the wavefronts at its first nw entries
+// (nw = min(units / 64, 64)) each take every nw-th group of 64 units, with the entries' keys and
+// values read through the scalar cache eight at a time and their hidden units loaded eight at a
+// time.  Keys of column >= V (padding after the entries) are skipped.
 constexpr int64_t kLinDweightBlocks = 65536;
+constexpr int64_t kLinShortColumn = 32;
+constexpr int kLinBatch = 8;
 
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kBlock) void fwl_lin_dweight(const void* __restrict__ hid, int64_t N, int64_t V, int d,
@@ -369,27 +377,77 @@ __global__ __launch_bounds__(kBlock) void fwl_lin_dweight(const void* __restrict
   const int64_t twoN = 2 * N;
   const uint32_t row_bytes = (uint32_t)(d * kElemBytes<T>);
   const int units = (d + U - 1) / U;
-  for (int64_t p0 = (int64_t)blockIdx.x * kWavesPerBlock + wid; p0 < P; p0 += (int64_t)gridDim.x * kWavesPerBlock) {
-    const int64_t j = keys[p0] / twoN;
+  const int groups = (units + kWave - 1) / kWave;        // groups of 64 units
+  const int nw = groups < kWave ? groups : kWave;         // wavefronts on a long column
+  auto col = [&](int64_t p) { return keys[p] / twoN; };
+  auto hrow = [&](int64_t p) {   // the entry's row of hidden (keys >= 0: 0 <= n < N)
+    const int64_t n = (keys[p] % twoN) / 2;
+    return make_rsrc(static_cast<const char*>(hid) + n * d * kElemBytes<T>, row_bytes);
+  };
+  for (int64_t p = (int64_t)blockIdx.x * kWavesPerBlock + wid; p < P; p += (int64_t)gridDim.x * kWavesPerBlock) {
+    const int64_t j = col(p);
     if (j >= V) break;                                       // padding: sorted after every entry
     if (j < 0) continue;                                     // not a column of weight
-    if (p0 > 0 && keys[p0 - 1] / twoN == j) continue;        // not the column's first entry
-    int64_t p1 = p0 + 1;
-    while (p1 < P && keys[p1] / twoN == j) ++p1;
+    // c: entries of the same column directly before p, counted up to nw (lane i looks at p - 1 - i)
+    const int64_t q = p - 1 - lane;
+    const uint64_t same = ballot(lane < nw && q >= 0 && col(q) == j);
+    const int c = (int)__builtin_ctzll(~same);
+    if (c >= nw) continue;                                   // deeper into its column: no work
+    const int64_t p0 = p - c;
+    // the column's end: galloping from p0, then a binary search
+    int64_t lo = p0, step = 1;
+    while (lo + step < P && col(lo + step) == j) {
+      lo += step;
+      step *= 2;
+    }
+    int64_t hi = lo + step < P ? lo + step : P;
+    while (hi - lo > 1) {
+      const int64_t mid = lo + (hi - lo) / 2;
+      if (col(mid) == j) lo = mid;
+      else hi = mid;
+    }
+    const int64_t p1 = hi;
     const rsrc_t out = make_rsrc(static_cast<char*>(dW) + j * d * kElemBytes<T>, row_bytes);
-    for (int u = lane; u - lane < units; u += kWave) {
+    if (p1 - p0 <= kLinShortColumn) {
+      if (c != 0) continue;
+      for (int u = lane; u - lane < units; u += kWave) {
+        float acc[U];
+#pragma unroll
+        for (int e = 0; e < U; ++e) acc[e] = 0.0f;
+        for (int64_t pp = p0; pp < p1; ++pp) {
+          const float gv = vals[pp];
+          float h[U];
+          load_unit<T, VEC>(hrow(pp), (uint32_t)u, h);
+#pragma unroll
+          for (int e = 0; e < U; ++e) acc[e] = fmaf(gv, h[e], acc[e]);
+        }
+        store_unit<T, VEC>(out, (uint32_t)u, acc);
+      }
+      continue;
+    }
+    // a long column: unit groups c, c + nw, ... of it (offsets past the row read 0, stores dropped)
+    for (int gi = c; gi < groups; gi += nw) {
+      const uint32_t u = (uint32_t)(kWave * gi + lane);
       float acc[U];
 #pragma unroll
       for (int e = 0; e < U; ++e) acc[e] = 0.0f;
-      for (int64_t p = p0; p < p1; ++p) {
-        const int64_t n = (keys[p] % twoN) / 2;   // keys >= 0: 0 <= n < N
-        const float gv = vals[p];
-        float h[U];
-        load_unit<T, VEC>(make_rsrc(static_cast<const char*>(hid) + n * d * kElemBytes<T>, row_bytes), (uint32_t)u, h);
+      for (int64_t pb = p0; pb < p1; pb += kLinBatch) {
+        float h[kLinBatch][U];
+        float gv[kLinBatch];
 #pragma unroll
-        for (int e = 0; e < U; ++e) acc[e] = fmaf(gv, h[e], acc[e]);
+        for (int k = 0; k < kLinBatch; ++k) {
+          const bool in = pb + k < p1;
+          gv[k] = in ? vals[pb + k] : 0.0f;
+          load_unit<T, VEC>(in ? hrow(pb + k) : make_rsrc(hid, 0u), u, h[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < kLinBatch; ++k) {
+          if (pb + k >= p1) break;
+#pragma unroll
+          for (int e = 0; e < U; ++e) acc[e] = fmaf(gv[k], h[k][e], acc[e]);
+        }
       }
-      store_unit<T, VEC>(out, (uint32_t)u, acc);
+      store_unit<T, VEC>(out, u, acc);
     }
   }
 }

@@ -209,6 +209,38 @@ def test_grads_unaligned_hidden_size(dev, dt):
     close(ww.grad, dw_ref, TOL[dt])
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("labels", ["one", "zipf"])
+@pytest.mark.parametrize("d", [64, 37, 4160])
+def test_grads_skewed_labels(dev, dt, labels, d):
+    """Columns of weight with many entries (every row labelled with the same column, or Zipf
+    labels whose most frequent column takes about a third of the rows): the weight gradient
+    splits a long column over the hidden dimension, several wavefronts per column, each output
+    still one fma chain over the column's entries in key order (d = 4160 fp32: 17 groups of 64
+    units; d = 37: element-wise units)."""
+    import fwloss
+    N, V, chunk = 600, 3000, 1000
+    h, w, y = make(dev, N, d, V, dt, seed=23 + d)
+    if labels == "one":
+        y = torch.full_like(y, 5)
+    else:
+        u = np.random.default_rng(d).random(N)
+        y = torch.from_numpy(np.minimum(np.floor(u ** -1.2).astype(np.int64) - 1, V - 1)).to(dev)
+    print(f"skewed labels {labels} {dt} d={d} max count {int(torch.bincount(y).max())}", flush=True)
+    hh = h.clone().requires_grad_(True)
+    ww = w.clone().requires_grad_(True)
+    fwloss.familywise_linear_loss(hh, ww, y, "sum", chunk).backward()
+    z = chunk_logits(h, w, chunk).float().cpu().numpy()
+    _, dh_ref, dw_ref = dense_grads(z, y.cpu().numpy(), h, w, np.ones(N))
+    close(hh.grad, dh_ref, TOL[dt])
+    close(ww.grad, dw_ref, TOL[dt])
+    # the same call again gives the same bits (a fixed order of every sum)
+    ww2 = w.clone().requires_grad_(True)
+    fwloss.familywise_linear_loss(h, ww2, y, "sum", chunk).backward()
+    assert torch.equal(ww.grad.view(torch.int16 if ww.grad.element_size() == 2 else torch.int32),
+                       ww2.grad.view(torch.int16 if ww2.grad.element_size() == 2 else torch.int32))
+
+
 def test_only_hidden_needs_grad(dev):
     import fwloss
     N, d, V, chunk = 64, 32, 1000, 300
