@@ -3085,13 +3085,13 @@ int device_cus() {
 // the blocks per CU set the number of concurrent row streams.  Measured on MI355X with 4000-byte
 // rows: two blocks per CU (8 wavefronts, ~64 KB in flight per CU) stream best; more concurrent
 // streams over a wider address window lose DRAM efficiency.  Shorter rows (in bytes) get
-// proportionally more blocks, up to the resident limit.  At most kRowsPerWave rows per wavefront:
-// larger N gets more (queued) blocks.
-int wave_grid(int64_t N, int64_t row_bytes, int resident) {
+// proportionally more blocks, up to the resident limit; longer rows at least min_per_cu blocks.
+// At most kRowsPerWave rows per wavefront: larger N gets more (queued) blocks.
+int wave_grid(int64_t N, int64_t row_bytes, int resident, int min_per_cu = 2) {
   const int cus = device_cus();
   const int per_cu_resident = cus > 0 && resident > 0 ? resident / cus : 0;
   int per_cu = (int)((8000 + row_bytes - 1) / (row_bytes > 0 ? row_bytes : 1));
-  if (per_cu < 2) per_cu = 2;
+  if (per_cu < min_per_cu) per_cu = min_per_cu;
   if (per_cu_resident > 0 && per_cu > per_cu_resident) per_cu = per_cu_resident;
   const int target = cus > 0 ? per_cu * cus : (resident > 0 ? resident : kMaxBlocksWave);
   const int64_t min_blocks = (N + (int64_t)kWavesPerBlock * kRowsPerWave - 1) / ((int64_t)kWavesPerBlock * kRowsPerWave);
@@ -3105,7 +3105,11 @@ int wave_grid(int64_t N, int64_t row_bytes, int resident) {
 template <typename T, int MODE, int NV, bool V4, bool AW = false>
 int launch_wave(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   const void* k = reinterpret_cast<const void*>(&fwl_wave_rows<T, MODE, NV, V4, AW>);
-  const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
+  // fp32 register rows of >= 8000 bytes stream best from one block per CU (65536 x 2000: 184.8
+  // against 196.9 us with two; 32768 x 2048: 95.7 against 97.7); 6000-7999 bytes gain nothing,
+  // and 16-bit rows, bound by instruction issue, lose with fewer wavefronts
+  const int64_t row_bytes = (int64_t)C * kElemBytes<T>;
+  const int grid = wave_grid(N, row_bytes, resident_blocks(k), kElemBytes<T> == 4 && row_bytes >= 8000 ? 1 : 2);
   hipLaunchKernelGGL((fwl_wave_rows<T, MODE, NV, V4, AW>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
   return grid;
 }
