@@ -218,6 +218,14 @@ __device__ __forceinline__ int64_t uniform64(int64_t x) {
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
+// make_rsrc for a base address and size that the whole wavefront shares, forced into scalar
+// registers (the compiler may hold a row pointer derived from a spilled kernel argument in vector
+// registers; a buffer instruction with such a resource runs in a loop over its distinct values)
+__device__ __forceinline__ rsrc_t make_rsrc_u(const void* base, uint32_t bytes) {
+  const int64_t b = uniform64(reinterpret_cast<int64_t>(base));
+  return make_rsrc(reinterpret_cast<const void*>(b), (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes));
+}
+
 // number of set bits of b in lanes below this one
 __device__ __forceinline__ int rank_in(uint64_t b) {
   return __builtin_amdgcn_mbcnt_hi((unsigned)(b >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)b, 0u));

@@ -1275,7 +1275,7 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
 // the first round of a row (or stretch), loaded ahead of stream_span (C = 0: no row, no traffic)
 template <int W, typename T, bool VEC>
 __device__ __forceinline__ void stream_first(const void* __restrict__ row, int C, int lane, int wid, Round<T, VEC>& a) {
-  load_round<W, T, VEC>(make_rsrc(row, (uint32_t)(kElemBytes<T> * C)), 0, wid, lane, a);
+  load_round<W, T, VEC>(make_rsrc_u(row, (uint32_t)(kElemBytes<T> * C)), 0, wid, lane, a);
 }
 
 // Stream this wavefront's share of a row (or of a stretch of one: `row`, `out_row` and C narrowed
@@ -1289,10 +1289,10 @@ __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* 
   constexpr int per_round = kWave * W * Round<T, VEC>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
-  const rsrc_t in = make_rsrc(row, row_bytes);
+  const rsrc_t in = make_rsrc_u(row, row_bytes);
   rsrc_t out = make_rsrc(nullptr, 0u);
-  if constexpr (MODE == kGrad) out = make_rsrc(out_row, row_bytes);
-  else if constexpr (MODE == kMask) out = make_rsrc(out_row, (uint32_t)C);
+  if constexpr (MODE == kGrad) out = make_rsrc_u(out_row, row_bytes);
+  else if constexpr (MODE == kMask) out = make_rsrc_u(out_row, (uint32_t)C);
   Round<T, VEC> b;
   // stores to a zero-size resource (no traffic) so that the wait counts on entry match those of
   // the loop's back edge (a round's loads, then a round's stores)
@@ -1301,11 +1301,11 @@ __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* 
   __builtin_amdgcn_sched_barrier(0);
   int k = 0;
   while (true) {
-    load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, b);
+    load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc_u(row, 0u), k + 1, wid, lane, b);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
     scan_round<W, T, VEC>(a, k, C, wid, lane, bv, bi, tr, cap, icap, st);
     if (++k >= rounds) break;
-    load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc(row, 0u), k + 1, wid, lane, a);
+    load_round<W, T, VEC>(k + 1 < rounds ? in : make_rsrc_u(row, 0u), k + 1, wid, lane, a);
     zero_round<W, T, MODE, VEC>(out, k, wid, lane);
     scan_round<W, T, VEC>(b, k, C, wid, lane, bv, bi, tr, cap, icap, st);
     if (++k >= rounds) break;
@@ -1540,8 +1540,8 @@ __device__ __forceinline__ void row_pass(const void* row, int C, int lane, int w
   constexpr int S = Round<T, VEC>::kSlots;
   constexpr int per_round = kWave * W * S;
   const int rounds = (C + per_round - 1) / per_round;
-  const rsrc_t in = make_rsrc(row, (uint32_t)(kElemBytes<T> * C));
-  const rsrc_t none = make_rsrc(row, 0u);
+  const rsrc_t in = make_rsrc_u(row, (uint32_t)(kElemBytes<T> * C));
+  const rsrc_t none = make_rsrc_u(row, 0u);
   auto process = [&](Round<T, VEC>& a, int k) {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -1944,7 +1944,7 @@ __device__ void write_support(const void* row, int64_t r, int C, int yr, float H
     constexpr int S = Round<T, VEC>::kSlots;
     constexpr int per_round = kWave * W * S;
     const int rounds = (C + per_round - 1) / per_round;
-    const rsrc_t in = make_rsrc(row, (uint32_t)(kElemBytes<T> * C));
+    const rsrc_t in = make_rsrc_u(row, (uint32_t)(kElemBytes<T> * C));
     float* cv = o.cval != nullptr ? o.cval + r * (int64_t)o.cstride : nullptr;   // null: indices only
     int32_t* ci = o.cidx + r * (int64_t)o.cstride;
     int base = 0;
@@ -2876,8 +2876,8 @@ __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
       constexpr int U = kUnit<T, V4>;
       constexpr int per_round = kWave * Round<T, V4>::kSlots;
       const int rounds = (C + per_round - 1) / per_round;
-      const rsrc_t in = make_rsrc(row, (uint32_t)(kElemBytes<T> * C));
-      const rsrc_t none = make_rsrc(row, 0u);
+      const rsrc_t in = make_rsrc_u(row, (uint32_t)(kElemBytes<T> * C));
+      const rsrc_t none = make_rsrc_u(row, 0u);
       const rsrc_t out = make_rsrc(static_cast<char*>(grad) + g0 * kElemBytes<T>, (uint32_t)(kElemBytes<T> * C));
       const uint32_t b_inv = encode<T>(inv);
       auto emit = [&](const Round<T, V4>& a, int k) {
