@@ -1090,6 +1090,8 @@ struct StreamState {
   int acc_c;      // (per lane)
   int ylab;       // an element index of the span whose value is kept in zy as it streams by (-1: none)
   float zy;
+  int sh;         // elements of the streamed window in front of the row (a window that starts on a
+                  // 4-byte boundary before a 16-bit row of odd start; 0 otherwise)
 };
 
 __device__ __forceinline__ StreamState stream_state(bool force) {
@@ -1104,6 +1106,7 @@ __device__ __forceinline__ StreamState stream_state(bool force) {
   st.acc_c = 0;
   st.ylab = -1;
   st.zy = NAN;
+  st.sh = 0;
   return st;
 }
 
@@ -1173,7 +1176,7 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
     if (b != 0) st.zy = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)__builtin_ctzll(b)));
   }
   float lm = -INFINITY;
-  if ((round + 1) * kRoundElems <= C) {
+  if ((round + 1) * kRoundElems <= C && (round > 0 || st.sh == 0)) {
     // a round inside the row: nothing to mask
 #pragma unroll
     for (int i = 0; i < S; ++i) lm = fmaxf(lm, a.x[i]);
@@ -1181,7 +1184,7 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int j = round_slot_index<W, T, VEC>(round, i, wid, lane);
-      a.x[i] = j < C ? a.x[i] : -INFINITY;
+      a.x[i] = j < C && j >= st.sh ? a.x[i] : -INFINITY;
       lm = fmaxf(lm, a.x[i]);
     }
   }
@@ -1234,7 +1237,8 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
           if (!st.noidx) {
             int id = 0;
 #pragma unroll
-            for (int i = 0; i < S; ++i) id = a.x[i] == lm ? round_slot_index<W, T, VEC>(round, i, wid, lane) : id;
+            for (int i = 0; i < S; ++i)
+              id = a.x[i] == lm ? round_slot_index<W, T, VEC>(round, i, wid, lane) - st.sh : id;
             *(p ? bi + pos : reinterpret_cast<int*>(tr)) = id;
           }
         } else if (st.noidx) {
@@ -1249,7 +1253,7 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
           for (int i = 0; i < S; ++i) {
             const bool p = a.x[i] > tw;
             *(p ? bv + pos : tr) = a.x[i];
-            *(p ? bi + pos : reinterpret_cast<int*>(tr)) = round_slot_index<W, T, VEC>(round, i, wid, lane);
+            *(p ? bi + pos : reinterpret_cast<int*>(tr)) = round_slot_index<W, T, VEC>(round, i, wid, lane) - st.sh;
             pos += p ? 1 : 0;
           }
         }
@@ -1272,16 +1276,26 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
   }
 }
 
+// bytes of the resource of a streamed row (or window) of C elements: 128-bit rounds take whole
+// dwords (the buffer range check is per dword), so a 16-bit window of odd length takes the dword
+// that holds its last element (its other half is masked; a dword never crosses a page)
+template <typename T, bool VEC>
+__device__ __forceinline__ uint32_t stream_bytes(int C) {
+  const uint32_t b = (uint32_t)(kElemBytes<T> * C);
+  return VEC ? (b + 3u) & ~3u : b;
+}
+
 // the first round of a row (or stretch), loaded ahead of stream_span (C = 0: no row, no traffic)
 template <int W, typename T, bool VEC>
 __device__ __forceinline__ void stream_first(const void* __restrict__ row, int C, int lane, int wid, Round<T, VEC>& a) {
-  load_round<W, T, VEC>(make_rsrc_u(row, (uint32_t)(kElemBytes<T> * C)), 0, wid, lane, a);
+  load_round<W, T, VEC>(make_rsrc_u(row, stream_bytes<T, VEC>(C)), 0, wid, lane, a);
 }
 
 // Stream this wavefront's share of a row (or of a stretch of one: `row`, `out_row` and C narrowed
 // to it) once: loads run one round ahead of the candidate scan, and every dense output element
 // (gradient or mask; `out_row` null in candidate-list mode) gets its zero placeholder.  `a` holds
-// the first round, from stream_first.
+// the first round, from stream_first.  With st.sh > 0 (candidate-list mode only), `row` is the
+// start of a window st.sh elements before the row and C the window's length.
 template <int W, typename T, int MODE, bool VEC>
 __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* out_row, int C, int lane, int wid,
                                             float* bv, int* bi, float* tr, int cap, int icap,
@@ -1289,7 +1303,7 @@ __device__ __forceinline__ void stream_span(const void* __restrict__ row, void* 
   constexpr int per_round = kWave * W * Round<T, VEC>::kSlots;   // elements per round of the row
   const int rounds = (C + per_round - 1) / per_round;
   const uint32_t row_bytes = (uint32_t)(kElemBytes<T> * C);
-  const rsrc_t in = make_rsrc_u(row, row_bytes);
+  const rsrc_t in = make_rsrc_u(row, stream_bytes<T, VEC>(C));
   rsrc_t out = make_rsrc(nullptr, 0u);
   if constexpr (MODE == kGrad) out = make_rsrc_u(out_row, row_bytes);
   else if constexpr (MODE == kMask) out = make_rsrc_u(out_row, (uint32_t)C);
@@ -1983,6 +1997,16 @@ __device__ void write_support(const void* row, int64_t r, int C, int yr, float H
   }
 }
 
+// 16-bit rows of odd start in candidate-list mode (the two-pass op's read pass) stream a window
+// from the 4-byte boundary below the row, one element longer (every dword of the 128-bit loads
+// then lies in the window; the element in front of the row is masked): win_shift is that element
+// count (0 or 1), 0 for every other row.  Nothing is stored through the window.
+template <typename T, int MODE, bool V4>
+__device__ __forceinline__ int win_shift(const void* row) {
+  if constexpr (MODE == kCand && V4 && kElemBytes<T> == 2) return (int)((reinterpret_cast<uintptr_t>(row) >> 1) & 1);
+  else return 0;
+}
+
 // (BIG: the long lists of BlockSharedBig, in candidate-list mode; a row one of whose wavefronts'
 // lists outgrew its indices has its support, where the caller wants it listed, written from one
 // more pass over the row)
@@ -2000,7 +2024,11 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
   // the first round of the next row is loaded before this row is resolved, so that the stream of
   // every row after the first starts with its loads in flight
   Round<T, V4> first;
-  if (blockIdx.x < N) stream_first<kWavesPerBlock, T, V4>(row_at(blockIdx.x), C, lane, wid, first);
+  auto first_round = [&](const void* p) {
+    const int ws = win_shift<T, MODE, V4>(p);
+    stream_first<kWavesPerBlock, T, V4>(static_cast<const char*>(p) - kElemBytes<T> * ws, C + ws, lane, wid, first);
+  };
+  if (blockIdx.x < N) first_round(row_at(blockIdx.x));
   const SelMem sm = {nullptr, nullptr, nullptr, 0, 0, sh.red_s, sh.red_c, nullptr};
   for (int64_t r = blockIdx.x; r < N; r += gridDim.x) {
     const void* row = row_at(r);
@@ -2014,11 +2042,12 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
     const int vcap = BIG && o.cap >= kCapMax ? kWaveVCap : o.cap;
 
     StreamState st = stream_state(o.force_generic != 0);
+    st.sh = win_shift<T, MODE, V4>(row);
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-    stream_span<kWavesPerBlock, T, MODE, V4>(row, out_row, C, lane, wid, bv, bi, sh.trash[wid] + lane, vcap, o.cap, st,
-                                             first);
+    stream_span<kWavesPerBlock, T, MODE, V4>(static_cast<const char*>(row) - kElemBytes<T> * st.sh, out_row, C + st.sh,
+                                             lane, wid, bv, bi, sh.trash[wid] + lane, vcap, o.cap, st, first);
     if constexpr (BIG) pad_list(bv, st.n, lane);
     if (lane == 0) {
       sh.wmax[wid] = st.m;
@@ -2031,7 +2060,7 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
       // every wavefront's zero placeholders have landed before any support entry is rewritten
       wait_vmem();
     }
-    if (rn < N) stream_first<kWavesPerBlock, T, V4>(row_at(rn), C, lane, wid, first);
+    if (rn < N) first_round(row_at(rn));
     __syncthreads();
     const bool overflow = sh.ovf[0] | sh.ovf[1] | sh.ovf[2] | sh.ovf[3];
 
@@ -2177,7 +2206,11 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
   auto row_at = [&](int k) { return static_cast<const char*>(z) + (w + (int64_t)k * stride) * o.ld * kElemBytes<T>; };
   // the next row's first round is loaded before this row is resolved (see fwl_block_rows)
   Round<T, V4> first;
-  if (nrows > 0) stream_first<1, T, V4>(row_at(0), C, lane, 0, first);
+  auto first_round = [&](const void* p) {
+    const int ws = win_shift<T, MODE, V4>(p);
+    stream_first<1, T, V4>(static_cast<const char*>(p) - kElemBytes<T> * ws, C + ws, lane, 0, first);
+  };
+  if (nrows > 0) first_round(row_at(0));
   for (int k = 0; k < nrows; ++k) {
     const int ku = uniform(k);   // (the compiler keeps the counter in a vector register)
     const int64_t r = w + (int64_t)ku * stride;
@@ -2188,12 +2221,14 @@ __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __res
     const int yr = yok ? (int)y64 : -1;
 
     StreamState st = stream_state(o.force_generic != 0);
-    st.ylab = yr;   // the label's logit, taken from the stream (no dependent load at the row's end)
+    st.sh = win_shift<T, MODE, V4>(row);
+    st.ylab = yr >= 0 ? yr + st.sh : -1;   // the label's logit, taken from the stream (window index)
     void* out_row = nullptr;
     if constexpr (MODE == kGrad) out_row = static_cast<char*>(o.grad) + r * (int64_t)C * kElemBytes<T>;
     else if constexpr (MODE == kMask) out_row = o.mask + r * (int64_t)C;
-    stream_span<1, T, MODE, V4>(row, out_row, C, lane, 0, bv, bi, s_w[wid].trash + lane, vcap, icap, st, first);
-    if (k + 1 < nrows) stream_first<1, T, V4>(row_at(ku + 1), C, lane, 0, first);
+    stream_span<1, T, MODE, V4>(static_cast<const char*>(row) - kElemBytes<T> * st.sh, out_row, C + st.sh, lane, 0,
+                                bv, bi, s_w[wid].trash + lane, vcap, icap, st, first);
+    if (k + 1 < nrows) first_round(row_at(ku + 1));
     double tau;
     int kappa;
     uint64_t support = 0;
@@ -3233,20 +3268,22 @@ int launch_overflow(const void* z, const int64_t* y, int64_t N, int C, Outs o, i
   return grid;
 }
 
-template <typename T, int MODE, bool V4, bool BIG = false>
+// (OV4: the access width of the overflow kernel after the stream, which reads rows from their
+// own start: 16-bit rows that the stream read through windows take 16-bit accesses there)
+template <typename T, int MODE, bool V4, bool BIG = false, bool OV4 = V4>
 int launch_block(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   const void* k = reinterpret_cast<const void*>(&fwl_block_rows<T, MODE, V4, BIG>);
   const int grid = persistent_grid(N, 1, resident_blocks(k), kMaxBlocksRow);
   hipLaunchKernelGGL((fwl_block_rows<T, MODE, V4, BIG>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
-  return grid + launch_overflow<T, MODE, V4>(z, y, N, C, o, grid, s);
+  return grid + launch_overflow<T, MODE, OV4>(z, y, N, C, o, grid, s);
 }
 
-template <typename T, int MODE, bool V4>
+template <typename T, int MODE, bool V4, bool OV4 = V4>
 int launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
   const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<T, MODE, V4>);
   const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
   hipLaunchKernelGGL((fwl_wave_stream_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
-  return grid + launch_overflow<T, MODE, V4>(z, y, N, C, o, grid, s);
+  return grid + launch_overflow<T, MODE, OV4>(z, y, N, C, o, grid, s);
 }
 
 size_t mean_ws_bytes(int64_t N);
@@ -3275,9 +3312,16 @@ int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Out
   // wavefronts per CU (8192 x 32000: 178 us against 206 us with one block per row), else one row
   // per block (520 x 128256: 181 us with one row per wavefront, 119 us per block), both with long
   // lists.
+  // 16-bit rows without 128-bit units (odd lengths or strides) are read one row per wavefront
+  // through windows from the 4-byte boundary below each row (win_shift), their overflow solve with
+  // 16-bit elements; read one row per block they stay on 16-bit elements (windows measured slower
+  // there at N(0, 0.01^2): 600 x 65537 bf16 166 against 78 us)
+  constexpr bool kWin = !V4 && kElemBytes<T> == 2;
   int grid;
-  if (N >= kTwoPassWaveRowsPerCU * (int64_t)device_cus()) grid = launch_wave_stream<T, kCand, V4>(z, y, N, C, o1, s);
-  else grid = launch_block<T, kCand, V4, true>(z, y, N, C, o1, s);
+  if (N >= kTwoPassWaveRowsPerCU * (int64_t)device_cus())
+    grid = launch_wave_stream<T, kCand, V4 || kWin, V4>(z, y, N, C, o1, s);
+  else
+    grid = launch_block<T, kCand, V4, true>(z, y, N, C, o1, s);
   const int64_t row_bytes = (int64_t)C * kElemBytes<T>;
   if (V4 && row_bytes % 16 == 0) {
     const int64_t wb = (N * row_bytes + kWriteBytes - 1) / kWriteBytes;
@@ -3489,9 +3533,15 @@ int forward(const void* z, int64_t ld, const int64_t* y, int64_t N, int64_t C64,
     }
   }
   const bool two_pass_ok = MODE == kGrad && aligned(o.grad, 4) && ws_have >= ws_head + two_pass_bytes(N);
+  // 16-bit rows without 128-bit units (odd lengths or strides), long and many: the two-pass op,
+  // whose read pass takes them through windows with 128-bit loads (bf16 2048 x 50257: 188 -> 100 us,
+  // 8192 x 32001: 414 -> 238; the same at N(0, 0.01^2); fewer rows read one block per row, which
+  // lost at N(0, 0.01^2): 512 x 50257 140 against 70)
+  const bool win16 = kElemBytes<T> == 2 && !v4 && C >= kTwoPassMinC &&
+                     N >= kTwoPassWaveRowsPerCU * (int64_t)device_cus();
   if (path == 0 && !aligned_rows && C <= 128) path = 6;   // short unaligned rows: 32-bit segments
   if (path == 0) {
-    const bool two_pass = two_pass_ok && two_pass_rows(N, C, kElemBytes<T>, 0);
+    const bool two_pass = two_pass_ok && (two_pass_rows(N, C, kElemBytes<T>, 0) || win16);
     const bool stream = C <= kMaxStreamC || (kElemBytes<T> == 2 && C <= kMaxStreamC16 && N >= kStreamMinRows16);
     path = C <= max_wave_c ? 6 : (two_pass ? 2 : (stream ? 4 : 2));
   }
@@ -3505,7 +3555,7 @@ int forward(const void* z, int64_t ld, const int64_t* y, int64_t N, int64_t C64,
   } else if (path == 4 || path == 5) {
     grid = v4 ? launch_wave_stream<T, MODE, true>(z, y, N, C, o, s) : launch_wave_stream<T, MODE, false>(z, y, N, C, o, s);
   } else if (path >= 0) {
-    if (two_pass_ok && two_pass_rows(N, C, kElemBytes<T>, p.path)) {
+    if (two_pass_ok && (two_pass_rows(N, C, kElemBytes<T>, p.path) || (p.path == 0 && win16))) {
       grid = v4 ? launch_two_pass<T, true>(z, y, N, C, o, ws, ws_have, s)
                 : launch_two_pass<T, false>(z, y, N, C, o, ws, ws_have, s);
     } else {

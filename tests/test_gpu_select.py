@@ -203,6 +203,25 @@ def test_two_pass_lists(ext, dev, reset_params, path, C):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_two_pass_odd_16bit_windows(ext, dev, reset_params, dtype):
+    """16-bit rows of odd length, long and many (2048 x 32001): the default dispatch takes the
+    two-pass op, whose read pass streams every row through a window from the 4-byte boundary below
+    it with 128-bit loads (the element in front of the row masked, the last dword whole)."""
+    z, y = list_mix(2048, 32001, seed=11)
+    z16 = torch.from_numpy(z).to(dtype)
+    z32 = z16.float().numpy()
+    ref = oracle.definition(z32, y)
+    ext.set_params(0, 512)
+    print(f"two-pass odd 16-bit windows {dtype}", flush=True)
+    H, loss, mean, kappa, grad = ext.fw_forward_backward(z16.to(dev), torch.from_numpy(y).to(dev))
+    torch.cuda.synchronize()
+    assert_parity(dict(H=H.cpu().numpy(), loss=loss.cpu().numpy(), kappa=kappa.cpu().numpy(), mean=float(mean.cpu())),
+                  ref, z32)
+    g16 = torch.from_numpy(ref["grad"]).to(dtype)
+    assert torch.equal(grad.cpu().view(torch.int16), g16.view(torch.int16)), "grad not bit-identical"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("path", [2, 3])
 @pytest.mark.parametrize("C", [4096, 4097])
 def test_two_pass_lists_16bit(ext, dev, reset_params, dtype, path, C):
