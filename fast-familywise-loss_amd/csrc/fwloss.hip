@@ -1554,7 +1554,7 @@ __device__ __forceinline__ void row_pass(const void* row, int C, int lane, int w
   constexpr int S = Round<T, VEC>::kSlots;
   constexpr int per_round = kWave * W * S;
   const int rounds = (C + per_round - 1) / per_round;
-  const rsrc_t in = make_rsrc_u(row, (uint32_t)(kElemBytes<T> * C));
+  const rsrc_t in = make_rsrc_u(row, stream_bytes<T, VEC>(C));
   const rsrc_t none = make_rsrc_u(row, 0u);
   auto process = [&](Round<T, VEC>& a, int k) {
 #pragma unroll
@@ -2934,6 +2934,16 @@ __global__ __launch_bounds__(kBlock) void fwl_scatter_support(
         emit(b, k + 1);
       }
       wait_vmem();   // the label element below is stored over its value here
+    } else if constexpr (!V4 && kElemBytes<T> == 2) {
+      // a support longer than the list, 16-bit row without 128-bit units: its entries from the
+      // logits (the fill wrote the zeros), streamed with 128-bit loads through a window from the
+      // 4-byte boundary below the row (see win_shift), two rounds in flight
+      const int ws = (int)((reinterpret_cast<uintptr_t>(row) >> 1) & 1);
+      row_pass<1, T, true, true>(static_cast<const char*>(row) - kElemBytes<T> * ws, C + ws, lane, 0,
+                                 [&](float zj, int jw) {
+                                   const int j = jw - ws;
+                                   if (j >= 0 && zj > Hf && j != yr) store_elem<T>(grad, g0 + j, inv);
+                                 });
     } else {
       // a support longer than the list: its entries from the logits (the fill wrote the zeros),
       // the row streamed in 128-bit units with two rounds in flight
