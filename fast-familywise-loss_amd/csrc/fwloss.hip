@@ -992,10 +992,18 @@ static_assert(sizeof(unsigned) * kHistBlock + sizeof(double) * kHistBlock <= 8 *
 // comes from them) and writes its support from one more pass over the row (the two-pass op's
 // write pass): rows of low-variance logits (hundreds to thousands of support entries) then need
 // no overflow solve.  49 KB of LDS per block (lists and trash slots): three blocks per CU.
+// The two-pass op's read pass holds kStreamVCapLong values per list (66.5 KB per block, two
+// blocks per CU, enough for one row per wavefront at 2048 rows of the chip's 256 CUs): a list
+// that is full before its row ends is tightened, and at N(0, 0.001^2) rows of 131072 elements
+// (supports of about 2700) a 3072-value list took about 11 tightenings per row, a 4096-value one
+// about 5 (2048 x 131072: 607 -> 582 us per step; 4864 values: no better).
 constexpr int kWaveVCap = 3072;
+constexpr int kStreamVCapLong = 4096;
 static_assert(kWaveVCap >= 2 * kCapMax && kWaveVCap % (4 * kWave) == 0, "indices share the value list");
+static_assert(kStreamVCapLong >= 2 * kCapMax && kStreamVCapLong % (4 * kWave) == 0, "indices share the value list");
+template <int CAP>
 struct alignas(16) WaveShared {
-  float val[kWaveVCap];
+  float val[CAP];
   float trash[kWave];   // each lane's sink for the list appends it does not make
 };
 
@@ -1241,6 +1249,36 @@ __device__ __forceinline__ void scan_round(Round<T, VEC>& a, int round, int C, i
               id = a.x[i] == lm ? round_slot_index<W, T, VEC>(round, i, wid, lane) - st.sh : id;
             *(p ? bi + pos : reinterpret_cast<int*>(tr)) = id;
           }
+        } else if (ballot(lc > 2) == 0) {
+          // at most two entries per lane: its first and its last entry in slot order (the same
+          // entry when it has one), so the list's order is that of the per-slot appends below
+          // (2048 x 131072 at N(0, 0.001^2): most rounds after the first few dozen)
+          auto pair = [&](auto idx) {
+            constexpr bool IDX = decltype(idx)::value;
+            float fv = 0.0f, lv = 0.0f;
+            int fs = 0, ls = 0;
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+              const bool p = a.x[i] > tw;
+              lv = p ? a.x[i] : lv;
+              if constexpr (IDX) ls = p ? i : ls;
+            }
+#pragma unroll
+            for (int i = S - 1; i >= 0; --i) {
+              const bool p = a.x[i] > tw;
+              fv = p ? a.x[i] : fv;
+              if constexpr (IDX) fs = p ? i : fs;
+            }
+            *(lc >= 1 ? bv + pos : tr) = fv;
+            *(lc == 2 ? bv + pos + 1 : tr) = lv;
+            if constexpr (IDX) {
+              *(lc >= 1 ? bi + pos : reinterpret_cast<int*>(tr)) = round_slot_index<W, T, VEC>(round, fs, wid, lane) - st.sh;
+              *(lc == 2 ? bi + pos + 1 : reinterpret_cast<int*>(tr)) =
+                  round_slot_index<W, T, VEC>(round, ls, wid, lane) - st.sh;
+            }
+          };
+          if (st.noidx) pair(std::false_type{});
+          else pair(std::true_type{});
         } else if (st.noidx) {
 #pragma unroll
           for (int i = 0; i < S; ++i) {
@@ -2180,21 +2218,22 @@ __global__ __launch_bounds__(kBlock) void fwl_block_rows(const void* __restrict_
 // the support entries and the label are rewritten.  No block-wide barrier: each wavefront runs
 // its own rows, as in fwl_wave_rows.  A row whose list overflows is solved in memory by its
 // wavefront (select_in_memory with W = 1).
-template <typename T, int MODE, bool V4>
+template <typename T, int MODE, bool V4, bool LONG>
 __global__ __launch_bounds__(kBlock) void fwl_wave_stream_rows(const void* __restrict__ z,
                                                                const int64_t* __restrict__ tgt, int64_t N,
                                                                int C, Outs o) {
-  __shared__ WaveShared s_w[kWavesPerBlock];
+  constexpr int kVCap = LONG ? kStreamVCapLong : kWaveVCap;   // (LONG: the two-pass op's read pass)
+  __shared__ WaveShared<kVCap> s_w[kWavesPerBlock];
   const int lane = lane_id();
   const int wid = uniform((int)(threadIdx.x >> 6));
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
   const int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wid;   // this wavefront's rows: w + k*stride
   const int nrows = w < N ? (int)((N - 1 - w) / stride + 1) : 0;   // <= kRowsPerWave (host grid)
   float* bv = s_w[wid].val;
-  int* bi = reinterpret_cast<int*>(s_w[wid].val + (kWaveVCap - kCapMax));
+  int* bi = reinterpret_cast<int*>(s_w[wid].val + (kVCap - kCapMax));
   const SelMem sm = {nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr};
   // the default capacity takes the whole value list; a smaller one (fwl_options) shrinks both
-  const int vcap = o.cap >= kCapMax ? kWaveVCap : o.cap;
+  const int vcap = o.cap >= kCapMax ? kVCap : o.cap;
   const int icap = o.cap < kCapMax ? o.cap : kCapMax;
   const int64_t my_y = lane < nrows ? tgt[w + (int64_t)lane * stride] : 0;
   float my_H = 0.0f, my_loss = 0.0f;
@@ -3288,11 +3327,11 @@ int launch_block(const void* z, const int64_t* y, int64_t N, int C, const Outs& 
   return grid + launch_overflow<T, MODE, OV4>(z, y, N, C, o, grid, s);
 }
 
-template <typename T, int MODE, bool V4, bool OV4 = V4>
+template <typename T, int MODE, bool V4, bool OV4 = V4, bool LONG = false>
 int launch_wave_stream(const void* z, const int64_t* y, int64_t N, int C, const Outs& o, hipStream_t s) {
-  const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<T, MODE, V4>);
+  const void* k = reinterpret_cast<const void*>(&fwl_wave_stream_rows<T, MODE, V4, LONG>);
   const int grid = wave_grid(N, (int64_t)C * kElemBytes<T>, resident_blocks(k));
-  hipLaunchKernelGGL((fwl_wave_stream_rows<T, MODE, V4>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
+  hipLaunchKernelGGL((fwl_wave_stream_rows<T, MODE, V4, LONG>), dim3(grid), dim3(kBlock), 0, s, z, y, N, C, o);
   return grid + launch_overflow<T, MODE, OV4>(z, y, N, C, o, grid, s);
 }
 
@@ -3329,7 +3368,7 @@ int launch_two_pass(const void* z, const int64_t* y, int64_t N, int C, const Out
   constexpr bool kWin = !V4 && kElemBytes<T> == 2;
   int grid;
   if (N >= kTwoPassWaveRowsPerCU * (int64_t)device_cus())
-    grid = launch_wave_stream<T, kCand, V4 || kWin, V4>(z, y, N, C, o1, s);
+    grid = launch_wave_stream<T, kCand, V4 || kWin, V4, true>(z, y, N, C, o1, s);
   else
     grid = launch_block<T, kCand, V4, true>(z, y, N, C, o1, s);
   const int64_t row_bytes = (int64_t)C * kElemBytes<T>;
