@@ -210,7 +210,6 @@ template <typename T, int MODE, int E, bool V4>
 __device__ __forceinline__ void solve_many(const float* x, float lm, float t0, float m, int lane, float* cl,
                                            int* ci_lds, int& n, double& tau, int& kappa, uint64_t& support) {
   const double tl = select_tier<kWave>(lm, kWave, lane);
-  const float B = fmaxf(fabsf(m), fabsf(t0));
   float t1 = t0;
   if (tl == tl) {
     const float r = rd32(tl - ((double)kWave * (double)(fabsf(m) + 1.0f) + fabs(tl) + 1.0) * 0x1p-51);
@@ -240,13 +239,15 @@ __device__ __forceinline__ void solve_many(const float* x, float lm, float t0, f
     return;
   }
   support = 0;
-  // bound steps with fp32 partial sums
+  // bound steps with fp32 partial sums; the entries summed lie in (t, m], so their magnitudes are
+  // at most max(|t|, |m|), which shrinks the allowance for rounding as t rises (rows of values
+  // near 0 then take the steps until the set stops changing: fewer exact fp64 steps follow)
   float t = t1;
   for (int it = 0; it < kRegSteps; ++it) {
     double s;
     int c;
     reg_sum_count32<E>(x, t, s, c);
-    const float nt = safe_lower32(s, c, B);
+    const float nt = safe_lower32(s, c, fmaxf(fabsf(m), fabsf(t)));
     if (!(nt > t)) break;
     t = nt;
   }
