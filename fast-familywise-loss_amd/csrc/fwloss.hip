@@ -179,6 +179,15 @@ __device__ __forceinline__ void reg_sum_count(const float* x, float thr, double&
   c = wave_sum_i32(cnt);
 }
 
+// the count alone (ballots on the scalar unit)
+template <int E>
+__device__ __forceinline__ int reg_count(const float* x, float thr) {
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < E; ++i) cnt += __popcll(ballot(x[i] > thr));
+  return cnt;
+}
+
 // the same for bounds (see safe_lower32): per-lane fp32 partial sums added by an fp32 tree, the
 // count from ballots (on the scalar unit, beside the tree's chain of dependent steps)
 template <int E>
@@ -260,18 +269,19 @@ __device__ __forceinline__ void solve_many(const float* x, float lm, float t0, f
   kappa = 0;
   for (int it = 0; it < kRegSteps && c > 0; ++it) {
     const double tn = (s - 1.0) / (double)c;
-    double s2;
-    int c2;
-    reg_sum_count<E>(x, rd32(tn), s2, c2);
+    // the set above the new iterate: its count decides, its fp64 sum is needed only for another
+    // step (after bound steps that reached the support, the first step confirms it)
+    const int c2 = reg_count<E>(x, rd32(tn));
     if (c2 == c || !(tn > tt)) {
       tau = tn;
       kappa = c2;
       conv = true;
       break;
     }
+    double s2;
+    reg_sum_count<E>(x, rd32(tn), s2, c);
     tt = tn;
     s = s2;
-    c = c2;
   }
   if (!conv) {
     // G(a) >= 1 > G(b) over keys: tau in [a, b), the support {z > a}
