@@ -3458,11 +3458,14 @@ size_t ovf_ws_bytes(int64_t N) { return ws_round(2 * sizeof(float) * (size_t)(N 
 // With the fill-and-scatter write pass, large fp32 batches of shorter rows gain too (256 MB of
 // logits): 8192 x 8192 102.0 -> 95.6 us, 5592 x 12000 113.5 -> 96.6, 4096 x 16384 106.2 -> 93.5,
 // 2796 x 24000 119.7 -> 106.8; at 128 MB they are even, below it one pass wins (16-64 MB: 18-36 us
-// against 22-43).  bf16: 2048 x 131072 218 -> 190 us, but 8192 x 32000 228 -> 264 us (its read
-// pass is issue-bound at that length).  Automatic dispatch: fp32 rows of >= 32000 elements, >= 384
-// of them, or of >= 8192 elements in batches of >= 48M elements; 16-bit rows of >= 65536
-// elements, >= 512 of them.  Forced paths 2 and 3 always (their tests exercise both passes in
-// every element type).
+// against 22-43).  bf16 (against one row per block): 2048 x 131072 218 -> 190 us; with the
+// read pass's sparse and two-entry rounds, rows of 32000-50000 elements gain once the read pass
+// takes one row per wavefront (8192 x 32000 242 -> 203 us, 4096 x 32000 130 -> 114, 2048 x 40000
+// 88 -> 77, 4096 x 50000 199 -> 155) but not below that (1024 x 32000 46 -> 56).  Automatic
+// dispatch: fp32 rows of >= 32000 elements, >= 384 of them, or of >= 8192 elements in batches of
+// >= 48M elements; 16-bit rows of >= 65536 elements, >= 512 of them, or of >= 32000 elements,
+// kTwoPassWaveRowsPerCU of them per CU.  Forced paths 2 and 3 always (their tests exercise both
+// passes in every element type).
 constexpr int64_t kTwoPassMinC = 32000;
 constexpr int64_t kTwoPassMinRows = 384;
 constexpr int64_t kTwoPassMinCBig = 8192;
@@ -3474,14 +3477,18 @@ bool two_pass_rows(int64_t N, int64_t C, int64_t elem, int path) {
   if (path != 0) return false;
   if (elem == 4)
     return (C >= kTwoPassMinC && N >= kTwoPassMinRows) || (C >= kTwoPassMinCBig && N * C >= kTwoPassMinElemsBig);
-  return C >= kTwoPassMinC16 && N >= kTwoPassMinRows16;
+  return (C >= kTwoPassMinC16 && N >= kTwoPassMinRows16) ||
+         (C >= kTwoPassMinC && N >= kTwoPassWaveRowsPerCU * (int64_t)device_cus());
 }
 
-// 16-bit rows a little beyond kMaxStreamC stream faster on one wavefront each than on one block
-// each once there are enough rows (bf16, one wavefront per row against one block per row):
-// 5592 x 12000 65.7 us against 98.1, 4096 x 16384 61.7 against 79.7, 1198 x 28000 43.1 against
-// 50.3; below about 1024 rows, or at 32000 elements, one block per row wins.
-constexpr int kMaxStreamC16 = 28672;
+// 16-bit rows beyond kMaxStreamC stream faster on one wavefront each than on one block each once
+// there are enough rows (bf16, one wavefront per row against one block per row): 5592 x 12000
+// 65.7 us against 98.1, 4096 x 16384 61.7 against 79.7, 1198 x 28000 43.1 against 50.3, 1024 x
+// 32000 40.9 against 46.4, 1024 x 50000 55.7 against 62.5; below about 1024 rows one block per
+// row wins (512 x 32000: 38.7 against 31.9).  From 65536 elements the two passes take them.
+// Rows without 128-bit units (16-bit loads) stream up to the length measured before.
+constexpr int kMaxStreamC16 = 65535;
+constexpr int kMaxStreamC16V1 = 28672;
 constexpr int64_t kStreamMinRows16 = 1024;
 
 // the two passes' scratch: cut candidate lists (values, indices), kappa and H per row
@@ -3602,7 +3609,8 @@ int forward(const void* z, int64_t ld, const int64_t* y, int64_t N, int64_t C64,
   if (path == 0 && !aligned_rows && C <= 128) path = 6;   // short unaligned rows: 32-bit segments
   if (path == 0) {
     const bool two_pass = two_pass_ok && (two_pass_rows(N, C, kElemBytes<T>, 0) || win16);
-    const bool stream = C <= kMaxStreamC || (kElemBytes<T> == 2 && C <= kMaxStreamC16 && N >= kStreamMinRows16);
+    const bool stream = C <= kMaxStreamC ||
+                        (kElemBytes<T> == 2 && C <= (v4 ? kMaxStreamC16 : kMaxStreamC16V1) && N >= kStreamMinRows16);
     path = C <= max_wave_c ? 6 : (two_pass ? 2 : (stream ? 4 : 2));
   }
   if ((path == 1 || path == 6) && C > max_wave_c) path = 4;
