@@ -3457,19 +3457,20 @@ size_t ovf_ws_bytes(int64_t N) { return ws_round(2 * sizeof(float) * (size_t)(N 
 // 357 us, 520 x 128256 132 -> 118 us, 400 x 50257 50.5 -> 46.8 us; but 256 x 128256 67 -> 79 us.
 // With the fill-and-scatter write pass, large fp32 batches of shorter rows gain too (256 MB of
 // logits): 8192 x 8192 102.0 -> 95.6 us, 5592 x 12000 113.5 -> 96.6, 4096 x 16384 106.2 -> 93.5,
-// 2796 x 24000 119.7 -> 106.8; at 128 MB they are even, below it one pass wins (16-64 MB: 18-36 us
-// against 22-43).  bf16 (against one row per block): 2048 x 131072 218 -> 190 us; with the
+// 2796 x 24000 119.7 -> 106.8; with the current read pass also from 128 MB (4096 x 10000 78.4 ->
+// 69.8 us, 2560 x 16384 80.2 -> 75.2, 1700 x 24000 79.7 -> 74.4, 2048 x 16384 63.2 -> 59.9;
+// 3000 x 10000 even), below it one pass wins (16-64 MB: 18-36 us against 22-43).  bf16 (against one row per block): 2048 x 131072 218 -> 190 us; with the
 // read pass's sparse and two-entry rounds, rows of 32000-50000 elements gain once the read pass
 // takes one row per wavefront (8192 x 32000 242 -> 203 us, 4096 x 32000 130 -> 114, 2048 x 40000
 // 88 -> 77, 4096 x 50000 199 -> 155) but not below that (1024 x 32000 46 -> 56).  Automatic
 // dispatch: fp32 rows of >= 32000 elements, >= 384 of them, or of >= 8192 elements in batches of
-// >= 48M elements; 16-bit rows of >= 65536 elements, >= 512 of them, or of >= 32000 elements,
+// >= 32M elements; 16-bit rows of >= 65536 elements, >= 512 of them, or of >= 32000 elements,
 // kTwoPassWaveRowsPerCU of them per CU.  Forced paths 2 and 3 always (their tests exercise both
 // passes in every element type).
 constexpr int64_t kTwoPassMinC = 32000;
 constexpr int64_t kTwoPassMinRows = 384;
 constexpr int64_t kTwoPassMinCBig = 8192;
-constexpr int64_t kTwoPassMinElemsBig = (int64_t)48 << 20;
+constexpr int64_t kTwoPassMinElemsBig = (int64_t)32 << 20;
 constexpr int64_t kTwoPassMinC16 = 65536;
 constexpr int64_t kTwoPassMinRows16 = 512;
 bool two_pass_rows(int64_t N, int64_t C, int64_t elem, int path) {
