@@ -375,18 +375,19 @@ def main():
 
     # the (dominant) kernel the automatic dispatch runs for this shape (16-byte aligned rows)
     unit = 16 // ELEM_BYTES[args.dtype]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
     if args.dtype == "f64":
         tag = "fwl_rows_f64"
     elif N <= 128 and C * ELEM_BYTES[args.dtype] >= 96 * 1024:
         tag = "fwl_split_chunks"
-    elif (args.dtype == "f32" and ((N >= 384 and C >= 32000) or (C >= 8192 and N * C >= 48 << 20))) or \
-            (args.dtype != "f32" and N >= 512 and C >= 65536):
+    elif (args.dtype == "f32" and ((N >= 384 and C >= 32000) or (C >= 8192 and N * C >= 32 << 20))) or \
+            (args.dtype != "f32" and ((N >= 512 and C >= 65536) or (N >= 8 * cus and C >= 32000))):
         tag = "fwl_two_pass"      # the candidate-list read pass + fwl_fill_zero + fwl_scatter_support
     elif (C % unit == 0 and C // unit <= 64) or (C % unit != 0 and C <= 128):
         tag = "fwl_seg_rows"
     elif C <= 2048:
         tag = "fwl_wave_rows"
-    elif C <= 8192 or (args.dtype != "f32" and C <= 28672 and N >= 1024):
+    elif C <= 8192 or (args.dtype != "f32" and C <= (65535 if C % unit == 0 else 28672) and N >= 1024):
         tag = "fwl_wave_stream_rows"
     else:
         tag = "fwl_block_rows"

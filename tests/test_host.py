@@ -225,7 +225,7 @@ def test_workspace_sizes():
     """The split-row scratch is counted exactly where the split kernels may run: few rows (<= 128)
     of at least 96 KiB (24576 fp32 elements; the size covers every element type), or rows of any
     length when path 7 is forced; the two-pass scratch where the fused op may run in two passes
-    (>= 384 rows of >= 32000 elements, rows of >= 8192 elements in batches of >= 48M elements, or
+    (>= 384 rows of >= 32000 elements, rows of >= 8192 elements in batches of >= 32M elements, or
     path 2/3 forced).  The two share one region (the larger is counted)."""
     L = capi.lib()
     p, c = ctypes.c_int(-1), ctypes.c_int(-1)
@@ -237,15 +237,16 @@ def test_workspace_sizes():
         assert W(16, 1000) == ws_expect(16)           # short rows: no scratch
         assert W(65536, 8191) == ws_expect(65536)
         assert W(0, 131072) == ws_expect(0)
-        # >= 384 rows of >= 32000 elements, or batches of >= 48M elements in rows of >= 8192 (the
-        # fp32 rules, which cover the 16-bit one) run the fused op in two passes: per row 512
+        # >= 384 rows of >= 32000 elements, or batches of >= 32M elements in rows of >= 8192 (the
+        # fp32 rules, which cover the 16-bit ones) run the fused op in two passes: per row 512
         # support indices, the read pass's count and H
         row = 512 * 4 + 4 + 4
         assert W(2048, 131072) == ws_expect(2048, 2048 * row)
         assert W(384, 32000) == ws_expect(384, 384 * row)
         assert W(383, 32000) == ws_expect(383)
-        assert W(6144, 8192) == ws_expect(6144, 6144 * row)      # 48M elements
-        assert W(6143, 8192) == ws_expect(6143)
+        assert W(4096, 8192) == ws_expect(4096, 4096 * row)      # 32M elements
+        assert W(4095, 8192) == ws_expect(4095)
+        assert W(6144, 8191) == ws_expect(6144)
         assert W(65536, 8192) == ws_expect(65536, 65536 * row)
         assert W(1024, 31999) == ws_expect(1024)
         assert W(129, 24576) == ws_expect(129)
