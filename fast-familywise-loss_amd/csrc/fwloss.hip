@@ -2892,6 +2892,7 @@ constexpr int kTwoPassCap = kCapMax;     // support indices kept per row between
 __device__ __forceinline__ bool two_pass_listed(int k) { return k > 0 && k <= kTwoPassCap; }
 __device__ __forceinline__ int two_pass_kappa(int k) { return k < 0 ? -k : k; }
 constexpr int kTwoPassWaveRowsPerCU = 8;    // rows per CU from which the read pass takes a wavefront per row
+constexpr int64_t kTwoPassMinCWin16 = 12000;   // 16-bit rows without 128-bit units: two passes from this length
 constexpr int kFillBytes = 4096;         // bytes per block of the fill
 
 // kap (optional): per row the read pass's count; rows whose support is not listed are left alone
@@ -3509,7 +3510,11 @@ size_t workspace_bytes(int64_t N, int64_t C, int path) {
   // the two passes' scratch
   size_t extra = 0;
   if (split_rows(N, C, 4, path)) extra = split_scratch_bytes(N, C);
-  if (two_pass_rows(N, C, 4, path) && two_pass_bytes(N) > extra) extra = two_pass_bytes(N);
+  // (16-bit rows without 128-bit units take two passes from kTwoPassMinCWin16 elements at
+  // kTwoPassWaveRowsPerCU rows per CU; without a device, per 256 CUs)
+  const int cus = device_cus();
+  const bool win16 = C >= kTwoPassMinCWin16 && N >= kTwoPassWaveRowsPerCU * (int64_t)(cus > 0 ? cus : 256);
+  if ((two_pass_rows(N, C, 4, path) || (path == 0 && win16)) && two_pass_bytes(N) > extra) extra = two_pass_bytes(N);
   return mean_ws_bytes(N) + ovf_ws_bytes(N) + extra;
 }
 
@@ -3604,8 +3609,10 @@ int forward(const void* z, int64_t ld, const int64_t* y, int64_t N, int64_t C64,
   // 16-bit rows without 128-bit units (odd lengths or strides), long and many: the two-pass op,
   // whose read pass takes them through windows with 128-bit loads (bf16 2048 x 50257: 188 -> 100 us,
   // 8192 x 32001: 414 -> 238; the same at N(0, 0.01^2); fewer rows read one block per row, which
-  // lost at N(0, 0.01^2): 512 x 50257 140 against 70)
-  const bool win16 = kElemBytes<T> == 2 && !v4 && C >= kTwoPassMinC &&
+  // lost at N(0, 0.01^2): 512 x 50257 140 against 70).  From kTwoPassMinCWin16 elements against
+  // the one-pass stream with 16-bit loads: 2048 x 12001 47.3 -> 41.1 us, 4095 x 16385 83.1 -> 72.8,
+  // 2048 x 24001 69.9 -> 55.1, 8191 x 12001 115.3 -> 112.3; at 8193 elements it is even or loses.
+  const bool win16 = kElemBytes<T> == 2 && !v4 && C >= kTwoPassMinCWin16 &&
                      N >= kTwoPassWaveRowsPerCU * (int64_t)device_cus();
   if (path == 0 && !aligned_rows && C <= 128) path = 6;   // short unaligned rows: 32-bit segments
   if (path == 0) {

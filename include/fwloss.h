@@ -75,8 +75,8 @@ const char* fwl_status_string(int status);
 /* Bytes of device workspace the forward entry points need for an [N, C] problem: one fp64 per
  * block of the largest grid (>= 4096 blocks), rounded up to 256 bytes, then the larger of: 528
  * bytes per (row, chunk) for at most 128 rows of >= 24576 elements (the split rows), and 2056
- * bytes per row for >= 384 rows of >= 32000 elements or for batches of >= 32M elements in rows of
- * >= 8192 (the fused op in two passes).  The answer follows the current fwl_set_params switches
+ * bytes per row for >= 384 rows of >= 32000 elements, for batches of >= 32M elements in rows of
+ * >= 8192, or for 8 rows per CU of >= 12000 elements (the fused op in two passes).  The answer follows the current fwl_set_params switches
  * (forcing path 7 needs the chunk scratch, forcing path 2 or 3 the two-pass scratch, for rows of
  * any length).  A smaller workspace is accepted: the mean needs only its first part, and without
  * room for the rest the one-pass kernels run. */

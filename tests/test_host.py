@@ -247,6 +247,12 @@ def test_workspace_sizes():
         assert W(4096, 8192) == ws_expect(4096, 4096 * row)      # 32M elements
         assert W(4095, 8192) == ws_expect(4095)
         assert W(6144, 8191) == ws_expect(6144)
+        # 16-bit rows without 128-bit units take two passes from 12000 elements at 8 rows per CU
+        # (the count follows the device's CUs: 256 on MI355X, and 256 without a device)
+        cus = 256
+        assert W(8 * cus, 12000) == ws_expect(8 * cus, 8 * cus * row)
+        assert W(8 * cus - 1, 12000) == ws_expect(8 * cus - 1)
+        assert W(8 * cus, 11999) == ws_expect(8 * cus)
         assert W(65536, 8192) == ws_expect(65536, 65536 * row)
         assert W(1024, 31999) == ws_expect(1024)
         assert W(129, 24576) == ws_expect(129)
