@@ -381,7 +381,7 @@ def main():
     elif N <= 128 and C * ELEM_BYTES[args.dtype] >= 96 * 1024:
         tag = "fwl_split_chunks"
     elif (args.dtype == "f32" and ((N >= 384 and C >= 32000) or (C >= 8192 and N * C >= 32 << 20))) or \
-            (args.dtype != "f32" and ((N >= 512 and C >= 65536) or (N >= 8 * cus and C >= 32000) or
+            (args.dtype != "f32" and ((N >= 512 and C >= 65536) or (N >= 8 * cus and C >= 32000) or (N >= 16 * cus and C >= 28000) or
                                       (N >= 8 * cus and C >= 12000 and C % 2 == 1))):
         tag = "fwl_two_pass"      # the candidate-list read pass + fwl_fill_zero + fwl_scatter_support
     elif (C % unit == 0 and C // unit <= 64) or (C % unit != 0 and C <= 128):

@@ -3474,13 +3474,18 @@ constexpr int64_t kTwoPassMinCBig = 8192;
 constexpr int64_t kTwoPassMinElemsBig = (int64_t)32 << 20;
 constexpr int64_t kTwoPassMinC16 = 65536;
 constexpr int64_t kTwoPassMinRows16 = 512;
+// 16-bit rows of 28000-31999 elements, at twice kTwoPassWaveRowsPerCU rows per CU: 8192 x 28000
+// 193.1 -> 183.8 us, 8192 x 30000 211.7 -> 192.7, 4096 x 28000 even; 24000 elements lose
+// (4096 x 24000 90.8 -> 97.0, 8192 x 24000 165.5 -> 170.6)
+constexpr int64_t kTwoPassMinC16Many = 28000;
 bool two_pass_rows(int64_t N, int64_t C, int64_t elem, int path) {
   if (path == 2 || path == 3) return true;
   if (path != 0) return false;
   if (elem == 4)
     return (C >= kTwoPassMinC && N >= kTwoPassMinRows) || (C >= kTwoPassMinCBig && N * C >= kTwoPassMinElemsBig);
-  return (C >= kTwoPassMinC16 && N >= kTwoPassMinRows16) ||
-         (C >= kTwoPassMinC && N >= kTwoPassWaveRowsPerCU * (int64_t)device_cus());
+  const int64_t w = kTwoPassWaveRowsPerCU * (int64_t)device_cus();
+  return (C >= kTwoPassMinC16 && N >= kTwoPassMinRows16) || (C >= kTwoPassMinC && N >= w) ||
+         (C >= kTwoPassMinC16Many && N >= 2 * w);
 }
 
 // 16-bit rows beyond kMaxStreamC stream faster on one wavefront each than on one block each once
